@@ -1,0 +1,112 @@
+// Shared helpers for the HIP/CDNA4 (gfx950) recurrent-step library.
+//
+// Status codes returned by every extern "C" entry point (never exceptions
+// across the ABI): 0 ok, negative = error class; hk_last_error() holds text.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#define HK_OK 0
+#define HK_ERR_ARG (-1)       // bad shape / pointer / size (the reference asserts)
+#define HK_ERR_HIP (-2)       // a HIP runtime call failed
+#define HK_ERR_CAPACITY (-3)  // more rows / runs than the engine was sized for
+#define HK_ERR_STATE (-4)     // engine used before weights were bound, etc.
+
+namespace hk {
+
+void set_error(const char* fmt, ...);
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// softplus with torch's default beta=1, threshold=20: x above the threshold
+// is returned unchanged, otherwise log1p(exp(x)).
+__device__ __forceinline__ float softplus(float x) {
+  return x > 20.0f ? x : log1pf(expf(x));
+}
+
+// log(sigmoid(x)) in the overflow-free form min(x, 0) - log1p(exp(-|x|)).
+__device__ __forceinline__ float logsigmoid(float x) {
+  return fminf(x, 0.0f) - log1pf(expf(-fabsf(x)));
+}
+
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (no NaN inputs on this path, but a
+// NaN stays a NaN: the quiet bit is forced).
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+__host__ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+__host__ __device__ __forceinline__ float round_bf16(float f) {
+  return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+// Wave-wide sum with DPP-free shuffles (xor butterfly over 64 lanes).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` must hold
+// blockDim.x / 64 floats of LDS. Every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+}  // namespace hk
+
+#define HK_CHECK_HIP(expr)                                                        \
+  do {                                                                            \
+    hipError_t e_ = (expr);                                                       \
+    if (e_ != hipSuccess) {                                                       \
+      hk::set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, \
+                    __LINE__);                                                    \
+      return HK_ERR_HIP;                                                          \
+    }                                                                             \
+  } while (0)
+
+#define HK_REQUIRE(cond, ...)     \
+  do {                            \
+    if (!(cond)) {                \
+      hk::set_error(__VA_ARGS__); \
+      return HK_ERR_ARG;          \
+    }                             \
+  } while (0)
+
+#define HK_LAUNCH_CHECK()                                                              \
+  do {                                                                                 \
+    hipError_t e_ = hipGetLastError();                                                 \
+    if (e_ != hipSuccess) {                                                            \
+      hk::set_error("kernel launch failed: %s (%s:%d)", hipGetErrorString(e_), __FILE__, \
+                    __LINE__);                                                         \
+      return HK_ERR_HIP;                                                               \
+    }                                                                                  \
+  } while (0)

@@ -1,0 +1,44 @@
+// Matrix-state scan: the one recurrence shared by the three large per-symbol
+// states (xLSTM mLSTM cell, RetNet retention state, Mamba2 SSM state).
+//
+// For every step t of a symbol's run, with S a rows x cols fp32 tile per head:
+//   S[r][c]  <- alpha_t * S[r][c] + (scale_t * beta_t[r]) * gamma_t[c]
+//   out_t[c]  = sum_r w_t[r] * S_new[r][c]
+// mLSTM  (model/kernels.py:143-151): alpha=f, scale=i, beta=k, gamma=v, w=q
+// RetNet (model/kernels.py:154-160): alpha=decay[head], scale=1, beta=k_rope,
+//                                    gamma=v, w=q_scaled
+// Mamba2 (model/kernels.py:163-171): alpha=decay, scale=dt, beta=b, gamma=x,
+//                                    w=c (rows = the contracted bc axis)
+#pragma once
+
+#include "common.h"
+
+namespace hk {
+
+struct Operand {
+  const float* ptr = nullptr;  // nullptr => the value 1.0 (scale only)
+  int64_t row_stride = 0;      // elements between request rows
+  int64_t head_stride = 0;     // elements between heads
+};
+
+struct MatScanDesc {
+  float* state = nullptr;
+  int64_t slot_stride = 0, head_stride = 0, row_stride = 0, col_stride = 1;
+  int rows = 0, cols = 0, heads = 0;
+  // Run descriptors: run i advances slot slot_ids[i] over request rows
+  // run_off[i] .. run_off[i+1]-1, in order. With `per_row` set instead, run i
+  // is request row i of slot i and advances iff mask is null or mask[i] != 0
+  // (the reference kernel API, model/kernels.py:28-34).
+  const int* slot_ids = nullptr;
+  const int* run_off = nullptr;
+  bool per_row = false;
+  const uint8_t* mask = nullptr;
+  int n_runs = 0;
+  Operand alpha, scale, beta, gamma, w;
+  float* out = nullptr;
+  int64_t out_row_stride = 0, out_head_stride = 0;
+};
+
+int launch_mat_scan(const MatScanDesc& d, hipStream_t stream);
+
+}  // namespace hk

@@ -1,0 +1,119 @@
+"""Fused recurrent state steps on gfx950, behind the reference's kernel API.
+
+Drop-in for `model/kernels.py:346-401` (`mlstm_step`, `retnet_step`,
+`mamba2_step`) with the same contract (`model/kernels.py:28-34`):
+
+- the state is updated IN PLACE; rows whose mask is False end bit-identical,
+  rows whose mask is True hold the new value;
+- the returned output is a fresh contiguous fp32 tensor, zero on idle rows;
+- `mask=None` means every row is active;
+- nothing is data-dependent on the host.
+
+Argument checks follow `model/kernels.py:85-121`: wrong dtype, shape, device
+or a non-contiguous state raise AssertionError and are never repaired. Unlike
+the reference there is no torch fallback: the state must live on a GPU and
+the HIP library must be present, or the call raises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _state_ok(state: torch.Tensor, name: str) -> None:
+    # model/kernels.py:116-121
+    assert state.dtype == torch.float32, f"{name} must be fp32, got {state.dtype}"
+    assert state.is_contiguous(), f"{name} must be contiguous, it is written in place"
+    assert state.dim() == 4, f"{name} must be 4-D, got {tuple(state.shape)}"
+    if state.device.type != "cuda":
+        raise _lib.HipLibraryError(f"{name} is on {state.device}; the HIP kernels need a GPU tensor")
+
+
+def _small(t: torch.Tensor, shape: tuple, name: str, device) -> torch.Tensor:
+    # model/kernels.py:85-98
+    assert t.dtype == torch.float32, f"{name} must be fp32, got {t.dtype}"
+    assert tuple(t.shape) == shape, f"{name} must be {shape}, got {tuple(t.shape)}"
+    assert t.device == device, f"{name} must be on {device}, it is on {t.device}"
+    return t.contiguous()
+
+
+def _mask_u8(mask, batch: int, device):
+    # model/kernels.py:101-113; None stays None (every row active).
+    if mask is None:
+        return None
+    assert mask.dtype == torch.bool, f"mask must be bool, got {mask.dtype}"
+    assert mask.shape == (batch,), f"mask must be ({batch},), got {tuple(mask.shape)}"
+    assert mask.device == device, f"mask must be on {device}, it is on {mask.device}"
+    return mask.contiguous().view(torch.uint8)
+
+
+def mlstm_step(cell, q, k, v, i_gate, f_gate, mask):
+    """cell <- f*cell + (i*k) outer v on active rows; returns sum_h q*cell_new.
+
+    Reference: model/kernels.py:346-360 (Triton) and :143-151 (torch twin).
+    """
+    _state_ok(cell, "cell")
+    batch, heads, size_h, size_k = (int(s) for s in cell.shape)
+    dev = cell.device
+    q = _small(q, (batch, heads, size_h), "q", dev)
+    k = _small(k, (batch, heads, size_h), "k", dev)
+    v = _small(v, (batch, heads, size_k), "v", dev)
+    i_gate = _small(i_gate, (batch, heads), "i_gate", dev)
+    f_gate = _small(f_gate, (batch, heads), "f_gate", dev)
+    m = _mask_u8(mask, batch, dev)
+    out = torch.empty((batch, heads, size_k), dtype=torch.float32, device=dev)
+    st = _lib.lib().hk_mlstm_step(
+        cell.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), i_gate.data_ptr(),
+        f_gate.data_ptr(), _lib.ptr(m), out.data_ptr(), batch, heads, size_h, size_k,
+        _lib.current_stream(dev),
+    )
+    _lib.check(st, "hk_mlstm_step")
+    return out
+
+
+def retnet_step(state, k_rope, v, q_scaled, decay, mask):
+    """state <- decay[head]*state + k_rope outer v; returns sum_h q_scaled*state_new.
+
+    Reference: model/kernels.py:363-376 (Triton) and :154-160 (torch twin).
+    """
+    _state_ok(state, "recurrent_state")
+    batch, heads, size_h, size_k = (int(s) for s in state.shape)
+    dev = state.device
+    k_rope = _small(k_rope, (batch, heads, size_h), "k_rope", dev)
+    v = _small(v, (batch, heads, size_k), "v", dev)
+    q_scaled = _small(q_scaled, (batch, heads, size_h), "q_scaled", dev)
+    decay = _small(decay, (heads,), "decay", dev)
+    m = _mask_u8(mask, batch, dev)
+    out = torch.empty((batch, heads, size_k), dtype=torch.float32, device=dev)
+    st = _lib.lib().hk_retnet_step(
+        state.data_ptr(), k_rope.data_ptr(), v.data_ptr(), q_scaled.data_ptr(), decay.data_ptr(),
+        _lib.ptr(m), out.data_ptr(), batch, heads, size_h, size_k, _lib.current_stream(dev),
+    )
+    _lib.check(st, "hk_retnet_step")
+    return out
+
+
+def mamba2_step(ssm, x, b, c, dt, decay, mask):
+    """ssm <- decay*ssm + (dt*b) outer x on active rows; returns sum_c c*ssm_new.
+
+    Reference: model/kernels.py:379-401 (Triton) and :163-171 (torch twin).
+    """
+    _state_ok(ssm, "ssm_state")
+    batch, heads, size_h, size_c = (int(s) for s in ssm.shape)
+    dev = ssm.device
+    x = _small(x, (batch, heads, size_h), "x", dev)
+    b = _small(b, (batch, size_c), "b", dev)
+    c = _small(c, (batch, size_c), "c", dev)
+    dt = _small(dt, (batch, heads), "dt", dev)
+    decay = _small(decay, (batch, heads), "decay", dev)
+    m = _mask_u8(mask, batch, dev)
+    y = torch.empty((batch, heads, size_h), dtype=torch.float32, device=dev)
+    st = _lib.lib().hk_mamba2_step(
+        ssm.data_ptr(), x.data_ptr(), b.data_ptr(), c.data_ptr(), dt.data_ptr(),
+        decay.data_ptr(), _lib.ptr(m), y.data_ptr(), batch, heads, size_h, size_c,
+        _lib.current_stream(dev),
+    )
+    _lib.check(st, "hk_mamba2_step")
+    return y
