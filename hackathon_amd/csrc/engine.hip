@@ -1,0 +1,918 @@
+// The ensemble engine: packed weights, a slot-indexed recurrent state store
+// resident in HBM, and the layer-major tick.
+//
+// A tick receives a batch of requests grouped into runs, one run per symbol
+// (its slot) holding that symbol's requests in arrival order, runs sorted by
+// non-increasing length. Every layer processes all requests of the tick at
+// once: projections are GEMMs over every request row, and each recurrent
+// layer scans each run in order while holding the symbol's state tile on
+// chip, so a symbol's state crosses HBM twice per tick however many requests
+// it has. The maths is exactly the reference's round-by-round evaluation
+// (example_model.py:885-899): rows never mix (example_model.py:422-427) and
+// each symbol's requests are applied in list order.
+//
+// Per request, per tower (model/inference_model.py:85-95, :55-68):
+//   x = input_down(relu(input_up(features)))
+//   12 x { x += layer(RMSNorm(x)); x += fc2(relu(fc1(RMSNorm(x)))) }
+//   pred[tower] = output_proj(x)                          (shared weights)
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "gemm.h"
+#include "ops.h"
+#include "scan_mat.h"
+
+namespace hk {
+namespace {
+
+enum TowerType { kXLSTM = 0, kMamba2 = 1, kRetNet = 2, kHawk = 3 };
+constexpr int kTowers = 4;
+
+// ---- weight slots ----------------------------------------------------------
+// Block-level slots common to every tower type.
+enum { B_NORM1, B_NORM2, B_FC1_W, B_FC1_B, B_FC2_W, B_FC2_B, B_LAYER0 };
+enum {  // xLSTM layer
+  X_S_NORM = B_LAYER0, X_S_CONV_W, X_S_CONV_B, X_S_IN_W, X_S_ST_W, X_S_ST_B, X_S_GN_W, X_S_GN_B,
+  X_L_NORM, X_L_XG_W, X_L_QKV_W, X_L_CONV_W, X_L_CONV_B, X_L_IF_W, X_L_IF_B, X_L_GN_W, X_L_GN_B,
+  X_L_DOWN_W, X_L_SKIP, X_F_NORM, X_NSLOTS
+};
+enum {  // Mamba2 layer
+  M_PROJ_W = B_LAYER0, M_DT_W, M_DT_B, M_CONV_W, M_CONV_B, M_A, M_D, M_NORM, M_OUT_W, M_NSLOTS
+};
+enum { R_QKVG_W = B_LAYER0, R_OUT_W, R_DECAY, R_ANGLE, R_NSLOTS };  // RetNet layer
+enum { K_PROJ_W = B_LAYER0, K_CONV_W, K_CONV_B, K_GATES_W, K_A, K_OUT_W, K_NSLOTS };  // Hawk
+enum { T_UP_W, T_UP_B, T_DOWN_W, T_DOWN_B, T_NSLOTS };  // tower level (layer = -1)
+enum { G_OUT_W, G_OUT_B, G_NSLOTS };                     // global (tower = -1)
+
+// State leaves, in the reference's init_state order per block.
+enum { XS_S_CONV, XS_S_H, XS_S_C, XS_S_N, XS_S_M, XS_L_CONV, XS_L_C, XS_L_N, XS_L_M, XS_N };
+enum { MS_CONV, MS_SSM, MS_N };
+enum { RS_OFF, RS_SCALE, RS_S, RS_N };
+enum { KS_CONV, KS_H, KS_N };
+
+struct SlotDef {
+  const char* name;
+  int64_t numel;
+  bool lp;          // a CastLinear weight: bf16 storage in reduced-precision mode
+  bool lp_bias;     // a CastLinear bias: rounded to bf16 in reduced-precision mode
+};
+
+struct Slot {
+  SlotDef def{};
+  void* ptr = nullptr;   // device storage (bf16 when def.lp && lowp, else fp32)
+  bool bound = false;
+};
+
+struct Dims {
+  int H, P, D, nh, F, Fpad;
+  int nh_s, bs_s;        // sLSTM heads / head size
+  int I, hs_m;           // mLSTM inner / head size
+  int Im, hm, bc, nhm;   // Mamba2 inner / head / bc / heads
+  int hs_r;              // RetNet head size
+  int nb_h, bs_h;        // Hawk RG-LRU blocks
+};
+
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+std::vector<SlotDef> block_slots(const Dims& d, int tower) {
+  std::vector<SlotDef> v = {
+      {"norm1.weight", d.H, false, false},
+      {"norm2.weight", d.H, false, false},
+      {"mlp.fc1.weight", (int64_t)d.P * d.H, true, false},
+      {"mlp.fc1.bias", d.P, false, true},
+      {"mlp.fc2.weight", (int64_t)d.H * d.P, true, false},
+      {"mlp.fc2.bias", d.H, false, true},
+  };
+  switch (tower) {
+    case kXLSTM: {
+      const int64_t I = d.I;
+      v.push_back({"slstm.norm.weight", d.H, false, false});
+      v.push_back({"slstm.conv (4 taps x H)", 4LL * d.H, false, false});
+      v.push_back({"slstm.conv1d.conv.bias", d.H, false, false});
+      v.push_back({"slstm.{i,f,z,o}gate_input.weight", 4LL * d.H * d.bs_s, false, false});
+      v.push_back({"slstm.{i,f,z,o}gate_state.weight", 4LL * d.H * d.bs_s, false, false});
+      v.push_back({"slstm.{i,f,z,o}gate_state.bias", 4LL * d.H, false, false});
+      v.push_back({"slstm.group_norm.weight", d.H, false, false});
+      v.push_back({"slstm.group_norm.bias", d.H, false, false});
+      v.push_back({"mlstm.norm.weight", d.H, false, false});
+      v.push_back({"mlstm.{x_proj,gate_proj}.weight", 2 * I * d.H, true, false});
+      v.push_back({"mlstm.{q,k,v}_proj.weight", 3 * I * 4, false, false});
+      v.push_back({"mlstm.conv (4 taps x I)", 4 * I, false, false});
+      v.push_back({"mlstm.conv1d.conv.bias", I, false, false});
+      v.push_back({"mlstm.mlstm_cell.{igate,fgate}_proj.weight", 2LL * d.nh * 3 * I, false, false});
+      v.push_back({"mlstm.mlstm_cell.{igate,fgate}_proj.bias", 2LL * d.nh, false, false});
+      v.push_back({"mlstm.mlstm_cell.outnorm.weight", I, false, false});
+      v.push_back({"mlstm.mlstm_cell.outnorm.bias", I, false, false});
+      v.push_back({"mlstm.proj_down.weight", (int64_t)d.H * I, true, false});
+      v.push_back({"mlstm.learnable_skip", I, false, false});
+      v.push_back({"final_norm.weight", d.H, false, false});
+      break;
+    }
+    case kMamba2: {
+      const int64_t C = d.Im + 2LL * d.bc;
+      v.push_back({"{input,b,c,z}_proj.weight", (C + d.Im) * d.H, true, false});
+      v.push_back({"dt_proj.weight", (int64_t)d.nhm * d.H, false, false});
+      v.push_back({"dt_proj.bias", d.nhm, false, false});
+      v.push_back({"{input,b,c}_conv (4 taps x C)", 4 * C, false, false});
+      v.push_back({"{input,b,c}_conv.conv.bias", C, false, false});
+      v.push_back({"a", d.nhm, false, false});
+      v.push_back({"d", d.nhm, false, false});
+      v.push_back({"norm.weight", d.Im, false, false});
+      v.push_back({"out_proj.weight", (int64_t)d.H * d.Im, true, false});
+      break;
+    }
+    case kRetNet: {
+      v.push_back({"{q,k,v,g}_proj.weight", 4LL * d.H * d.H, true, false});
+      v.push_back({"out_proj.weight", (int64_t)d.H * d.H, true, false});
+      v.push_back({"decay", d.nh, false, false});
+      v.push_back({"angle", d.hs_r, false, false});
+      break;
+    }
+    case kHawk: {
+      v.push_back({"{gate,recurrent}_proj.weight", 2LL * d.H * d.H, true, false});
+      v.push_back({"conv (4 taps x H)", 4LL * d.H, false, false});
+      v.push_back({"conv.conv.bias", d.H, false, false});
+      v.push_back({"rglru.{input,recurrence}_gate.weight", 2LL * d.H * d.bs_h, false, false});
+      v.push_back({"rglru.a", d.H, false, false});
+      v.push_back({"out_proj.weight", (int64_t)d.H * d.H, true, false});
+      break;
+    }
+  }
+  return v;
+}
+
+std::vector<SlotDef> tower_slots(const Dims& d) {
+  return {{"input_up.weight (K padded)", (int64_t)d.P * d.Fpad, true, false},
+          {"input_up.bias", d.P, false, true},
+          {"input_down.weight", (int64_t)d.H * d.P, true, false},
+          {"input_down.bias", d.H, false, true}};
+}
+
+std::vector<SlotDef> global_slots(const Dims& d) {
+  return {{"output_proj.weight", d.H, false, false}, {"output_proj.bias", 1, false, false}};
+}
+
+std::vector<int64_t> state_leaves(const Dims& d, int tower) {
+  switch (tower) {
+    case kXLSTM:
+      return {3LL * d.H, d.H, d.H, d.H, d.H, 3LL * d.I, (int64_t)d.nh * d.hs_m * d.hs_m,
+              (int64_t)d.nh * d.hs_m, d.nh};
+    case kMamba2:
+      return {3LL * (d.Im + 2 * d.bc), (int64_t)d.nhm * d.bc * d.hm};
+    case kRetNet:
+      return {1, d.nh, (int64_t)d.nh * d.hs_r * d.hs_r};
+    default:
+      return {3LL * d.H, d.H};
+  }
+}
+
+// ---- device buffers ----------------------------------------------------------
+
+struct DevBuf {
+  void* p = nullptr;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+};
+
+struct Act {  // an activation: fp32 copy and (reduced-precision mode) bf16 copy
+  float* f = nullptr;
+  uint16_t* l = nullptr;
+};
+
+struct TowerWS {
+  Act X, A, H1;
+  // xLSTM
+  float *XN = nullptr, *XCA = nullptr, *GIN = nullptr, *SY = nullptr, *X1 = nullptr,
+        *XMG = nullptr, *XMC = nullptr, *QKV = nullptr, *KS = nullptr, *IF = nullptr,
+        *IG = nullptr, *FG = nullptr, *DEN = nullptr, *NUM = nullptr, *X2 = nullptr;
+  Act XN2, HS;
+  // Mamba2
+  float *PROJ = nullptr, *DTR = nullptr, *DTS = nullptr, *DEC = nullptr, *MXC = nullptr,
+        *YS = nullptr;
+  Act YN;
+  // RetNet
+  float *QKVG = nullptr, *KR = nullptr, *QS = nullptr, *O = nullptr;
+  Act YO;
+  // Hawk
+  float *GRP = nullptr, *KXC = nullptr, *GATES = nullptr;
+  Act GH;
+  GemmWorkspace gemm_ws;
+};
+
+}  // namespace
+
+struct Engine {
+  Dims d{};
+  int capacity = 0, max_rows = 0, max_runs = 0;
+  bool lowp = false;
+  std::vector<std::unique_ptr<DevBuf>> bufs;
+  // slots[tower][layer+1][slot]; layer index 0 holds the tower-level slots.
+  std::vector<std::vector<std::vector<Slot>>> slots;
+  std::vector<Slot> gslots;
+  // state[tower][layer][leaf] -> device base, per-slot elements
+  std::vector<std::vector<std::vector<float*>>> state;
+  std::vector<std::vector<int64_t>> leaf_elems;
+  TowerWS ws[kTowers];
+  Act FE;
+  int* d_slots = nullptr;
+  int* d_off = nullptr;
+  int* h_stage = nullptr;  // pinned [2][max_runs * 2 + 1]
+  hipEvent_t stage_done[2] = {nullptr, nullptr};
+  int stage_idx = 0;
+  std::vector<char> seen;
+
+  ~Engine() {
+    for (auto& e : stage_done)
+      if (e) (void)hipEventDestroy(e);
+    if (h_stage) (void)hipHostFree(h_stage);
+  }
+
+  void* alloc_bytes(size_t bytes) {
+    auto b = std::make_unique<DevBuf>();
+    if (hipMalloc(&b->p, std::max<size_t>(bytes, 256)) != hipSuccess) {
+      b->p = nullptr;
+      return nullptr;
+    }
+    void* p = b->p;
+    bufs.push_back(std::move(b));
+    return p;
+  }
+  float* alloc_f(int64_t n) { return static_cast<float*>(alloc_bytes((size_t)n * 4)); }
+  uint16_t* alloc_l(int64_t n) { return static_cast<uint16_t*>(alloc_bytes((size_t)n * 2)); }
+  Act alloc_act(int64_t n, bool need_f32) {
+    Act a;
+    if (need_f32 || !lowp) a.f = alloc_f(n);
+    if (lowp) a.l = alloc_l(n);
+    return a;
+  }
+};
+
+namespace {
+
+bool any_null(const Act& a, bool need_f32, bool lowp) {
+  return ((need_f32 || !lowp) && !a.f) || (lowp && !a.l);
+}
+
+int build_workspace(Engine& e) {
+  const Dims& d = e.d;
+  const int64_t R = e.max_rows;
+  for (int t = 0; t < kTowers; ++t) {
+    TowerWS& w = e.ws[t];
+    w.X.f = e.alloc_f(R * d.H);
+    w.A = e.alloc_act(R * d.H, true);
+    w.H1 = e.alloc_act(R * d.P, false);
+    if (!w.X.f || any_null(w.A, true, e.lowp) || any_null(w.H1, false, e.lowp)) return HK_ERR_HIP;
+    int64_t max_n = std::max<int64_t>(d.P, d.H);
+    switch (t) {
+      case kXLSTM:
+        w.XN = e.alloc_f(R * d.H);
+        w.XCA = e.alloc_f(R * d.H);
+        w.GIN = e.alloc_f(R * 4 * d.H);
+        w.SY = e.alloc_f(R * d.H);
+        w.X1 = e.alloc_f(R * d.H);
+        w.XN2 = e.alloc_act(R * d.H, false);
+        w.XMG = e.alloc_f(R * 2 * d.I);
+        w.XMC = e.alloc_f(R * d.I);
+        w.QKV = e.alloc_f(R * 3 * d.I);
+        w.KS = e.alloc_f(R * d.I);
+        w.IF = e.alloc_f(R * 2 * d.nh);
+        w.IG = e.alloc_f(R * d.nh);
+        w.FG = e.alloc_f(R * d.nh);
+        w.DEN = e.alloc_f(R * d.nh);
+        w.NUM = e.alloc_f(R * d.I);
+        w.HS = e.alloc_act(R * d.I, false);
+        w.X2 = e.alloc_f(R * d.H);
+        if (!w.XN || !w.XCA || !w.GIN || !w.SY || !w.X1 || any_null(w.XN2, false, e.lowp) ||
+            !w.XMG || !w.XMC || !w.QKV || !w.KS || !w.IF || !w.IG || !w.FG || !w.DEN || !w.NUM ||
+            any_null(w.HS, false, e.lowp) || !w.X2)
+          return HK_ERR_HIP;
+        max_n = std::max<int64_t>(max_n, 2 * d.I);
+        break;
+      case kMamba2: {
+        const int64_t C = d.Im + 2LL * d.bc;
+        w.PROJ = e.alloc_f(R * (C + d.Im));
+        w.DTR = e.alloc_f(R * d.nhm);
+        w.DTS = e.alloc_f(R * d.nhm);
+        w.DEC = e.alloc_f(R * d.nhm);
+        w.MXC = e.alloc_f(R * C);
+        w.YS = e.alloc_f(R * d.Im);
+        w.YN = e.alloc_act(R * d.Im, false);
+        if (!w.PROJ || !w.DTR || !w.DTS || !w.DEC || !w.MXC || !w.YS ||
+            any_null(w.YN, false, e.lowp))
+          return HK_ERR_HIP;
+        max_n = std::max<int64_t>(max_n, C + d.Im);
+        break;
+      }
+      case kRetNet:
+        w.QKVG = e.alloc_f(R * 4 * d.H);
+        w.KR = e.alloc_f(R * d.H);
+        w.QS = e.alloc_f(R * d.H);
+        w.O = e.alloc_f(R * d.H);
+        w.YO = e.alloc_act(R * d.H, false);
+        if (!w.QKVG || !w.KR || !w.QS || !w.O || any_null(w.YO, false, e.lowp)) return HK_ERR_HIP;
+        max_n = std::max<int64_t>(max_n, 4 * d.H);
+        break;
+      case kHawk:
+        w.GRP = e.alloc_f(R * 2 * d.H);
+        w.KXC = e.alloc_f(R * d.H);
+        w.GATES = e.alloc_f(R * 2 * d.H);
+        w.GH = e.alloc_act(R * d.H, false);
+        if (!w.GRP || !w.KXC || !w.GATES || any_null(w.GH, false, e.lowp)) return HK_ERR_HIP;
+        max_n = std::max<int64_t>(max_n, 2 * d.H);
+        break;
+    }
+    // Split-K partial sums: up to 8 splits of the widest projection.
+    w.gemm_ws.partial_elems = std::min<int64_t>(8 * R * max_n, 1LL << 26);
+    w.gemm_ws.partial = e.alloc_f(w.gemm_ws.partial_elems);
+    if (!w.gemm_ws.partial) return HK_ERR_HIP;
+  }
+  e.FE = e.alloc_act(R * d.Fpad, false);
+  if (any_null(e.FE, false, e.lowp)) return HK_ERR_HIP;
+  e.d_slots = static_cast<int*>(e.alloc_bytes((size_t)e.max_runs * 4));
+  e.d_off = static_cast<int*>(e.alloc_bytes((size_t)(e.max_runs + 1) * 4));
+  if (!e.d_slots || !e.d_off) return HK_ERR_HIP;
+  HK_CHECK_HIP(hipHostMalloc((void**)&e.h_stage, (size_t)2 * (2 * e.max_runs + 1) * 4,
+                             hipHostMallocDefault));
+  for (auto& ev : e.stage_done) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  return HK_OK;
+}
+
+// ---- one linear layer --------------------------------------------------------
+
+struct Lin {
+  const Slot* w;
+  const Slot* b;  // may be null
+};
+
+// y = x . W^T (+ b); CastLinear semantics when W is a reduced-precision slot.
+int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int M, int N, int K,
+           int act, const float* residual, int64_t ldr, float* out, int64_t ldo, uint16_t* out_lp,
+           int64_t ldl, hipStream_t s) {
+  GemmArgs g;
+  const bool lp = lin.w->def.lp && e.lowp;
+  g.type = lp ? GemmType::kBF16 : GemmType::kF32;
+  g.A = lp ? (const void*)x.l : (const void*)x.f;
+  HK_REQUIRE(g.A != nullptr, "linear %s: missing %s input", lin.w->def.name, lp ? "bf16" : "fp32");
+  g.lda = ldx;
+  g.W = lin.w->ptr;
+  g.ldw = K;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.ep.bias = lin.b ? static_cast<const float*>(lin.b->ptr) : nullptr;
+  g.ep.round_lp = lp;
+  g.ep.act = act;
+  g.ep.residual = residual;
+  g.ep.ldr = ldr;
+  g.ep.out = out;
+  g.ep.ldo = ldo;
+  g.ep.out_lp = out_lp;
+  g.ep.ldl = ldl;
+  return gemm(g, w.gemm_ws, s);
+}
+
+// Block-diagonal fp32 product (BlockLinear, model/modules.py:71-79):
+// out[:, b*bs + k] = sum_h x[:, b*bs + h] * W[b][k][h], for b < blocks.
+int block_linear(TowerWS& w, const float* x, int64_t ldx, const float* W, int blocks, int bs,
+                 int M, const float* bias, float* out, int64_t ldo, hipStream_t s) {
+  GemmArgs g;
+  g.type = GemmType::kF32;
+  g.A = x;
+  g.lda = ldx;
+  g.W = W;
+  g.ldw = bs;
+  g.M = M;
+  g.N = bs;
+  g.K = bs;
+  g.batch = blocks;
+  g.a_bstride = bs;
+  g.w_bstride = (int64_t)bs * bs;
+  g.c_bstride = bs;
+  g.ep.bias = bias;
+  g.ep.out = out;
+  g.ep.ldo = ldo;
+  return gemm(g, w.gemm_ws, s);
+}
+
+#define HK_TRY(expr)          \
+  do {                        \
+    int st_ = (expr);         \
+    if (st_ != HK_OK) return st_; \
+  } while (0)
+
+const Slot* S(Engine& e, int t, int l, int i) { return &e.slots[t][l + 1][i]; }
+const float* F32(Engine& e, int t, int l, int i) {
+  return static_cast<const float*>(e.slots[t][l + 1][i].ptr);
+}
+
+int run_xlstm(Engine& e, int l, const Runs& r, const std::vector<int>& act, hipStream_t s) {
+  const Dims& d = e.d;
+  TowerWS& w = e.ws[kXLSTM];
+  const int n = r.n_rows;
+  const int H = d.H, I = d.I;
+  float** st = e.state[kXLSTM][l].data();
+  const int64_t* le = e.leaf_elems[kXLSTM].data();
+  // sLSTM block (model/xlstm.py:400-424); its input and skip is A = norm1(x).
+  HK_TRY(layernorm_rows(w.A.f, F32(e, kXLSTM, l, X_S_NORM), nullptr, n, H, w.XN, nullptr, s));
+  HK_TRY(conv_scan(r, w.XN, H, H, st[XS_S_CONV], le[XS_S_CONV], F32(e, kXLSTM, l, X_S_CONV_W),
+                   F32(e, kXLSTM, l, X_S_CONV_B), 1, w.XCA, H, s));
+  const float* win = F32(e, kXLSTM, l, X_S_IN_W);
+  for (int g = 0; g < 4; ++g) {  // i, f from the conv path; z, o from LN(x)
+    const float* src = g < 2 ? w.XCA : w.XN;
+    HK_TRY(block_linear(w, src, H, win + (int64_t)g * H * d.bs_s, d.nh_s, d.bs_s, n, nullptr,
+                        w.GIN + (int64_t)g * H, 4 * H, s));
+  }
+  for (size_t t = 0; t < act.size(); ++t) {
+    HK_TRY(slstm_round(r, (int)t, act[t], w.GIN, H, d.nh_s, F32(e, kXLSTM, l, X_S_ST_W),
+                       F32(e, kXLSTM, l, X_S_ST_B), st[XS_S_H], st[XS_S_C], st[XS_S_N],
+                       st[XS_S_M], w.SY, s));
+  }
+  HK_TRY(slstm_final(r, w.SY, H, st[XS_S_H], s));
+  HK_TRY(slstm_post(w.SY, w.A.f, F32(e, kXLSTM, l, X_S_GN_W), F32(e, kXLSTM, l, X_S_GN_B), d.nh_s,
+                    F32(e, kXLSTM, l, X_L_NORM), n, H, w.X1, w.XN2.f, w.XN2.l, s));
+  // mLSTM block (model/xlstm.py:298-325).
+  HK_TRY(linear(e, w, w.XN2, H, {S(e, kXLSTM, l, X_L_XG_W), nullptr}, n, 2 * I, H, 0, nullptr, 0,
+                w.XMG, 2 * I, nullptr, 0, s));
+  HK_TRY(conv_scan(r, w.XMG, 2 * I, I, st[XS_L_CONV], le[XS_L_CONV], F32(e, kXLSTM, l, X_L_CONV_W),
+                   F32(e, kXLSTM, l, X_L_CONV_B), 1, w.XMC, I, s));
+  const float* wqkv = F32(e, kXLSTM, l, X_L_QKV_W);
+  HK_TRY(mlstm_qkv(w.XMC, w.XMG, 2 * I, wqkv, wqkv + (int64_t)I * 4, wqkv + (int64_t)2 * I * 4, n,
+                   I, 4, (float)std::sqrt((double)d.hs_m), w.QKV, w.KS, s));
+  HK_TRY(linear(e, w, Act{w.QKV, nullptr}, 3 * I,
+                {S(e, kXLSTM, l, X_L_IF_W), S(e, kXLSTM, l, X_L_IF_B)}, n, 2 * d.nh, 3 * I, 0,
+                nullptr, 0, w.IF, 2 * d.nh, nullptr, 0, s));
+  HK_TRY(mlstm_gates(r, w.IF, d.nh, w.QKV, I, w.KS, st[XS_L_N], st[XS_L_M], w.IG, w.FG, w.DEN, s));
+  MatScanDesc m;
+  m.state = st[XS_L_C];
+  m.rows = d.hs_m;
+  m.cols = d.hs_m;
+  m.heads = d.nh;
+  m.row_stride = d.hs_m;
+  m.col_stride = 1;
+  m.head_stride = (int64_t)d.hs_m * d.hs_m;
+  m.slot_stride = le[XS_L_C];
+  m.slot_ids = r.slot_ids;
+  m.run_off = r.run_off;
+  m.n_runs = r.n_runs;
+  m.alpha = {w.FG, d.nh, 1};
+  m.scale = {w.IG, d.nh, 1};
+  m.beta = {w.KS, I, d.hs_m};
+  m.gamma = {w.QKV + 2 * I, 3 * I, d.hs_m};
+  m.w = {w.QKV, 3 * I, d.hs_m};
+  m.out = w.NUM;
+  m.out_row_stride = I;
+  m.out_head_stride = d.hs_m;
+  HK_TRY(launch_mat_scan(m, s));
+  HK_TRY(mlstm_post(w.NUM, w.DEN, d.nh, F32(e, kXLSTM, l, X_L_GN_W), F32(e, kXLSTM, l, X_L_GN_B),
+                    F32(e, kXLSTM, l, X_L_SKIP), w.XMC, w.XMG + I, 2 * I, n, I, d.nh, w.HS.f,
+                    w.HS.l, s));
+  HK_TRY(linear(e, w, w.HS, I, {S(e, kXLSTM, l, X_L_DOWN_W), nullptr}, n, H, I, 0, w.X1, H, w.X2,
+                H, nullptr, 0, s));
+  // final_norm, then the Block's residual: x = final_norm(x2) + x.
+  HK_TRY(layernorm_rows(w.X2, F32(e, kXLSTM, l, X_F_NORM), w.X.f, n, H, w.X.f, nullptr, s));
+  return HK_OK;
+}
+
+int run_mamba2(Engine& e, int l, const Runs& r, hipStream_t s) {
+  const Dims& d = e.d;
+  TowerWS& w = e.ws[kMamba2];
+  const int n = r.n_rows;
+  const int H = d.H, I = d.Im;
+  const int C = I + 2 * d.bc;
+  const int W = C + I;
+  float** st = e.state[kMamba2][l].data();
+  const int64_t* le = e.leaf_elems[kMamba2].data();
+  // model/mamba2.py:77-97
+  HK_TRY(linear(e, w, w.A, H, {S(e, kMamba2, l, M_PROJ_W), nullptr}, n, W, H, 0, nullptr, 0,
+                w.PROJ, W, nullptr, 0, s));
+  HK_TRY(linear(e, w, Act{w.A.f, nullptr}, H, {S(e, kMamba2, l, M_DT_W), S(e, kMamba2, l, M_DT_B)},
+                n, d.nhm, H, 0, nullptr, 0, w.DTR, d.nhm, nullptr, 0, s));
+  HK_TRY(mamba2_dt(w.DTR, F32(e, kMamba2, l, M_A), n, d.nhm, w.DTS, w.DEC, s));
+  HK_TRY(conv_scan(r, w.PROJ, W, C, st[MS_CONV], le[MS_CONV], F32(e, kMamba2, l, M_CONV_W),
+                   F32(e, kMamba2, l, M_CONV_B), 1, w.MXC, C, s));
+  // SSM state stored [head][c][h]: tile rows are the contracted bc axis.
+  MatScanDesc m;
+  m.state = st[MS_SSM];
+  m.rows = d.bc;
+  m.cols = d.hm;
+  m.heads = d.nhm;
+  m.row_stride = d.hm;
+  m.col_stride = 1;
+  m.head_stride = (int64_t)d.bc * d.hm;
+  m.slot_stride = le[MS_SSM];
+  m.slot_ids = r.slot_ids;
+  m.run_off = r.run_off;
+  m.n_runs = r.n_runs;
+  m.alpha = {w.DEC, d.nhm, 1};
+  m.scale = {w.DTS, d.nhm, 1};
+  m.beta = {w.MXC + I, C, 0};
+  m.gamma = {w.MXC, C, d.hm};
+  m.w = {w.MXC + I + d.bc, C, 0};
+  m.out = w.YS;
+  m.out_row_stride = I;
+  m.out_head_stride = d.hm;
+  HK_TRY(launch_mat_scan(m, s));
+  HK_TRY(mamba2_post(w.YS, w.MXC, C, w.PROJ + C, W, F32(e, kMamba2, l, M_D),
+                     F32(e, kMamba2, l, M_NORM), n, I, d.hm, w.YN.f, w.YN.l, s));
+  HK_TRY(linear(e, w, w.YN, I, {S(e, kMamba2, l, M_OUT_W), nullptr}, n, H, I, 0, w.X.f, H, w.X.f,
+                H, nullptr, 0, s));
+  return HK_OK;
+}
+
+int run_retnet(Engine& e, int l, const Runs& r, hipStream_t s) {
+  const Dims& d = e.d;
+  TowerWS& w = e.ws[kRetNet];
+  const int n = r.n_rows;
+  const int H = d.H;
+  float** st = e.state[kRetNet][l].data();
+  const int64_t* le = e.leaf_elems[kRetNet].data();
+  // model/retnet.py:234-269
+  HK_TRY(linear(e, w, w.A, H, {S(e, kRetNet, l, R_QKVG_W), nullptr}, n, 4 * H, H, 0, nullptr, 0,
+                w.QKVG, 4 * H, nullptr, 0, s));
+  const float scaling = (float)std::pow((double)d.hs_r, -0.5);
+  HK_TRY(retnet_prep(r, w.QKVG, 4 * H, H, d.nh, scaling, F32(e, kRetNet, l, R_ANGLE),
+                     F32(e, kRetNet, l, R_DECAY), reinterpret_cast<int*>(st[RS_OFF]),
+                     st[RS_SCALE], w.KR, w.QS, s));
+  MatScanDesc m;
+  m.state = st[RS_S];
+  m.rows = d.hs_r;
+  m.cols = d.hs_r;
+  m.heads = d.nh;
+  m.row_stride = d.hs_r;
+  m.col_stride = 1;
+  m.head_stride = (int64_t)d.hs_r * d.hs_r;
+  m.slot_stride = le[RS_S];
+  m.slot_ids = r.slot_ids;
+  m.run_off = r.run_off;
+  m.n_runs = r.n_runs;
+  m.alpha = {F32(e, kRetNet, l, R_DECAY), 0, 1};
+  m.beta = {w.KR, H, d.hs_r};
+  m.gamma = {w.QKVG + 2 * H, 4 * H, d.hs_r};
+  m.w = {w.QS, H, d.hs_r};
+  m.out = w.O;
+  m.out_row_stride = H;
+  m.out_head_stride = d.hs_r;
+  HK_TRY(launch_mat_scan(m, s));
+  HK_TRY(retnet_post(w.O, w.QKVG + 3 * H, 4 * H, n, H, d.hs_r, w.YO.f, w.YO.l, s));
+  HK_TRY(linear(e, w, w.YO, H, {S(e, kRetNet, l, R_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f,
+                H, nullptr, 0, s));
+  return HK_OK;
+}
+
+int run_hawk(Engine& e, int l, const Runs& r, hipStream_t s) {
+  const Dims& d = e.d;
+  TowerWS& w = e.ws[kHawk];
+  const int n = r.n_rows;
+  const int H = d.H;
+  float** st = e.state[kHawk][l].data();
+  const int64_t* le = e.leaf_elems[kHawk].data();
+  // model/hawk.py:77-84; GRP = [gate | recurrent]
+  HK_TRY(linear(e, w, w.A, H, {S(e, kHawk, l, K_PROJ_W), nullptr}, n, 2 * H, H, 0, nullptr, 0,
+                w.GRP, 2 * H, nullptr, 0, s));
+  HK_TRY(conv_scan(r, w.GRP + H, 2 * H, H, st[KS_CONV], le[KS_CONV], F32(e, kHawk, l, K_CONV_W),
+                   F32(e, kHawk, l, K_CONV_B), 0, w.KXC, H, s));
+  const float* gw = F32(e, kHawk, l, K_GATES_W);
+  for (int g = 0; g < 2; ++g)
+    HK_TRY(block_linear(w, w.KXC, H, gw + (int64_t)g * H * d.bs_h, d.nb_h, d.bs_h, n, nullptr,
+                        w.GATES + (int64_t)g * H, 2 * H, s));
+  HK_TRY(rglru_scan(r, w.KXC, w.GATES, w.GATES + H, 2 * H, w.GRP, 2 * H, F32(e, kHawk, l, K_A),
+                    8.0f, H, st[KS_H], w.GH.f, w.GH.l, s));
+  HK_TRY(linear(e, w, w.GH, H, {S(e, kHawk, l, K_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f, H,
+                nullptr, 0, s));
+  return HK_OK;
+}
+
+int run_tower(Engine& e, int t, const Runs& r, const std::vector<int>& act, float* preds,
+              hipStream_t s) {
+  const Dims& d = e.d;
+  TowerWS& w = e.ws[t];
+  const int n = r.n_rows;
+  const int H = d.H, P = d.P;
+  // input_up -> relu -> input_down (model/inference_model.py:88-90)
+  HK_TRY(linear(e, w, e.FE, d.Fpad, {S(e, t, -1, T_UP_W), S(e, t, -1, T_UP_B)}, n, P, d.Fpad, 1,
+                nullptr, 0, w.H1.f, P, w.H1.l, P, s));
+  HK_TRY(linear(e, w, w.H1, P, {S(e, t, -1, T_DOWN_W), S(e, t, -1, T_DOWN_B)}, n, H, P, 0, nullptr,
+                0, w.X.f, H, nullptr, 0, s));
+  for (int l = 0; l < d.D; ++l) {
+    // Block (model/inference_model.py:63-68)
+    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM1), 1.1920928955078125e-07f, n, H, w.A.f, H,
+                        w.A.l, H, s));
+    switch (t) {
+      case kXLSTM: HK_TRY(run_xlstm(e, l, r, act, s)); break;
+      case kMamba2: HK_TRY(run_mamba2(e, l, r, s)); break;
+      case kRetNet: HK_TRY(run_retnet(e, l, r, s)); break;
+      default: HK_TRY(run_hawk(e, l, r, s)); break;
+    }
+    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM2), 1.1920928955078125e-07f, n, H, w.A.f, H,
+                        w.A.l, H, s));
+    HK_TRY(linear(e, w, w.A, H, {S(e, t, l, B_FC1_W), S(e, t, l, B_FC1_B)}, n, P, H, 1, nullptr, 0,
+                  w.H1.f, P, w.H1.l, P, s));
+    HK_TRY(linear(e, w, w.H1, P, {S(e, t, l, B_FC2_W), S(e, t, l, B_FC2_B)}, n, H, P, 0, w.X.f, H,
+                  w.X.f, H, nullptr, 0, s));
+  }
+  HK_TRY(output_proj(w.X.f, static_cast<const float*>(e.gslots[G_OUT_W].ptr),
+                     static_cast<const float*>(e.gslots[G_OUT_B].ptr), n, H, preds, kTowers, t,
+                     s));
+  return HK_OK;
+}
+
+Slot* find_slot(Engine& e, int tower, int layer, int slot) {
+  if (tower == -1) {
+    if (layer != -1 || slot < 0 || slot >= (int)e.gslots.size()) return nullptr;
+    return &e.gslots[slot];
+  }
+  if (tower < 0 || tower >= kTowers || layer < -1 || layer >= e.d.D) return nullptr;
+  auto& v = e.slots[tower][layer + 1];
+  if (slot < 0 || slot >= (int)v.size()) return nullptr;
+  return &v[slot];
+}
+
+}  // namespace
+}  // namespace hk
+
+using hk::Engine;
+
+extern "C" {
+
+// cfg: hidden, proj, depth, heads, features, mamba_head, mamba_bc, capacity,
+//      max_rows, max_runs, lowp
+int hk_engine_create(const int* cfg, int n_cfg, void** out) {
+  HK_REQUIRE(cfg && out && n_cfg == 11, "hk_engine_create: expected 11 config ints");
+  *out = nullptr;
+  auto e = std::make_unique<Engine>();
+  hk::Dims& d = e->d;
+  d.H = cfg[0];
+  d.P = cfg[1];
+  d.D = cfg[2];
+  d.nh = cfg[3];
+  d.F = cfg[4];
+  d.hm = cfg[5];
+  d.bc = cfg[6];
+  e->capacity = cfg[7];
+  e->max_rows = cfg[8];
+  e->max_runs = cfg[9];
+  e->lowp = cfg[10] != 0;
+  HK_REQUIRE(d.H > 0 && d.P > 0 && d.D > 0 && d.nh > 0 && d.F > 0 && d.hm > 0 && d.bc > 0,
+             "hk_engine_create: non-positive dimension");
+  HK_REQUIRE(e->capacity > 0 && e->max_rows > 0 && e->max_runs > 0,
+             "hk_engine_create: capacity, max_rows and max_runs must be positive");
+  d.Fpad = (int)hk::round_up(d.F, 64);
+  d.nh_s = d.nh / 2;
+  HK_REQUIRE(d.nh_s >= 1 && d.H % d.nh_s == 0, "sLSTM heads (heads/2) must divide hidden");
+  d.bs_s = d.H / d.nh_s;
+  d.I = 2 * d.H;
+  HK_REQUIRE(d.I % d.nh == 0, "heads must divide 2*hidden");
+  d.hs_m = d.I / d.nh;
+  d.Im = 2 * d.H;
+  HK_REQUIRE(d.Im % d.hm == 0, "mamba head size must divide 2*hidden");
+  d.nhm = d.Im / d.hm;
+  HK_REQUIRE(d.H % d.nh == 0 && (d.H / d.nh) % 2 == 0, "heads must divide hidden evenly");
+  d.hs_r = d.H / d.nh;
+  d.nb_h = 4;
+  HK_REQUIRE(d.H % 4 == 0, "hidden must be a multiple of 4");
+  d.bs_h = d.H / 4;
+  HK_REQUIRE(d.bs_s % 16 == 0 && d.bs_h % 16 == 0 && d.H % 16 == 0,
+             "block sizes must be multiples of 16 (fp32 MFMA K tile)");
+  HK_REQUIRE(d.hs_m <= 512 && d.hs_r <= 512 && d.bc <= 512 && d.nh <= 16 && d.nh_s <= 16,
+             "head sizes above 512 or more than 16 heads are not supported");
+  HK_REQUIRE(d.bs_s <= 1008, "sLSTM head size too large for LDS staging");
+
+  // weights
+  e->slots.resize(hk::kTowers);
+  for (int t = 0; t < hk::kTowers; ++t) {
+    e->slots[t].resize(d.D + 1);
+    for (auto& def : hk::tower_slots(d)) e->slots[t][0].push_back(hk::Slot{def});
+    for (int l = 0; l < d.D; ++l)
+      for (auto& def : hk::block_slots(d, t)) e->slots[t][l + 1].push_back(hk::Slot{def});
+  }
+  for (auto& def : hk::global_slots(d)) e->gslots.push_back(hk::Slot{def});
+  auto alloc_slot = [&](hk::Slot& s) -> bool {
+    const size_t bytes = (size_t)s.def.numel * ((s.def.lp && e->lowp) ? 2 : 4);
+    s.ptr = e->alloc_bytes(bytes);
+    return s.ptr != nullptr;
+  };
+  for (auto& tv : e->slots)
+    for (auto& lv : tv)
+      for (auto& s : lv)
+        if (!alloc_slot(s)) {
+          hk::set_error("hk_engine_create: out of device memory for weights");
+          return HK_ERR_HIP;
+        }
+  for (auto& s : e->gslots)
+    if (!alloc_slot(s)) {
+      hk::set_error("hk_engine_create: out of device memory for weights");
+      return HK_ERR_HIP;
+    }
+
+  // state store
+  e->state.resize(hk::kTowers);
+  e->leaf_elems.resize(hk::kTowers);
+  for (int t = 0; t < hk::kTowers; ++t) {
+    e->leaf_elems[t] = hk::state_leaves(d, t);
+    e->state[t].resize(d.D);
+    for (int l = 0; l < d.D; ++l) {
+      for (int64_t per : e->leaf_elems[t]) {
+        float* p = e->alloc_f(per * e->capacity);
+        if (!p) {
+          hk::set_error("hk_engine_create: out of device memory for the state store "
+                        "(%d slots)", e->capacity);
+          return HK_ERR_HIP;
+        }
+        e->state[t][l].push_back(p);
+      }
+    }
+  }
+  int st = hk::build_workspace(*e);
+  if (st != HK_OK) {
+    hk::set_error("hk_engine_create: out of device memory for the workspace (%d rows)",
+                  e->max_rows);
+    return st;
+  }
+  e->seen.assign(e->capacity, 0);
+  *out = e.release();
+  return HK_OK;
+}
+
+int hk_engine_destroy(void* h) {
+  if (!h) return HK_OK;
+  (void)hipDeviceSynchronize();
+  delete static_cast<Engine*>(h);
+  return HK_OK;
+}
+
+int hk_engine_param_numel(void* h, int tower, int layer, int slot, int64_t* numel) {
+  HK_REQUIRE(h && numel, "hk_engine_param_numel: null argument");
+  hk::Slot* s = hk::find_slot(*static_cast<Engine*>(h), tower, layer, slot);
+  HK_REQUIRE(s, "hk_engine_param_numel: no slot (%d, %d, %d)", tower, layer, slot);
+  *numel = s->def.numel;
+  return HK_OK;
+}
+
+// Synchronous: copies `numel` fp32 values from host memory into the slot,
+// converting to bf16 (weights) or rounding through bf16 (biases) when the
+// slot is a reduced-precision linear and the engine runs in that mode.
+int hk_engine_load_param(void* h, int tower, int layer, int slot, const float* host,
+                         int64_t numel) {
+  HK_REQUIRE(h && host, "hk_engine_load_param: null argument");
+  Engine& e = *static_cast<Engine*>(h);
+  hk::Slot* s = hk::find_slot(e, tower, layer, slot);
+  HK_REQUIRE(s, "hk_engine_load_param: no slot (%d, %d, %d)", tower, layer, slot);
+  HK_REQUIRE(numel == s->def.numel, "hk_engine_load_param: %s expects %lld values, got %lld",
+             s->def.name, (long long)s->def.numel, (long long)numel);
+  if (s->def.lp && e.lowp) {
+    float* tmp = nullptr;
+    HK_CHECK_HIP(hipMalloc(&tmp, (size_t)numel * 4));
+    hipError_t err = hipMemcpy(tmp, host, (size_t)numel * 4, hipMemcpyHostToDevice);
+    int st = err == hipSuccess ? hk::to_bf16(tmp, static_cast<uint16_t*>(s->ptr), numel, nullptr)
+                               : HK_ERR_HIP;
+    if (st == HK_OK) err = hipDeviceSynchronize();
+    (void)hipFree(tmp);
+    if (err != hipSuccess) {
+      hk::set_error("hk_engine_load_param: %s", hipGetErrorString(err));
+      return HK_ERR_HIP;
+    }
+    if (st != HK_OK) return st;
+  } else if (s->def.lp_bias && e.lowp) {
+    std::vector<float> v(host, host + numel);
+    for (auto& x : v) x = hk::round_bf16(x);
+    HK_CHECK_HIP(hipMemcpy(s->ptr, v.data(), (size_t)numel * 4, hipMemcpyHostToDevice));
+  } else {
+    HK_CHECK_HIP(hipMemcpy(s->ptr, host, (size_t)numel * 4, hipMemcpyHostToDevice));
+  }
+  s->bound = true;
+  return HK_OK;
+}
+
+int hk_engine_state_numel(void* h, int tower, int leaf, int64_t* per_slot) {
+  HK_REQUIRE(h && per_slot, "hk_engine_state_numel: null argument");
+  Engine& e = *static_cast<Engine*>(h);
+  HK_REQUIRE(tower >= 0 && tower < hk::kTowers, "bad tower %d", tower);
+  HK_REQUIRE(leaf >= 0 && leaf < (int)e.leaf_elems[tower].size(), "bad leaf %d", leaf);
+  *per_slot = e.leaf_elems[tower][leaf];
+  return HK_OK;
+}
+
+// Copies leaf `leaf` of slots [slot0, slot0+nslots) between the store and a
+// device buffer (to_engine != 0: buffer -> store). Stream-ordered.
+int hk_engine_state_copy(void* h, int tower, int layer, int leaf, int slot0, int nslots,
+                         void* buf, int to_engine, void* stream) {
+  HK_REQUIRE(h && buf, "hk_engine_state_copy: null argument");
+  Engine& e = *static_cast<Engine*>(h);
+  HK_REQUIRE(tower >= 0 && tower < hk::kTowers && layer >= 0 && layer < e.d.D,
+             "hk_engine_state_copy: bad tower/layer");
+  HK_REQUIRE(leaf >= 0 && leaf < (int)e.leaf_elems[tower].size(), "bad leaf %d", leaf);
+  HK_REQUIRE(slot0 >= 0 && nslots >= 0 && slot0 + nslots <= e.capacity,
+             "hk_engine_state_copy: slots out of range");
+  const int64_t per = e.leaf_elems[tower][leaf];
+  float* base = e.state[tower][layer][leaf] + (int64_t)slot0 * per;
+  const size_t bytes = (size_t)nslots * per * 4;
+  if (to_engine)
+    HK_CHECK_HIP(hipMemcpyAsync(base, buf, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  else
+    HK_CHECK_HIP(hipMemcpyAsync(buf, base, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  return HK_OK;
+}
+
+// Resets slots to the reference's init_state values (zeros; the sLSTM
+// running max starts at -inf, model/xlstm.py:375). n < 0 resets every slot.
+int hk_engine_reset_slots(void* h, const int* slots_host, int n, void* stream) {
+  HK_REQUIRE(h, "hk_engine_reset_slots: null handle");
+  Engine& e = *static_cast<Engine*>(h);
+  hipStream_t s = (hipStream_t)stream;
+  for (int t = 0; t < hk::kTowers; ++t) {
+    for (int l = 0; l < e.d.D; ++l) {
+      for (size_t leaf = 0; leaf < e.leaf_elems[t].size(); ++leaf) {
+        const float v = (t == hk::kXLSTM && leaf == hk::XS_S_M) ? -INFINITY : 0.0f;
+        const int64_t per = e.leaf_elems[t][leaf];
+        float* base = e.state[t][l][leaf];
+        if (n < 0) {
+          HK_TRY(hk::fill_f32(base, per * e.capacity, v, s));
+        } else {
+          for (int i = 0; i < n; ++i) {
+            const int slot = slots_host[i];
+            HK_REQUIRE(slot >= 0 && slot < e.capacity, "reset: slot %d out of range", slot);
+            HK_TRY(hk::fill_f32(base + (int64_t)slot * per, per, v, s));
+          }
+        }
+      }
+    }
+  }
+  return HK_OK;
+}
+
+// One tick. slot_ids_host[n_runs] and run_off_host[n_runs+1] describe runs
+// sorted by non-increasing length; features_dev is [n_rows, features] fp32
+// and preds_dev receives [n_rows, 4] (one column per tower), in row order.
+int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, int n_runs,
+                   const float* features_dev, float* preds_dev, void* stream) {
+  HK_REQUIRE(h, "hk_engine_tick: null handle");
+  Engine& e = *static_cast<Engine*>(h);
+  hipStream_t s = (hipStream_t)stream;
+  if (n_runs == 0) return HK_OK;
+  HK_REQUIRE(slot_ids_host && run_off_host && features_dev && preds_dev,
+             "hk_engine_tick: null argument");
+  if (n_runs < 0 || n_runs > e.max_runs) {
+    hk::set_error("hk_engine_tick: %d runs exceeds max_runs %d", n_runs, e.max_runs);
+    return HK_ERR_CAPACITY;
+  }
+  for (auto& tv : e.slots)
+    for (auto& lv : tv)
+      for (auto& sl : lv) HK_REQUIRE(sl.bound, "hk_engine_tick: weight %s not loaded", sl.def.name);
+  HK_REQUIRE(run_off_host[0] == 0, "hk_engine_tick: run_off[0] must be 0");
+  const int n_rows = run_off_host[n_runs];
+  if (n_rows > e.max_rows) {
+    hk::set_error("hk_engine_tick: %d rows exceeds max_rows %d", n_rows, e.max_rows);
+    return HK_ERR_CAPACITY;
+  }
+  int prev = INT32_MAX;
+  for (int i = 0; i < n_runs; ++i) {
+    const int len = run_off_host[i + 1] - run_off_host[i];
+    HK_REQUIRE(len >= 1, "hk_engine_tick: run %d is empty", i);
+    HK_REQUIRE(len <= prev, "hk_engine_tick: runs must be sorted by non-increasing length");
+    prev = len;
+    const int slot = slot_ids_host[i];
+    HK_REQUIRE(slot >= 0 && slot < e.capacity, "hk_engine_tick: slot %d out of range", slot);
+  }
+  for (int i = 0; i < n_runs; ++i) {
+    char& seen = e.seen[slot_ids_host[i]];
+    if (seen) {
+      for (int j = 0; j < i; ++j) e.seen[slot_ids_host[j]] = 0;
+      hk::set_error("hk_engine_tick: slot %d appears in two runs", slot_ids_host[i]);
+      return HK_ERR_ARG;
+    }
+    seen = 1;
+  }
+  for (int i = 0; i < n_runs; ++i) e.seen[slot_ids_host[i]] = 0;
+
+  // Descriptors through a two-deep pinned ring (the copy of tick k-2 must be
+  // done before its staging area is rewritten).
+  const int k = e.stage_idx;
+  e.stage_idx ^= 1;
+  HK_CHECK_HIP(hipEventSynchronize(e.stage_done[k]));
+  int* stage = e.h_stage + (size_t)k * (2 * e.max_runs + 1);
+  std::memcpy(stage, slot_ids_host, (size_t)n_runs * 4);
+  std::memcpy(stage + n_runs, run_off_host, (size_t)(n_runs + 1) * 4);
+  HK_CHECK_HIP(hipMemcpyAsync(e.d_slots, stage, (size_t)n_runs * 4, hipMemcpyHostToDevice, s));
+  HK_CHECK_HIP(
+      hipMemcpyAsync(e.d_off, stage + n_runs, (size_t)(n_runs + 1) * 4, hipMemcpyHostToDevice, s));
+  HK_CHECK_HIP(hipEventRecord(e.stage_done[k], s));
+
+  std::vector<int> act(run_off_host[1] - run_off_host[0]);
+  for (size_t t = 0; t < act.size(); ++t) {
+    int c = 0;
+    while (c < n_runs && run_off_host[c + 1] - run_off_host[c] > (int)t) ++c;
+    act[t] = c;
+  }
+  hk::Runs r{e.d_slots, e.d_off, n_runs, n_rows};
+  HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, s));
+  for (int t = 0; t < hk::kTowers; ++t) HK_TRY(hk::run_tower(e, t, r, act, preds_dev, s));
+  return HK_OK;
+}
+
+}  // extern "C"

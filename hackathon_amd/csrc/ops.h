@@ -1,0 +1,108 @@
+// Row-wise and per-run kernels of the ensemble step (launchers).
+//
+// Row kernels take request rows r in [0, n). Run kernels take run
+// descriptors: run i advances slot slot_ids[i] over rows run_off[i] ..
+// run_off[i+1]-1 in order; runs are sorted by non-increasing length.
+#pragma once
+
+#include "common.h"
+
+namespace hk {
+
+struct Runs {
+  const int* slot_ids = nullptr;  // device [n_runs]
+  const int* run_off = nullptr;   // device [n_runs + 1]
+  int n_runs = 0;
+  int n_rows = 0;
+};
+
+// ---- row kernels (rowops.hip) ---------------------------------------------
+
+// out = x * rsqrt(mean(x^2) + eps) * w (model/inference_model.py:58,60;
+// model/mamba2.py:45). out_lp (bf16) optional.
+int rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, int n_rows, int width,
+                 float* out, int64_t ldo, uint16_t* out_lp, int64_t ldl, hipStream_t s);
+
+// Features [n, f] -> zero-padded GEMM operand [n, kpad] (fp32 and/or bf16).
+int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, uint16_t* out_lp,
+                   hipStream_t s);
+
+// Mamba2 tail before out_proj (model/mamba2.py:158-164):
+// y = (ssm_out + d[head] * x) * silu(z); RMSNorm(eps 1e-5) * w.
+int mamba2_post(const float* ssm_out, const float* x, int64_t ldx, const float* z, int64_t ldz,
+                const float* d, const float* w, int n_rows, int inner, int head_size,
+                float* out, uint16_t* out_lp, hipStream_t s);
+
+// dt = softplus(dt_raw); decay = exp(a[head] * dt) (model/mamba2.py:92-97).
+int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float* dt,
+              float* decay, hipStream_t s);
+
+// RetNet tail before out_proj (model/retnet.py:168-169): per-head RMSNorm
+// (eps 1e-6, no affine), times silu(g).
+int retnet_post(const float* o, const float* g, int64_t ldg, int n_rows, int hidden,
+                int head_size, float* out, uint16_t* out_lp, hipStream_t s);
+
+// sLSTM block tail + mLSTM block norm (model/xlstm.py:422-424, :308):
+// x1 = GroupNorm(groups)(y) + skip; xn = LayerNorm(x1) * w_ln.
+int slstm_post(const float* y, const float* skip, const float* gn_w, const float* gn_b,
+               int groups, const float* ln_w, int n_rows, int hidden, float* x1, float* xn,
+               uint16_t* xn_lp, hipStream_t s);
+
+// out = LayerNorm(x) * w (+ residual) (no bias; eps 1e-5).
+int layernorm_rows(const float* x, const float* w, const float* residual, int n_rows, int width,
+                   float* out, uint16_t* out_lp, hipStream_t s);
+
+// mLSTM cell/block tail (model/xlstm.py:236-241, :321-322):
+// out = GroupNorm(num / den) ; h = (out + skip * x_conv) * silu(x_gate).
+int mlstm_post(const float* num, const float* den, int den_ld, const float* gn_w,
+               const float* gn_b, const float* skip_w, const float* x_conv, const float* x_gate,
+               int64_t ld_gate, int n_rows, int inner, int heads, float* out, uint16_t* out_lp,
+               hipStream_t s);
+
+// preds[r, col] = x[r] . w + b (shared output_proj, model/inference_model.py:142).
+int output_proj(const float* x, const float* w, const float* b, int n_rows, int hidden,
+                float* preds, int pred_ld, int col, hipStream_t s);
+
+// mLSTM q/k/v BlockLinear with 4x4 blocks (model/xlstm.py:286-288, :315-317):
+// qkv[:, 0:I] = q, [:, I:2I] = k, [:, 2I:3I] = v; ks = k / k_div.
+int mlstm_qkv(const float* x_conv, const float* x_m, int64_t ld_xm, const float* wq,
+              const float* wk, const float* wv, int n_rows, int inner, int blk, float k_div,
+              float* qkv, float* ks, hipStream_t s);
+
+// bf16 copy of an fp32 matrix (weights at bind time).
+int to_bf16(const float* src, uint16_t* dst, int64_t n, hipStream_t s);
+// fill with a constant
+int fill_f32(float* dst, int64_t n, float v, hipStream_t s);
+
+// ---- run kernels (scans.hip) ----------------------------------------------
+
+// Depthwise causal conv over each run (model/modules.py:45-49), kernel 4:
+// window = [state(3 oldest..newest), x]; out = bias + sum_j w[j] * window[j];
+// state <- last three inputs. state is [slot][3][C], w is [4][C] (tap-major).
+int conv_scan(const Runs& r, const float* in, int64_t ld_in, int channels, float* state,
+              int64_t slot_stride, const float* w, const float* bias, int act_silu, float* out,
+              int64_t ldo, hipStream_t s);
+
+// RetNet rotary + scale recurrence (model/retnet.py:239-269, :340).
+int retnet_prep(const Runs& r, const float* qkvg, int64_t ld, int hidden, int heads,
+                float k_scaling, const float* angle, const float* decay, int* offsets,
+                float* scales, float* k_rope, float* q_scaled, hipStream_t s);
+
+// Hawk RG-LRU over each run, times gelu(gate) (model/hawk.py:31-37, :77, :83).
+int rglru_scan(const Runs& r, const float* x, const float* gi, const float* gr, int64_t ldg,
+               const float* gate, int64_t ld_gate, const float* a, float c_exp, int hidden,
+               float* h_state, float* out, uint16_t* out_lp, hipStream_t s);
+
+// One sLSTM step for the first n_active runs (model/xlstm.py:414-421, :355-369).
+int slstm_round(const Runs& r, int step, int n_active, const float* gin, int hidden, int heads,
+                const float* w_state, const float* b_state, const float* h_state, float* c_state,
+                float* n_state, float* m_state, float* y, hipStream_t s);
+// After the last round: h_state[slot] = y[last row of the run].
+int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipStream_t s);
+
+// mLSTM gate / normaliser recurrence (model/xlstm.py:147-168, :236-238).
+int mlstm_gates(const Runs& r, const float* if_pre, int heads, const float* qkv, int inner,
+                const float* ks, float* n_state, float* m_state, float* ig, float* fg, float* den,
+                hipStream_t s);
+
+}  // namespace hk

@@ -1,0 +1,388 @@
+// Row-wise kernels: norms and the fused elementwise tails of each layer.
+//
+// One work-group per request row. Normalisations keep the reference's
+// formulas (mean of squares / biased variance over the normalised extent,
+// eps inside the square root); reductions run in a fixed order, so a row's
+// result does not depend on the batch it rides in.
+#include "ops.h"
+
+namespace hk {
+namespace {
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, int64_t ldx,
+                                                      const float* __restrict__ w, float eps,
+                                                      int width, float* __restrict__ out,
+                                                      int64_t ldo, uint16_t* __restrict__ out_lp,
+                                                      int64_t ldl) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * ldx;
+  float ss = 0.0f;
+  for (int c = threadIdx.x; c < width; c += 256) {
+    const float v = xr[c];
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)width + eps);
+  for (int c = threadIdx.x; c < width; c += 256) {
+    const float o = (xr[c] * inv) * w[c];
+    if (out) out[row * ldo + c] = o;
+    if (out_lp) out_lp[row * ldl + c] = f32_to_bf16_bits(o);
+  }
+}
+
+__global__ void stage_features_kernel(const float* __restrict__ feat, int n_rows, int f, int kpad,
+                                      float* __restrict__ out, uint16_t* __restrict__ out_lp) {
+  const int64_t total = (int64_t)n_rows * kpad;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / kpad;
+    const int c = (int)(i % kpad);
+    const float v = c < f ? feat[r * f + c] : 0.0f;
+    if (out) out[i] = v;
+    if (out_lp) out_lp[i] = f32_to_bf16_bits(v);
+  }
+}
+
+__global__ __launch_bounds__(256) void mamba2_post_kernel(
+    const float* __restrict__ ssm_out, const float* __restrict__ x, int64_t ldx,
+    const float* __restrict__ z, int64_t ldz, const float* __restrict__ d,
+    const float* __restrict__ w, int inner, int head_size, float* __restrict__ out,
+    uint16_t* __restrict__ out_lp) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* so = ssm_out + row * inner;
+  const float* xr = x + row * ldx;
+  const float* zr = z + row * ldz;
+  float ss = 0.0f;
+  for (int c = threadIdx.x; c < inner; c += 256) {
+    const float y = (so[c] + d[c / head_size] * xr[c]) * silu(zr[c]);
+    ss += y * y;
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)inner + 1e-5f);
+  for (int c = threadIdx.x; c < inner; c += 256) {
+    const float y = (so[c] + d[c / head_size] * xr[c]) * silu(zr[c]);
+    const float o = (y * inv) * w[c];
+    if (out) out[row * inner + c] = o;
+    if (out_lp) out_lp[row * inner + c] = f32_to_bf16_bits(o);
+  }
+}
+
+__global__ void mamba2_dt_kernel(const float* __restrict__ dt_raw, const float* __restrict__ a,
+                                 int n_rows, int heads, float* __restrict__ dt,
+                                 float* __restrict__ decay) {
+  const int64_t total = (int64_t)n_rows * heads;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = softplus(dt_raw[i]);
+    dt[i] = v;
+    decay[i] = expf(a[i % heads] * v);
+  }
+}
+
+// One wave per head.
+__global__ void retnet_post_kernel(const float* __restrict__ o, const float* __restrict__ g,
+                                   int64_t ldg, int hidden, int head_size,
+                                   float* __restrict__ out, uint16_t* __restrict__ out_lp) {
+  const int64_t row = blockIdx.x;
+  const int head = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const float* orow = o + row * hidden + (int64_t)head * head_size;
+  const float* grow = g + row * ldg + (int64_t)head * head_size;
+  float ss = 0.0f;
+  for (int j = lane; j < head_size; j += 64) {
+    const float v = orow[j];
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)head_size + 1e-6f);
+  for (int j = lane; j < head_size; j += 64) {
+    const float v = silu(grow[j]) * (orow[j] * inv);
+    const int64_t idx = row * hidden + (int64_t)head * head_size + j;
+    if (out) out[idx] = v;
+    if (out_lp) out_lp[idx] = f32_to_bf16_bits(v);
+  }
+}
+
+// One wave per group, then a block-wide LayerNorm over the whole row.
+__global__ void slstm_post_kernel(const float* __restrict__ y, const float* __restrict__ skip,
+                                  const float* __restrict__ gn_w, const float* __restrict__ gn_b,
+                                  const float* __restrict__ ln_w, int hidden, int gsize,
+                                  float* __restrict__ x1, float* __restrict__ xn,
+                                  uint16_t* __restrict__ xn_lp) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const int grp = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t base = row * hidden + (int64_t)grp * gsize;
+  float s = 0.0f;
+  for (int j = lane; j < gsize; j += 64) s += y[base + j];
+  const float mean = wave_sum(s) / (float)gsize;
+  float v = 0.0f;
+  for (int j = lane; j < gsize; j += 64) {
+    const float dlt = y[base + j] - mean;
+    v += dlt * dlt;
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(v) / (float)gsize + 1e-5f);
+  float rs = 0.0f;
+  for (int j = lane; j < gsize; j += 64) {
+    const int c = grp * gsize + j;
+    const float o = ((y[base + j] - mean) * rstd) * gn_w[c] + gn_b[c] + skip[base + j];
+    x1[base + j] = o;
+    rs += o;
+  }
+  __threadfence_block();
+  const float rmean = block_sum(rs, red) / (float)hidden;
+  float rv = 0.0f;
+  for (int j = lane; j < gsize; j += 64) {
+    const float dlt = x1[base + j] - rmean;
+    rv += dlt * dlt;
+  }
+  const float rrstd = 1.0f / sqrtf(block_sum(rv, red) / (float)hidden + 1e-5f);
+  for (int j = lane; j < gsize; j += 64) {
+    const int c = grp * gsize + j;
+    const float o = ((x1[base + j] - rmean) * rrstd) * ln_w[c];
+    if (xn) xn[base + j] = o;
+    if (xn_lp) xn_lp[base + j] = f32_to_bf16_bits(o);
+  }
+}
+
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ residual,
+                                                        int width, float* __restrict__ out,
+                                                        uint16_t* __restrict__ out_lp) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * width;
+  float s = 0.0f;
+  for (int c = threadIdx.x; c < width; c += 256) s += xr[c];
+  const float mean = block_sum(s, red) / (float)width;
+  float v = 0.0f;
+  for (int c = threadIdx.x; c < width; c += 256) {
+    const float dlt = xr[c] - mean;
+    v += dlt * dlt;
+  }
+  const float rstd = 1.0f / sqrtf(block_sum(v, red) / (float)width + 1e-5f);
+  for (int c = threadIdx.x; c < width; c += 256) {
+    float o = ((xr[c] - mean) * rstd) * w[c];
+    if (residual) o += residual[row * width + c];
+    if (out) out[row * width + c] = o;
+    if (out_lp) out_lp[row * width + c] = f32_to_bf16_bits(o);
+  }
+}
+
+// One wave per head (= GroupNorm group).
+__global__ void mlstm_post_kernel(const float* __restrict__ num, const float* __restrict__ den,
+                                  int den_ld, const float* __restrict__ gn_w,
+                                  const float* __restrict__ gn_b, const float* __restrict__ skip_w,
+                                  const float* __restrict__ x_conv,
+                                  const float* __restrict__ x_gate, int64_t ld_gate, int inner,
+                                  int hs, float* __restrict__ out, uint16_t* __restrict__ out_lp) {
+  const int64_t row = blockIdx.x;
+  const int head = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t base = row * inner + (int64_t)head * hs;
+  const float dn = den[row * den_ld + head];
+  float s = 0.0f;
+  for (int j = lane; j < hs; j += 64) s += num[base + j] / dn;
+  const float mean = wave_sum(s) / (float)hs;
+  float v = 0.0f;
+  for (int j = lane; j < hs; j += 64) {
+    const float dlt = num[base + j] / dn - mean;
+    v += dlt * dlt;
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(v) / (float)hs + 1e-5f);
+  for (int j = lane; j < hs; j += 64) {
+    const int c = head * hs + j;
+    const float gnv = ((num[base + j] / dn - mean) * rstd) * gn_w[c] + gn_b[c];
+    const float h = (gnv + skip_w[c] * x_conv[base + j]) * silu(x_gate[row * ld_gate + c]);
+    if (out) out[base + j] = h;
+    if (out_lp) out_lp[base + j] = f32_to_bf16_bits(h);
+  }
+}
+
+// One wave per row.
+__global__ void output_proj_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                   const float* __restrict__ b, int n_rows, int hidden,
+                                   float* __restrict__ preds, int pred_ld, int col) {
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const int lane = threadIdx.x & 63;
+  const float* xr = x + row * hidden;
+  float s = 0.0f;
+  for (int c = lane; c < hidden; c += 64) s += xr[c] * w[c];
+  s = wave_sum(s);
+  if (lane == 0) preds[row * pred_ld + col] = s + b[0];
+}
+
+__global__ void mlstm_qkv_kernel(const float* __restrict__ x_conv, const float* __restrict__ x_m,
+                                 int64_t ld_xm, const float* __restrict__ wq,
+                                 const float* __restrict__ wk, const float* __restrict__ wv,
+                                 int n_rows, int inner, int blk, float k_div,
+                                 float* __restrict__ qkv, float* __restrict__ ks) {
+  const int64_t total = (int64_t)n_rows * inner;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / inner;
+    const int c = (int)(i % inner);
+    const int nb = c / blk;  // block index
+    const int kk = c % blk;  // output index within the block
+    const float* xc = x_conv + r * inner + (int64_t)nb * blk;
+    const float* xm = x_m + r * ld_xm + (int64_t)nb * blk;
+    const int64_t woff = ((int64_t)nb * blk + kk) * blk;  // W[nb][kk][:]
+    float q = 0.0f, k = 0.0f, v = 0.0f;
+    for (int h = 0; h < blk; ++h) {
+      q += xc[h] * wq[woff + h];
+      k += xc[h] * wk[woff + h];
+      v += xm[h] * wv[woff + h];
+    }
+    float* out = qkv + r * 3 * (int64_t)inner;
+    out[c] = q;
+    out[inner + c] = k;
+    out[2 * inner + c] = v;
+    ks[r * inner + c] = k / k_div;
+  }
+}
+
+__global__ void to_bf16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                               int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = f32_to_bf16_bits(src[i]);
+}
+
+__global__ void fill_f32_kernel(float* __restrict__ dst, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = v;
+}
+
+inline unsigned grid_for(int64_t total, int block = 256) {
+  int64_t g = (total + block - 1) / block;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (unsigned)g;
+}
+
+}  // namespace
+
+int rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, int n_rows, int width,
+                 float* out, int64_t ldo, uint16_t* out_lp, int64_t ldl, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_rows), dim3(256), 0, s, x, ldx, w, eps, width, out,
+                     ldo, out_lp, ldl);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, uint16_t* out_lp,
+                   hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  hipLaunchKernelGGL(stage_features_kernel, dim3(grid_for((int64_t)n_rows * kpad)), dim3(256), 0,
+                     s, feat, n_rows, f, kpad, out, out_lp);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int mamba2_post(const float* ssm_out, const float* x, int64_t ldx, const float* z, int64_t ldz,
+                const float* d, const float* w, int n_rows, int inner, int head_size,
+                float* out, uint16_t* out_lp, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  hipLaunchKernelGGL(mamba2_post_kernel, dim3(n_rows), dim3(256), 0, s, ssm_out, x, ldx, z, ldz,
+                     d, w, inner, head_size, out, out_lp);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float* dt,
+              float* decay, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  hipLaunchKernelGGL(mamba2_dt_kernel, dim3(grid_for((int64_t)n_rows * heads)), dim3(256), 0, s,
+                     dt_raw, a, n_rows, heads, dt, decay);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int retnet_post(const float* o, const float* g, int64_t ldg, int n_rows, int hidden,
+                int head_size, float* out, uint16_t* out_lp, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  const int heads = hidden / head_size;
+  HK_REQUIRE(heads * head_size == hidden && heads <= 16, "retnet_post: %d heads unsupported",
+             heads);
+  hipLaunchKernelGGL(retnet_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, o, g, ldg, hidden,
+                     head_size, out, out_lp);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int slstm_post(const float* y, const float* skip, const float* gn_w, const float* gn_b,
+               int groups, const float* ln_w, int n_rows, int hidden, float* x1, float* xn,
+               uint16_t* xn_lp, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  HK_REQUIRE(groups >= 1 && groups <= 16 && hidden % groups == 0,
+             "slstm_post: %d groups unsupported", groups);
+  hipLaunchKernelGGL(slstm_post_kernel, dim3(n_rows), dim3(64 * groups), 0, s, y, skip, gn_w,
+                     gn_b, ln_w, hidden, hidden / groups, x1, xn, xn_lp);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int layernorm_rows(const float* x, const float* w, const float* residual, int n_rows, int width,
+                   float* out, uint16_t* out_lp, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  hipLaunchKernelGGL(layernorm_kernel, dim3(n_rows), dim3(256), 0, s, x, w, residual, width, out,
+                     out_lp);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int mlstm_post(const float* num, const float* den, int den_ld, const float* gn_w,
+               const float* gn_b, const float* skip_w, const float* x_conv, const float* x_gate,
+               int64_t ld_gate, int n_rows, int inner, int heads, float* out, uint16_t* out_lp,
+               hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  HK_REQUIRE(heads >= 1 && heads <= 16 && inner % heads == 0, "mlstm_post: %d heads unsupported",
+             heads);
+  hipLaunchKernelGGL(mlstm_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, num, den, den_ld,
+                     gn_w, gn_b, skip_w, x_conv, x_gate, ld_gate, inner, inner / heads, out,
+                     out_lp);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int output_proj(const float* x, const float* w, const float* b, int n_rows, int hidden,
+                float* preds, int pred_ld, int col, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  hipLaunchKernelGGL(output_proj_kernel, dim3((n_rows + 3) / 4), dim3(256), 0, s, x, w, b, n_rows,
+                     hidden, preds, pred_ld, col);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int mlstm_qkv(const float* x_conv, const float* x_m, int64_t ld_xm, const float* wq,
+              const float* wk, const float* wv, int n_rows, int inner, int blk, float k_div,
+              float* qkv, float* ks, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  hipLaunchKernelGGL(mlstm_qkv_kernel, dim3(grid_for((int64_t)n_rows * inner)), dim3(256), 0, s,
+                     x_conv, x_m, ld_xm, wq, wk, wv, n_rows, inner, blk, k_div, qkv, ks);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int to_bf16(const float* src, uint16_t* dst, int64_t n, hipStream_t s) {
+  if (n == 0) return HK_OK;
+  hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int fill_f32(float* dst, int64_t n, float v, hipStream_t s) {
+  if (n == 0) return HK_OK;
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, dst, n, v);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+}  // namespace hk

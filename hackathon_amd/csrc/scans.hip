@@ -1,0 +1,368 @@
+// Per-run scan kernels: each work-group walks one symbol's run of requests
+// in order, carrying that symbol's small recurrent state in registers, so the
+// state is read once and written once per tick.
+#include "ops.h"
+
+namespace hk {
+namespace {
+
+// grid (runs, ceil(C/256)); thread per channel.
+__global__ __launch_bounds__(256) void conv_scan_kernel(
+    const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ in,
+    int64_t ld_in, int channels, float* __restrict__ state, int64_t slot_stride,
+    const float* __restrict__ w, const float* __restrict__ bias, int act_silu,
+    float* __restrict__ out, int64_t ldo) {
+  const int run = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  if (c >= channels) return;
+  const int slot = slot_ids[run];
+  const int r0 = run_off[run];
+  const int r1 = run_off[run + 1];
+  float* st = state + (int64_t)slot * slot_stride;
+  float s0 = st[c], s1 = st[channels + c], s2 = st[2 * channels + c];
+  const float w0 = w[c], w1 = w[channels + c], w2 = w[2 * channels + c], w3 = w[3 * channels + c];
+  const float b = bias[c];
+  for (int r = r0; r < r1; ++r) {
+    const float x = in[(int64_t)r * ld_in + c];
+    float v = b + w0 * s0;
+    v += w1 * s1;
+    v += w2 * s2;
+    v += w3 * x;
+    out[(int64_t)r * ldo + c] = act_silu ? silu(v) : v;
+    s0 = s1;
+    s1 = s2;
+    s2 = x;
+  }
+  st[c] = s0;
+  st[channels + c] = s1;
+  st[2 * channels + c] = s2;
+}
+
+// grid (runs, ceil(hidden/256)); thread per channel. The scale recurrence
+// s' = s*gamma + 1 is per head and is recomputed by every thread of the head.
+__global__ __launch_bounds__(256) void retnet_prep_kernel(
+    const int* __restrict__ slot_ids, const int* __restrict__ run_off,
+    const float* __restrict__ qkvg, int64_t ld, int hidden, int head_size, float k_scaling,
+    const float* __restrict__ angle, const float* __restrict__ decay,
+    const int* __restrict__ offsets, const float* __restrict__ scales, float* __restrict__ k_rope,
+    float* __restrict__ q_scaled) {
+  const int run = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  if (c >= hidden) return;
+  const int heads = hidden / head_size;
+  const int head = c / head_size;
+  const int j = c % head_size;
+  const int partner = (j & 1) ? c - 1 : c + 1;
+  const float sign = (j & 1) ? 1.0f : -1.0f;  // rotate_every_two: (-x1, x0)
+  const int slot = slot_ids[run];
+  const int r0 = run_off[run];
+  const int r1 = run_off[run + 1];
+  const int off0 = offsets[slot];
+  float sc = scales[(int64_t)slot * heads + head];
+  const float gam = decay[head];
+  const float ang = angle[j];
+  for (int r = r0; r < r1; ++r) {
+    const float* row = qkvg + (int64_t)r * ld;
+    const float theta = (float)(off0 + (r - r0)) * ang;
+    const float sn = sinf(theta);
+    const float cs = cosf(theta);
+    const float q = row[c];
+    const float qp = sign * row[partner];
+    const float k = row[hidden + c] * k_scaling;
+    const float kp = sign * (row[hidden + partner] * k_scaling);
+    const float qr = q * cs + qp * sn;
+    const float kr = k * cs + kp * sn;
+    sc = sc * gam + 1.0f;
+    const float sf = 1.0f / sqrtf(sc);
+    k_rope[(int64_t)r * hidden + c] = kr;
+    q_scaled[(int64_t)r * hidden + c] = qr * sf;
+  }
+}
+
+// After retnet_prep: offsets += run length; scales advanced through the run
+// (s' = s*gamma + 1 per step). Thread per (run, head).
+__global__ void retnet_advance_kernel(const int* __restrict__ slot_ids,
+                                      const int* __restrict__ run_off, int n_runs, int heads,
+                                      const float* __restrict__ decay, int* __restrict__ offsets,
+                                      float* __restrict__ scales) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_runs * heads) return;
+  const int run = i / heads;
+  const int head = i % heads;
+  const int slot = slot_ids[run];
+  const int len = run_off[run + 1] - run_off[run];
+  float sc = scales[(int64_t)slot * heads + head];
+  const float gam = decay[head];
+  for (int t = 0; t < len; ++t) sc = sc * gam + 1.0f;
+  scales[(int64_t)slot * heads + head] = sc;
+  if (head == 0) offsets[slot] += len;
+}
+
+// grid (runs, ceil(hidden/256)); thread per channel.
+__global__ __launch_bounds__(256) void rglru_scan_kernel(
+    const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ x,
+    const float* __restrict__ gi, const float* __restrict__ gr, int64_t ldg,
+    const float* __restrict__ gate, int64_t ld_gate, const float* __restrict__ a, float c_exp,
+    int hidden, float* __restrict__ h_state, float* __restrict__ out,
+    uint16_t* __restrict__ out_lp) {
+  const int run = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  if (c >= hidden) return;
+  const int slot = slot_ids[run];
+  const int r0 = run_off[run];
+  const int r1 = run_off[run + 1];
+  float h = h_state[(int64_t)slot * hidden + c];
+  const float base = a[c];
+  for (int r = r0; r < r1; ++r) {
+    const int64_t ri = (int64_t)r;
+    const float it = sigmoid(gi[ri * ldg + c]);
+    const float rt = sigmoid(gr[ri * ldg + c]);
+    const float at = powf(base, c_exp * rt);
+    const float mult = sqrtf(1.0f - at * at);
+    h = (h * at) + (mult * (it * x[ri * hidden + c]));
+    const float o = gelu_erf(gate[ri * ld_gate + c]) * h;
+    if (out) out[ri * hidden + c] = o;
+    if (out_lp) out_lp[ri * hidden + c] = f32_to_bf16_bits(o);
+  }
+  h_state[(int64_t)slot * hidden + c] = h;
+}
+
+// One sLSTM step. grid (heads, units/16, ceil(n_active/16)); 256 threads =
+// 4 waves, wave g computes gate g (i, f, z, o) for 16 units x 16 runs:
+// lane = (unit u = lane%16, k-quarter = lane/16), then a 4-lane butterfly.
+constexpr int kSlRuns = 16;
+constexpr int kSlUnits = 16;
+
+__global__ __launch_bounds__(256) void slstm_round_kernel(
+    const int* __restrict__ slot_ids, const int* __restrict__ run_off, int step, int n_active,
+    const float* __restrict__ gin, int hidden, int hs, const float* __restrict__ w_state,
+    const float* __restrict__ b_state, const float* __restrict__ h_state,
+    float* __restrict__ c_state, float* __restrict__ n_state, float* __restrict__ m_state,
+    float* __restrict__ y) {
+  extern __shared__ float smem[];
+  float* hp = smem;                            // [kSlRuns][hs]
+  float* gsum = smem + kSlRuns * hs;           // [4][kSlRuns][kSlUnits]
+  const int head = blockIdx.x;
+  const int u0 = blockIdx.y * kSlUnits;
+  const int rb = blockIdx.z * kSlRuns;
+  const int nr = min(kSlRuns, n_active - rb);
+  const int heads = hidden / hs;
+
+  // Stage h_{t-1} of each run's head block.
+  for (int i = threadIdx.x; i < kSlRuns * hs; i += 256) {
+    const int rr = i / hs;
+    const int k = i % hs;
+    float v = 0.0f;
+    if (rr < nr) {
+      const int run = rb + rr;
+      const int row = run_off[run] + step;
+      v = step == 0 ? h_state[(int64_t)slot_ids[run] * hidden + head * hs + k]
+                    : y[(int64_t)(row - 1) * hidden + head * hs + k];
+    }
+    hp[i] = v;
+  }
+  __syncthreads();
+
+  const int g = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int u = lane & 15;
+  const int kq = lane >> 4;
+  const int kchunk = hs / 4;
+  // W[g][head][unit][k] (BlockLinear weight (blocks, out, in)).
+  const float* wrow =
+      w_state + (((int64_t)g * heads + head) * hs + (u0 + u)) * hs + (int64_t)kq * kchunk;
+  float acc[kSlRuns];
+#pragma unroll
+  for (int i = 0; i < kSlRuns; ++i) acc[i] = 0.0f;
+  for (int k = 0; k < kchunk; ++k) {
+    const float wv = wrow[k];
+    const float* hk = hp + kq * kchunk + k;
+#pragma unroll
+    for (int i = 0; i < kSlRuns; ++i) acc[i] += wv * hk[i * hs];
+  }
+#pragma unroll
+  for (int i = 0; i < kSlRuns; ++i) {
+    float v = acc[i];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    acc[i] = v;
+  }
+  if (kq == 0) {
+#pragma unroll
+    for (int i = 0; i < kSlRuns; ++i) gsum[(g * kSlRuns + i) * kSlUnits + u] = acc[i];
+  }
+  __syncthreads();
+
+  const int rr = threadIdx.x / kSlUnits;
+  const int uu = threadIdx.x % kSlUnits;
+  if (rr >= nr) return;
+  const int run = rb + rr;
+  const int slot = slot_ids[run];
+  const int row = run_off[run] + step;
+  const int col = head * hs + u0 + uu;
+  const float* gr = gin + (int64_t)row * 4 * hidden;
+  const float ip = gr[col] + (gsum[(0 * kSlRuns + rr) * kSlUnits + uu] + b_state[col]);
+  const float fp = gr[hidden + col] + (gsum[(1 * kSlRuns + rr) * kSlUnits + uu] + b_state[hidden + col]);
+  const float zp =
+      gr[2 * hidden + col] + (gsum[(2 * kSlRuns + rr) * kSlUnits + uu] + b_state[2 * hidden + col]);
+  const float op =
+      gr[3 * hidden + col] + (gsum[(3 * kSlRuns + rr) * kSlUnits + uu] + b_state[3 * hidden + col]);
+  const int64_t si = (int64_t)slot * hidden + col;
+  const float m = m_state[si];
+  const float lfm = m + logsigmoid(fp);
+  const float mn = fmaxf(ip, lfm);
+  const float og = sigmoid(op);
+  const float ig = expf(ip - mn);
+  const float fg = expf(lfm - mn);
+  const float cn = fg * c_state[si] + ig * tanhf(zp);
+  const float nn = fg * n_state[si] + ig;
+  c_state[si] = cn;
+  n_state[si] = nn;
+  m_state[si] = mn;
+  y[(int64_t)row * hidden + col] = og * cn / (nn + 1e-6f);
+}
+
+__global__ void slstm_final_kernel(const int* __restrict__ slot_ids,
+                                   const int* __restrict__ run_off, const float* __restrict__ y,
+                                   int hidden, float* __restrict__ h_state) {
+  const int run = blockIdx.x;
+  const int last = run_off[run + 1] - 1;
+  const int slot = slot_ids[run];
+  for (int c = threadIdx.x; c < hidden; c += blockDim.x)
+    h_state[(int64_t)slot * hidden + c] = y[(int64_t)last * hidden + c];
+}
+
+// grid (runs, heads); 256 threads over the head's hs elements of n.
+__global__ __launch_bounds__(256) void mlstm_gates_kernel(
+    const int* __restrict__ slot_ids, const int* __restrict__ run_off,
+    const float* __restrict__ if_pre, int heads, const float* __restrict__ qkv, int inner,
+    const float* __restrict__ ks, float* __restrict__ n_state, float* __restrict__ m_state,
+    float* __restrict__ ig_out, float* __restrict__ fg_out, float* __restrict__ den_out) {
+  __shared__ float red[4];
+  constexpr int kMaxPer = 8;  // head size <= 2048
+  const int run = blockIdx.x;
+  const int head = blockIdx.y;
+  const int hs = inner / heads;
+  const int slot = slot_ids[run];
+  const int r0 = run_off[run];
+  const int r1 = run_off[run + 1];
+  float* nst = n_state + ((int64_t)slot * heads + head) * hs;
+  float nv[kMaxPer];
+#pragma unroll
+  for (int i = 0; i < kMaxPer; ++i) {
+    const int h = threadIdx.x + i * 256;
+    nv[i] = h < hs ? nst[h] : 0.0f;
+  }
+  float m = m_state[(int64_t)slot * heads + head];
+  for (int r = r0; r < r1; ++r) {
+    const float ipre = if_pre[(int64_t)r * 2 * heads + head];
+    const float fpre = if_pre[(int64_t)r * 2 * heads + heads + head];
+    const float log_f = logsigmoid(fpre);
+    const float mn = fmaxf(ipre, m + log_f);
+    const float ig = expf(ipre - mn);
+    const float fg = expf(log_f + m - mn);
+    const float* q = qkv + (int64_t)r * 3 * inner + (int64_t)head * hs;
+    const float* k = ks + (int64_t)r * inner + (int64_t)head * hs;
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) {
+      const int h = threadIdx.x + i * 256;
+      if (h < hs) {
+        nv[i] = fg * nv[i] + ig * k[h];
+        dot += q[h] * nv[i];
+      }
+    }
+    dot = block_sum(dot, red);
+    m = mn;
+    if (threadIdx.x == 0) {
+      ig_out[(int64_t)r * heads + head] = ig;
+      fg_out[(int64_t)r * heads + head] = fg;
+      den_out[(int64_t)r * heads + head] = fmaxf(fabsf(dot), expf(-mn)) + 1e-6f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxPer; ++i) {
+    const int h = threadIdx.x + i * 256;
+    if (h < hs) nst[h] = nv[i];
+  }
+  if (threadIdx.x == 0) m_state[(int64_t)slot * heads + head] = m;
+}
+
+}  // namespace
+
+int conv_scan(const Runs& r, const float* in, int64_t ld_in, int channels, float* state,
+              int64_t slot_stride, const float* w, const float* bias, int act_silu, float* out,
+              int64_t ldo, hipStream_t s) {
+  if (r.n_runs == 0) return HK_OK;
+  dim3 grid(r.n_runs, (channels + 255) / 256);
+  hipLaunchKernelGGL(conv_scan_kernel, grid, dim3(256), 0, s, r.slot_ids, r.run_off, in, ld_in,
+                     channels, state, slot_stride, w, bias, act_silu, out, ldo);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int retnet_prep(const Runs& r, const float* qkvg, int64_t ld, int hidden, int heads,
+                float k_scaling, const float* angle, const float* decay, int* offsets,
+                float* scales, float* k_rope, float* q_scaled, hipStream_t s) {
+  if (r.n_runs == 0) return HK_OK;
+  HK_REQUIRE(hidden % heads == 0 && (hidden / heads) % 2 == 0, "retnet_prep: bad head size");
+  dim3 grid(r.n_runs, (hidden + 255) / 256);
+  hipLaunchKernelGGL(retnet_prep_kernel, grid, dim3(256), 0, s, r.slot_ids, r.run_off, qkvg, ld,
+                     hidden, hidden / heads, k_scaling, angle, decay, offsets, scales, k_rope,
+                     q_scaled);
+  HK_LAUNCH_CHECK();
+  const int n = r.n_runs * heads;
+  hipLaunchKernelGGL(retnet_advance_kernel, dim3((n + 255) / 256), dim3(256), 0, s, r.slot_ids,
+                     r.run_off, r.n_runs, heads, decay, offsets, scales);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int rglru_scan(const Runs& r, const float* x, const float* gi, const float* gr, int64_t ldg,
+               const float* gate, int64_t ld_gate, const float* a, float c_exp, int hidden,
+               float* h_state, float* out, uint16_t* out_lp, hipStream_t s) {
+  if (r.n_runs == 0) return HK_OK;
+  dim3 grid(r.n_runs, (hidden + 255) / 256);
+  hipLaunchKernelGGL(rglru_scan_kernel, grid, dim3(256), 0, s, r.slot_ids, r.run_off, x, gi, gr,
+                     ldg, gate, ld_gate, a, c_exp, hidden, h_state, out, out_lp);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int slstm_round(const Runs& r, int step, int n_active, const float* gin, int hidden, int heads,
+                const float* w_state, const float* b_state, const float* h_state, float* c_state,
+                float* n_state, float* m_state, float* y, hipStream_t s) {
+  if (n_active == 0) return HK_OK;
+  const int hs = hidden / heads;
+  HK_REQUIRE(hs * heads == hidden && hs % kSlUnits == 0 && hs % 4 == 0,
+             "slstm_round: head size %d unsupported", hs);
+  const size_t smem = (size_t)(kSlRuns * hs + 4 * kSlRuns * kSlUnits) * sizeof(float);
+  HK_REQUIRE(smem <= 64 * 1024, "slstm_round: head size %d too large for LDS staging", hs);
+  dim3 grid(heads, hs / kSlUnits, (n_active + kSlRuns - 1) / kSlRuns);
+  hipLaunchKernelGGL(slstm_round_kernel, grid, dim3(256), smem, s, r.slot_ids, r.run_off, step,
+                     n_active, gin, hidden, hs, w_state, b_state, h_state, c_state, n_state,
+                     m_state, y);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipStream_t s) {
+  if (r.n_runs == 0) return HK_OK;
+  hipLaunchKernelGGL(slstm_final_kernel, dim3(r.n_runs), dim3(256), 0, s, r.slot_ids, r.run_off,
+                     y, hidden, h_state);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int mlstm_gates(const Runs& r, const float* if_pre, int heads, const float* qkv, int inner,
+                const float* ks, float* n_state, float* m_state, float* ig, float* fg, float* den,
+                hipStream_t s) {
+  if (r.n_runs == 0) return HK_OK;
+  HK_REQUIRE(inner % heads == 0 && inner / heads <= 2048, "mlstm_gates: head size unsupported");
+  hipLaunchKernelGGL(mlstm_gates_kernel, dim3(r.n_runs, heads), dim3(256), 0, s, r.slot_ids,
+                     r.run_off, if_pre, heads, qkv, inner, ks, n_state, m_state, ig, fg, den);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+}  // namespace hk

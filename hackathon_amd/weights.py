@@ -1,0 +1,42 @@
+"""Deterministic weights (the init spec in spec.py) generated on the host by
+the library's counter-based filler, returned as CPU fp32 tensors keyed by the
+reference's state_dict names."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+from . import _lib
+from .spec import ModelConfig, param_specs
+
+_lib.register("hk_param_key", ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_char_p])
+_lib.register(
+    "hk_fill_uniform_host",
+    ctypes.c_int,
+    [ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_int],
+)
+
+
+def param_key(seed: int, name: str) -> int:
+    return int(_lib.lib().hk_param_key(seed & (2**64 - 1), name.encode()))
+
+
+def fill_uniform(t: torch.Tensor, seed: int, name: str, lo: float, hi: float) -> torch.Tensor:
+    assert t.dtype == torch.float32 and t.device.type == "cpu" and t.is_contiguous()
+    threads = min(32, os.cpu_count() or 1)
+    st = _lib.lib().hk_fill_uniform_host(
+        t.data_ptr(), t.numel(), param_key(seed, name), lo, hi, threads
+    )
+    _lib.check(st, "hk_fill_uniform_host")
+    return t
+
+
+def generate(cfg: ModelConfig, seed: int = 0) -> dict[str, torch.Tensor]:
+    """All parameters of MultiTowerModel(cfg), initialised by the spec."""
+    out = {}
+    for p in param_specs(cfg):
+        out[p.name] = fill_uniform(torch.empty(p.shape, dtype=torch.float32), seed, p.name, p.lo, p.hi)
+    return out

@@ -59,6 +59,76 @@ int hk_mamba2_step(float* ssm, const float* x, const float* b, const float* c, c
                    const float* decay, const uint8_t* mask, float* y, int batch, int heads,
                    int size_h, int size_c, void* stream);
 
+
+/* ---------------------------------------------------------------------------
+ * Deterministic parameter initialisation (host, no GPU).
+ * The reference fills its torch.empty parameters from a checkpoint
+ * (example_model.py:296-302); the build's "random-init weights" restate the
+ * ranges of check_cell_rewrite.py:187-210 with a counter-based generator, so
+ * every value is a pure function of (seed, parameter name, index).
+ * ------------------------------------------------------------------------- */
+
+/* key = mix64(fnv1a64(name) ^ mix64(seed)) */
+uint64_t hk_param_key(uint64_t seed, const char* name);
+
+/* dst[i] = lo + (hi - lo) * u_i, u_i = (mix64(key + (i+1)*golden) >> 40) * 2^-24,
+ * fp32 with two roundings; `threads` host threads. */
+int hk_fill_uniform_host(float* dst, int64_t n, uint64_t key, float lo, float hi, int threads);
+
+/* ---------------------------------------------------------------------------
+ * Ensemble engine: packed weights + slot-indexed HBM state store + tick.
+ * Replaces MultiTowerModel(config) + init_state + forward
+ * (model/inference_model.py:103-146) and the per-round step of
+ * NnInferenceClient (example_model.py:400-429, :848-883).
+ * ------------------------------------------------------------------------- */
+
+/* cfg[11] = {hidden, proj, depth, heads, features, mamba_head, mamba_bc,
+ *            capacity (slots), max_rows, max_runs, lowp (1 = bf16 linears)}.
+ * Allocates weights, the state store (capacity slots) and workspaces on the
+ * current device. Replaces ModelConfig/MultiTowerModel construction
+ * (model/inference_model.py:21-27, :103-117) and convert_linears
+ * (example_model.py:109-148). */
+int hk_engine_create(const int* cfg, int n_cfg, void** out_handle);
+
+/* Frees everything the engine owns (synchronises the device first). */
+int hk_engine_destroy(void* handle);
+
+/* Number of fp32 values weight slot (tower, layer, slot) expects; tower -1 /
+ * layer -1 addresses the shared output_proj, layer -1 the tower's input
+ * projections. */
+int hk_engine_param_numel(void* handle, int tower, int layer, int slot, int64_t* numel);
+
+/* Synchronous bind of one packed weight slot from host fp32 values; converted
+ * to bf16 on the device for CastLinear weights in bf16 mode, biases rounded
+ * through bf16 (example_model.py:82-90). Replaces load_state_dict +
+ * convert_linears (example_model.py:301-331). */
+int hk_engine_load_param(void* handle, int tower, int layer, int slot, const float* host,
+                         int64_t numel);
+
+/* Elements per slot of state leaf `leaf` of tower `tower`. */
+int hk_engine_state_numel(void* handle, int tower, int leaf, int64_t* per_slot);
+
+/* Stream-ordered copy of leaf `leaf` of block `layer` for slots
+ * [slot0, slot0+nslots) to (to_engine=0) or from (to_engine=1) the device
+ * buffer `buf`. Used to export/import state in the reference's
+ * init_state layout (model/inference_model.py:145-146). */
+int hk_engine_state_copy(void* handle, int tower, int layer, int leaf, int slot0, int nslots,
+                         void* buf, int to_engine, void* stream);
+
+/* Resets slots to init_state values (zeros; sLSTM running max -inf,
+ * model/xlstm.py:375); n < 0 resets every slot. */
+int hk_engine_reset_slots(void* handle, const int* slots_host, int n, void* stream);
+
+/* One tick: n_runs runs, run i = slot slot_ids_host[i] advanced over request
+ * rows run_off_host[i] .. run_off_host[i+1]-1 in order; runs sorted by
+ * non-increasing length, slots distinct. features_dev [n_rows, features]
+ * fp32, preds_dev [n_rows, 4] (one column per tower). Equivalent to the
+ * reference's rounds (example_model.py:885-899), each a masked forward +
+ * _blend_state (example_model.py:400-429, :907-949). Returns -3 when the
+ * tick exceeds max_rows / max_runs. */
+int hk_engine_tick(void* handle, const int* slot_ids_host, const int* run_off_host, int n_runs,
+                   const float* features_dev, float* preds_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

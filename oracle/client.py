@@ -1,0 +1,64 @@
+"""Oracle for process_batch (test infrastructure only).
+
+Restates NnInferenceClient.process_batch / run_round / _row_for
+(example_model.py:724-767, :769-905) literally: rounds of at most one request
+per symbol, each round one masked forward over every capacity row through
+oracle.model.forward, predictions read back per round.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import model as om
+
+
+class OracleClient:
+    def __init__(self, P: om.Params, cfg, capacity: int):
+        self.P, self.cfg, self.capacity = P, cfg, capacity
+        self.state = om.init_state(cfg, capacity, P.dtype)
+        self.symbol_to_idx = {}
+
+    def _row_for(self, symbol):
+        row = self.symbol_to_idx.get(symbol)
+        if row is not None:
+            return row
+        row = len(self.symbol_to_idx)
+        if row >= self.capacity:
+            return None
+        self.symbol_to_idx[symbol] = row
+        return row
+
+    @torch.inference_mode()
+    def process_batch(self, requests_by_symbol):
+        ids, preds = [], []
+        items = []
+        for symbol, reqs in requests_by_symbol.items():
+            if not reqs:
+                continue
+            row = self._row_for(symbol)
+            if row is None:
+                for r in reqs:
+                    ids.append(r.unique_id)
+                    preds.append([0.0] * 4)
+                continue
+            items.append((row, reqs))
+        if not items:
+            return ids, preds
+        for k in range(max(len(r) for _, r in items)):
+            idx, feats, batch = [], [], []
+            for row, reqs in items:
+                if len(reqs) > k:
+                    idx.append(row)
+                    feats.append(reqs[k].features)
+                    batch.append(reqs[k])
+            x = torch.zeros(self.capacity, self.cfg.num_features, dtype=self.P.dtype)
+            x[idx] = torch.as_tensor(np.asarray(feats), dtype=self.P.dtype)
+            mask = torch.zeros(self.capacity, dtype=torch.bool)
+            mask[idx] = True
+            out, self.state = om.forward(self.P, self.cfg, x, self.state, mask)
+            for r, row in zip(batch, idx):
+                ids.append(r.unique_id)
+                preds.append(out[row].to(torch.float64).tolist())
+        return ids, preds

@@ -1,0 +1,207 @@
+"""GPU parity of the ensemble engine (hackathon_amd.engine / .client) against
+the oracle and the reference's golden vectors.
+
+fp32 path: predictions within rtol 1e-5 of the reference with an absolute
+floor of 2e-5 for predictions near zero (|d| <= 2e-5 + 1e-5 |ref|); state
+leaves within the same bound scaled by 10 (the state accumulates 16 steps of
+reassociated sums). bf16 path (CastLinear semantics): mean squared error
+against the fp32 reference below 1e-3 of the predictions' mean square.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from hackathon_amd import spec, weights
+from oracle import model as om
+from oracle.client import OracleClient
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+P_RTOL, P_ATOL = 1e-5, 2e-5
+
+
+def _close(got, want, rtol, atol, what):
+    got, want = got.double().cpu(), want.double().cpu()
+    err = (got - want).abs()
+    bound = atol + rtol * want.abs()
+    worst = float((err - bound).max())
+    assert worst <= 0, f"{what}: max |d|={float(err.max()):.3e}, worst excess {worst:.3e}"
+
+
+@pytest.fixture(scope="module")
+def small_params():
+    return weights.generate(spec.SMALL, 0)
+
+
+def _engine(cfg, params, capacity, dtype="fp32", max_rows=256):
+    from hackathon_amd.engine import Engine
+
+    e = Engine(cfg, capacity=capacity, max_rows=max_rows, linear_dtype=dtype)
+    e.load_weights(params)
+    return e
+
+
+def test_small_fixture_masked_steps_fp32(dev, small_params):
+    fx = np.load(GOLDEN / "small.npz")
+    e = _engine(spec.SMALL, small_params, capacity=6)
+    for t in range(16):
+        x = torch.from_numpy(fx[f"x/{t}"]).to(dev)
+        mask = torch.from_numpy(fx[f"mask/{t}"])
+        preds = e.forward_masked(x, mask.to(dev))
+        torch.cuda.synchronize()
+        want = torch.from_numpy(fx[f"preds/{t}"])
+        _close(preds.cpu()[mask], want[mask], P_RTOL, P_ATOL, f"step {t} preds")
+        assert torch.all(preds.cpu()[~mask] == 0)
+    state = list(om.flatten(e.export_state(0, 6)))
+    for i, leaf in enumerate(state):
+        want = torch.from_numpy(fx[f"state/{i}"])
+        if want.dtype == torch.int32:
+            assert torch.equal(leaf.cpu(), want), f"leaf {i}"
+        else:
+            _close(leaf, want, 10 * P_RTOL, 10 * P_ATOL, f"state leaf {i} {tuple(want.shape)}")
+    e.close()
+
+
+def _requests(rng, symbols, n_req, uid0, F):
+    from hackathon_amd.client import PendingRequest
+
+    by_sym = {}
+    for i in range(n_req):
+        s = symbols[min(int(rng.zipf(1.3)) - 1, len(symbols) - 1)]
+        feats = np.clip(rng.standard_normal(F), -5, 5).astype(np.float32).tolist()
+        by_sym.setdefault(s, []).append(PendingRequest(uid0 + i, s, feats, 0.0))
+    by_sym["EMPTY"] = []
+    return by_sym
+
+
+def test_process_batch_matches_reference_rounds_fp32(dev, small_params):
+    from hackathon_amd.client import NnInferenceClient
+
+    cfg = spec.SMALL
+    capacity = 5
+    eng = _engine(cfg, small_params, capacity=capacity, max_rows=64)
+    client = NnInferenceClient(capacity, engine=eng)
+    oracle = OracleClient(om.Params(small_params), cfg, capacity)
+    rng = np.random.default_rng(7)
+    symbols = [f"SYM_{i:03d}" for i in range(7)]  # 7 symbols > 5 slots: overflow path
+    uid = 0
+    for batch in range(6):
+        reqs = _requests(rng, symbols, 40, uid, cfg.num_features)
+        uid += 40
+        got = client.process_batch(reqs)
+        want_ids, want_preds = oracle.process_batch(reqs)
+        assert got.unique_ids == want_ids, f"batch {batch}: response order differs"
+        assert client.symbol_to_idx == oracle.symbol_to_idx
+        _close(torch.tensor(got.predictions), torch.tensor(want_preds), P_RTOL, P_ATOL,
+               f"batch {batch} preds")
+    assert client.process_batch({}).unique_ids == []
+    eng.close()
+
+
+def test_long_runs_chunked_fp32(dev, small_params):
+    # More requests than max_rows: split into round-major chunks.
+    from hackathon_amd.client import NnInferenceClient, PendingRequest
+
+    cfg = spec.SMALL
+    eng = _engine(cfg, small_params, capacity=4, max_rows=16)
+    client = NnInferenceClient(4, engine=eng)
+    oracle = OracleClient(om.Params(small_params), cfg, 4)
+    rng = np.random.default_rng(3)
+    reqs = {}
+    uid = 0
+    for s, n in (("A", 30), ("B", 3), ("C", 11)):
+        reqs[s] = []
+        for _ in range(n):
+            reqs[s].append(PendingRequest(uid, s, rng.standard_normal(cfg.num_features).tolist()))
+            uid += 1
+    got = client.process_batch(reqs)
+    want_ids, want_preds = oracle.process_batch(reqs)
+    assert got.unique_ids == want_ids
+    _close(torch.tensor(got.predictions), torch.tensor(want_preds), P_RTOL, P_ATOL, "chunked")
+    eng.close()
+
+
+def test_bf16_path_mse(dev, small_params):
+    from hackathon_amd.client import NnInferenceClient
+
+    cfg = spec.SMALL
+    eng = _engine(cfg, small_params, capacity=8, dtype="bf16", max_rows=64)
+    client = NnInferenceClient(8, engine=eng)
+    ref32 = OracleClient(om.Params(small_params), cfg, 8)
+    ref16 = OracleClient(om.Params(small_params, lp="bf16"), cfg, 8)
+    rng = np.random.default_rng(11)
+    symbols = [f"S{i}" for i in range(8)]
+    se32 = se16 = ms = 0.0
+    for b in range(5):
+        reqs = _requests(rng, symbols, 48, 1000 * b, cfg.num_features)
+        got = torch.tensor(client.process_batch(reqs).predictions, dtype=torch.float64)
+        ids32, p32 = ref32.process_batch(reqs)
+        _, p16 = ref16.process_batch(reqs)
+        p32, p16 = torch.tensor(p32, dtype=torch.float64), torch.tensor(p16, dtype=torch.float64)
+        se32 += float(((got - p32) ** 2).sum())
+        se16 += float(((got - p16) ** 2).sum())
+        ms += float((p32 ** 2).sum())
+    print(f"bf16 path: MSE vs fp32 ref {se32:.3e}, vs bf16-emulated ref {se16:.3e}, signal {ms:.3e}")
+    assert se32 <= 1e-3 * ms
+    assert se16 <= se32 + 1e-12
+    eng.close()
+
+
+def test_default_dims_fp32_golden(dev):
+    # The reference's CPU-runnable configuration at default dims (4 symbols),
+    # first 4 steps, against the reference's own predictions.
+    fx = np.load(GOLDEN / "default.npz")
+    cfg = spec.DEFAULT
+    e = _engine(cfg, weights.generate(cfg, 0), capacity=4, max_rows=16)
+    for t in range(4):
+        x = torch.from_numpy(fx[f"x/{t}"]).to(dev)
+        preds = e.forward_masked(x, None)
+        torch.cuda.synchronize()
+        _close(preds, torch.from_numpy(fx[f"preds/{t}"]), P_RTOL, P_ATOL, f"default step {t}")
+    e.close()
+
+
+def test_state_roundtrip_and_reset(dev, small_params):
+    from hackathon_amd.engine import pack_runs
+
+    cfg = spec.SMALL
+    e = _engine(cfg, small_params, capacity=6)
+    runs, _ = pack_runs([3, 1], [4, 2])
+    feats = torch.randn(6, cfg.num_features, device=dev)
+    e.tick(runs, feats)
+    s1 = e.export_state(0, 6)
+    e.reset_slots([3])
+    s2 = e.export_state(0, 6)
+    fresh = om.init_state(cfg, 6)
+    for a, b, z in zip(om.flatten(s1), om.flatten(s2), om.flatten(fresh)):
+        assert torch.equal(b[3].cpu(), z[3])          # reset to init values
+        assert torch.equal(b[1].cpu(), a[1].cpu())    # other slots untouched
+    e.import_state(s1)
+    s3 = e.export_state(0, 6)
+    for a, b in zip(om.flatten(s1), om.flatten(s3)):
+        assert torch.equal(a, b)
+    e.close()
+
+
+def test_tick_validation(dev, small_params):
+    from hackathon_amd import _lib
+    from hackathon_amd.engine import Runs
+
+    cfg = spec.SMALL
+    e = _engine(cfg, small_params, capacity=4, max_rows=8)
+    f = torch.zeros(8, cfg.num_features, device=dev)
+    bad = [
+        Runs(np.array([0, 1], np.int32), np.array([0, 1, 3], np.int32)),   # not sorted
+        Runs(np.array([0, 0], np.int32), np.array([0, 2, 3], np.int32)),   # duplicate slot
+        Runs(np.array([5], np.int32), np.array([0, 1], np.int32)),         # slot out of range
+    ]
+    for r in bad:
+        with pytest.raises(_lib.HipLibraryError):
+            e.tick(r, f[: r.n_rows])
+    with pytest.raises(_lib.CapacityError):
+        big = torch.zeros(9, cfg.num_features, device=dev)
+        e.tick(Runs(np.array([0], np.int32), np.array([0, 9], np.int32)), big)
+    e.close()
