@@ -226,8 +226,18 @@ struct Engine {
   hipEvent_t stage_done[2] = {nullptr, nullptr};
   int stage_idx = 0;
   std::vector<char> seen;
+  // Optional per-launch timing of the matrix-state scans (kind 0 mLSTM,
+  // 1 Mamba2, 2 RetNet): event pairs recorded on the launch stream.
+  bool prof = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[3];
+  size_t prof_used[3] = {0, 0, 0};
 
   ~Engine() {
+    for (auto& v : prof_ev)
+      for (auto& pr : v) {
+        (void)hipEventDestroy(pr.first);
+        (void)hipEventDestroy(pr.second);
+      }
     for (auto& e : stage_done)
       if (e) (void)hipEventDestroy(e);
     if (h_stage) (void)hipHostFree(h_stage);
@@ -407,6 +417,23 @@ int block_linear(TowerWS& w, const float* x, int64_t ldx, const float* W, int bl
   } while (0)
 
 const Slot* S(Engine& e, int t, int l, int i) { return &e.slots[t][l + 1][i]; }
+
+// launch_mat_scan, bracketed by timing events when profiling is on.
+int timed_mat_scan(Engine& e, int kind, const MatScanDesc& m, hipStream_t s) {
+  if (!e.prof) return launch_mat_scan(m, s);
+  auto& v = e.prof_ev[kind];
+  if (e.prof_used[kind] == v.size()) {
+    std::pair<hipEvent_t, hipEvent_t> pr;
+    HK_CHECK_HIP(hipEventCreate(&pr.first));
+    HK_CHECK_HIP(hipEventCreate(&pr.second));
+    v.push_back(pr);
+  }
+  auto& pr = v[e.prof_used[kind]++];
+  HK_CHECK_HIP(hipEventRecord(pr.first, s));
+  int st = launch_mat_scan(m, s);
+  HK_CHECK_HIP(hipEventRecord(pr.second, s));
+  return st;
+}
 const float* F32(Engine& e, int t, int l, int i) {
   return static_cast<const float*>(e.slots[t][l + 1][i].ptr);
 }
@@ -468,7 +495,7 @@ int run_xlstm(Engine& e, int l, const Runs& r, const std::vector<int>& act, hipS
   m.out = w.NUM;
   m.out_row_stride = I;
   m.out_head_stride = d.hs_m;
-  HK_TRY(launch_mat_scan(m, s));
+  HK_TRY(timed_mat_scan(e, 0, m, s));
   HK_TRY(mlstm_post(w.NUM, w.DEN, d.nh, F32(e, kXLSTM, l, X_L_GN_W), F32(e, kXLSTM, l, X_L_GN_B),
                     F32(e, kXLSTM, l, X_L_SKIP), w.XMC, w.XMG + I, 2 * I, n, I, d.nh, w.HS.f,
                     w.HS.l, s));
@@ -517,7 +544,7 @@ int run_mamba2(Engine& e, int l, const Runs& r, hipStream_t s) {
   m.out = w.YS;
   m.out_row_stride = I;
   m.out_head_stride = d.hm;
-  HK_TRY(launch_mat_scan(m, s));
+  HK_TRY(timed_mat_scan(e, 1, m, s));
   HK_TRY(mamba2_post(w.YS, w.MXC, C, w.PROJ + C, W, F32(e, kMamba2, l, M_D),
                      F32(e, kMamba2, l, M_NORM), n, I, d.hm, w.YN.f, w.YN.l, s));
   HK_TRY(linear(e, w, w.YN, I, {S(e, kMamba2, l, M_OUT_W), nullptr}, n, H, I, 0, w.X.f, H, w.X.f,
@@ -558,7 +585,7 @@ int run_retnet(Engine& e, int l, const Runs& r, hipStream_t s) {
   m.out = w.O;
   m.out_row_stride = H;
   m.out_head_stride = d.hs_r;
-  HK_TRY(launch_mat_scan(m, s));
+  HK_TRY(timed_mat_scan(e, 2, m, s));
   HK_TRY(retnet_post(w.O, w.QKVG + 3 * H, 4 * H, n, H, d.hs_r, w.YO.f, w.YO.l, s));
   HK_TRY(linear(e, w, w.YO, H, {S(e, kRetNet, l, R_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f,
                 H, nullptr, 0, s));
@@ -846,6 +873,36 @@ int hk_engine_reset_slots(void* h, const int* slots_host, int n, void* stream) {
   return HK_OK;
 }
 
+// Per-launch timing of the matrix-state scans (kind 0 mLSTM, 1 Mamba2,
+// 2 RetNet). enable != 0 starts recording (and clears earlier records).
+int hk_engine_profile(void* h, int enable) {
+  HK_REQUIRE(h, "hk_engine_profile: null handle");
+  Engine& e = *static_cast<Engine*>(h);
+  e.prof = enable != 0;
+  for (auto& u : e.prof_used) u = 0;
+  return HK_OK;
+}
+
+// Waits for the recorded launches of `kind` and returns their count and
+// summed duration (ms); clears the records.
+int hk_engine_profile_read(void* h, int kind, int* count, double* total_ms) {
+  HK_REQUIRE(h && count && total_ms, "hk_engine_profile_read: null argument");
+  Engine& e = *static_cast<Engine*>(h);
+  HK_REQUIRE(kind >= 0 && kind < 3, "hk_engine_profile_read: bad kind %d", kind);
+  double tot = 0.0;
+  for (size_t i = 0; i < e.prof_used[kind]; ++i) {
+    auto& pr = e.prof_ev[kind][i];
+    HK_CHECK_HIP(hipEventSynchronize(pr.second));
+    float ms = 0.0f;
+    HK_CHECK_HIP(hipEventElapsedTime(&ms, pr.first, pr.second));
+    tot += ms;
+  }
+  *count = (int)e.prof_used[kind];
+  *total_ms = tot;
+  e.prof_used[kind] = 0;
+  return HK_OK;
+}
+
 // One tick. slot_ids_host[n_runs] and run_off_host[n_runs+1] describe runs
 // sorted by non-increasing length; features_dev is [n_rows, features] fp32
 // and preds_dev receives [n_rows, 4] (one column per tower), in row order.
@@ -864,6 +921,7 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   for (auto& tv : e.slots)
     for (auto& lv : tv)
       for (auto& sl : lv) HK_REQUIRE(sl.bound, "hk_engine_tick: weight %s not loaded", sl.def.name);
+  for (auto& sl : e.gslots) HK_REQUIRE(sl.bound, "hk_engine_tick: weight %s not loaded", sl.def.name);
   HK_REQUIRE(run_off_host[0] == 0, "hk_engine_tick: run_off[0] must be 0");
   const int n_rows = run_off_host[n_runs];
   if (n_rows > e.max_rows) {

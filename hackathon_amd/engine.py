@@ -35,7 +35,11 @@ _lib.register(
 _lib.register("hk_engine_reset_slots", c_int, [c_void_p, c_void_p, c_int, c_void_p])
 _lib.register("hk_engine_tick", c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p])
 
+_lib.register("hk_engine_profile", c_int, [c_void_p, c_int])
+_lib.register("hk_engine_profile_read", c_int, [c_void_p, c_int, ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_double)])
+
 LINEAR_DTYPES = ("bf16", "fp32")
+SCAN_KINDS = {"mlstm": 0, "mamba2": 1, "retnet": 2}
 
 # Slot order per tower type; must match the enums in csrc/engine.hip.
 _COMMON = ["norm1.weight", "norm2.weight", "mlp.fc1.weight", "mlp.fc1.bias", "mlp.fc2.weight", "mlp.fc2.bias"]
@@ -323,6 +327,18 @@ class Engine:
         )
         _lib.check(st, "hk_engine_tick")
         return preds
+
+    # -- measurement ---------------------------------------------------------------
+    def profile(self, enable: bool):
+        """Start (or stop) timing every matrix-state scan launch."""
+        _lib.check(_lib.lib().hk_engine_profile(self._h, 1 if enable else 0), "hk_engine_profile")
+
+    def profile_read(self, kind: str) -> tuple[int, float]:
+        """(launch count, summed ms) of the recorded launches of `kind`."""
+        n, ms = c_int(), ctypes.c_double()
+        _lib.check(_lib.lib().hk_engine_profile_read(self._h, SCAN_KINDS[kind], ctypes.byref(n), ctypes.byref(ms)),
+                   "hk_engine_profile_read")
+        return n.value, ms.value
 
     def forward_masked(self, x: torch.Tensor, mask: torch.Tensor | None) -> torch.Tensor:
         """MultiTowerModel.forward(x, state, mask) with the state held in the

@@ -129,6 +129,16 @@ int hk_engine_reset_slots(void* handle, const int* slots_host, int n, void* stre
 int hk_engine_tick(void* handle, const int* slot_ids_host, const int* run_off_host, int n_runs,
                    const float* features_dev, float* preds_dev, void* stream);
 
+/* Measurement hook (no reference counterpart; the reference times with CUDA
+ * events and torch.profiler, profile_step.py:337-397): when enabled, every
+ * matrix-state scan launch (kind 0 mLSTM, 1 Mamba2, 2 RetNet) is bracketed by
+ * HIP events on its stream. */
+int hk_engine_profile(void* handle, int enable);
+
+/* Waits for the recorded launches of `kind`, returns their count and summed
+ * duration in ms, and clears the records. */
+int hk_engine_profile_read(void* handle, int kind, int* count, double* total_ms);
+
 #ifdef __cplusplus
 }
 #endif
