@@ -148,8 +148,9 @@ def main() -> int:
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     n_launch, scan_ms = eng.profile_read("mlstm")
-    other = {k: eng.profile_read(k) for k in ("mamba2", "retnet")}
+    other = {k: eng.profile_read(k) for k in ("mamba2", "retnet", "slstm", "gemm")}
     eng.profile(False)
+    eng.check()
     assert torch.isfinite(preds[W:]).all(), "non-finite predictions"
 
     lat_us = np.array([a.elapsed_time(b) * 1000.0 for a, b in ev])
@@ -177,6 +178,10 @@ def main() -> int:
         n_l, ms = other[name]
         kernels[f"{name}_scan"] = {"launches": n_l, "avg_us": 1000.0 * ms / max(n_l, 1),
                                    "GB/s": b / (ms / 1000.0) / 1e9 if ms > 0 else 0.0}
+    for name in ("slstm", "gemm"):
+        n_l, ms = other[name]
+        kernels[name] = {"launches": n_l, "avg_us": 1000.0 * ms / max(n_l, 1),
+                         "ms_per_step": ms / K}
 
     line = {
         "metric": METRIC,

@@ -172,7 +172,7 @@ class NnInferenceClient:
         self._feat_dev[:n].copy_(self._feat_host[:n], non_blocking=True)
         self.engine.tick(runs, self._feat_dev[:n], self._preds_dev[:n])
         self._preds_host[:n].copy_(self._preds_dev[:n], non_blocking=True)
-        torch.cuda.current_stream(self.device).synchronize()
+        self.engine.check()  # synchronises; raises if an in-kernel barrier timed out
         preds = self._preds_host[:n].numpy().astype(float)
         for k in range(max(lengths)):
             for i, (_, reqs) in enumerate(items):

@@ -17,6 +17,7 @@
 //   pred[tower] = output_proj(x)                          (shared weights)
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -222,15 +223,20 @@ struct Engine {
   Act FE;
   int* d_slots = nullptr;
   int* d_off = nullptr;
-  int* h_stage = nullptr;  // pinned [2][max_runs * 2 + 1]
+  int* d_act = nullptr;      // [max_rows]: runs active at each step
+  int* d_counters = nullptr; // [16]: sLSTM step-barrier counters
+  int* d_err = nullptr;      // [1]: set by a kernel whose barrier timed out
+  uint64_t* d_trace = nullptr;  // HK_TRACE_SLSTM: per-step stamps of layer 0's sLSTM
+  int* h_stage = nullptr;    // pinned [2][stage_ints()]
+  int stage_ints() const { return 2 * max_runs + 1 + max_rows; }
   hipEvent_t stage_done[2] = {nullptr, nullptr};
   int stage_idx = 0;
   std::vector<char> seen;
   // Optional per-launch timing of the matrix-state scans (kind 0 mLSTM,
   // 1 Mamba2, 2 RetNet): event pairs recorded on the launch stream.
   bool prof = false;
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[3];
-  size_t prof_used[3] = {0, 0, 0};
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[5];
+  size_t prof_used[5] = {0, 0, 0, 0, 0};
 
   ~Engine() {
     for (auto& v : prof_ev)
@@ -346,11 +352,39 @@ int build_workspace(Engine& e) {
   if (any_null(e.FE, false, e.lowp)) return HK_ERR_HIP;
   e.d_slots = static_cast<int*>(e.alloc_bytes((size_t)e.max_runs * 4));
   e.d_off = static_cast<int*>(e.alloc_bytes((size_t)(e.max_runs + 1) * 4));
-  if (!e.d_slots || !e.d_off) return HK_ERR_HIP;
-  HK_CHECK_HIP(hipHostMalloc((void**)&e.h_stage, (size_t)2 * (2 * e.max_runs + 1) * 4,
+  e.d_act = static_cast<int*>(e.alloc_bytes((size_t)e.max_rows * 4));
+  e.d_counters = static_cast<int*>(e.alloc_bytes(16 * 4));
+  e.d_err = static_cast<int*>(e.alloc_bytes(4));
+  if (!e.d_slots || !e.d_off || !e.d_act || !e.d_counters || !e.d_err) return HK_ERR_HIP;
+  HK_CHECK_HIP(hipMemset(e.d_err, 0, 4));
+  if (std::getenv("HK_TRACE_SLSTM")) {
+    e.d_trace = static_cast<uint64_t*>(e.alloc_bytes((size_t)e.max_rows * 8 * 8));
+    if (!e.d_trace) return HK_ERR_HIP;
+  }
+  HK_CHECK_HIP(hipMemset(e.d_counters, 0, 16 * 4));
+  HK_CHECK_HIP(hipHostMalloc((void**)&e.h_stage, (size_t)2 * e.stage_ints() * 4,
                              hipHostMallocDefault));
   for (auto& ev : e.stage_done) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   return HK_OK;
+}
+
+// Runs `fn` bracketed by timing events of `kind` when profiling is on
+// (0 mLSTM scan, 1 Mamba2 scan, 2 RetNet scan, 3 sLSTM recurrence, 4 GEMM).
+template <typename Fn>
+int timed(Engine& e, int kind, hipStream_t s, Fn&& fn) {
+  if (!e.prof) return fn();
+  auto& v = e.prof_ev[kind];
+  if (e.prof_used[kind] == v.size()) {
+    std::pair<hipEvent_t, hipEvent_t> pr;
+    HK_CHECK_HIP(hipEventCreate(&pr.first));
+    HK_CHECK_HIP(hipEventCreate(&pr.second));
+    v.push_back(pr);
+  }
+  auto& pr = v[e.prof_used[kind]++];
+  HK_CHECK_HIP(hipEventRecord(pr.first, s));
+  int st = fn();
+  HK_CHECK_HIP(hipEventRecord(pr.second, s));
+  return st;
 }
 
 // ---- one linear layer --------------------------------------------------------
@@ -384,12 +418,12 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
   g.ep.ldo = ldo;
   g.ep.out_lp = out_lp;
   g.ep.ldl = ldl;
-  return gemm(g, w.gemm_ws, s);
+  return timed(e, 4, s, [&] { return gemm(g, w.gemm_ws, s); });
 }
 
 // Block-diagonal fp32 product (BlockLinear, model/modules.py:71-79):
 // out[:, b*bs + k] = sum_h x[:, b*bs + h] * W[b][k][h], for b < blocks.
-int block_linear(TowerWS& w, const float* x, int64_t ldx, const float* W, int blocks, int bs,
+int block_linear(Engine& e, TowerWS& w, const float* x, int64_t ldx, const float* W, int blocks, int bs,
                  int M, const float* bias, float* out, int64_t ldo, hipStream_t s) {
   GemmArgs g;
   g.type = GemmType::kF32;
@@ -407,7 +441,7 @@ int block_linear(TowerWS& w, const float* x, int64_t ldx, const float* W, int bl
   g.ep.bias = bias;
   g.ep.out = out;
   g.ep.ldo = ldo;
-  return gemm(g, w.gemm_ws, s);
+  return timed(e, 4, s, [&] { return gemm(g, w.gemm_ws, s); });
 }
 
 #define HK_TRY(expr)          \
@@ -418,21 +452,8 @@ int block_linear(TowerWS& w, const float* x, int64_t ldx, const float* W, int bl
 
 const Slot* S(Engine& e, int t, int l, int i) { return &e.slots[t][l + 1][i]; }
 
-// launch_mat_scan, bracketed by timing events when profiling is on.
 int timed_mat_scan(Engine& e, int kind, const MatScanDesc& m, hipStream_t s) {
-  if (!e.prof) return launch_mat_scan(m, s);
-  auto& v = e.prof_ev[kind];
-  if (e.prof_used[kind] == v.size()) {
-    std::pair<hipEvent_t, hipEvent_t> pr;
-    HK_CHECK_HIP(hipEventCreate(&pr.first));
-    HK_CHECK_HIP(hipEventCreate(&pr.second));
-    v.push_back(pr);
-  }
-  auto& pr = v[e.prof_used[kind]++];
-  HK_CHECK_HIP(hipEventRecord(pr.first, s));
-  int st = launch_mat_scan(m, s);
-  HK_CHECK_HIP(hipEventRecord(pr.second, s));
-  return st;
+  return timed(e, kind, s, [&] { return launch_mat_scan(m, s); });
 }
 const float* F32(Engine& e, int t, int l, int i) {
   return static_cast<const float*>(e.slots[t][l + 1][i].ptr);
@@ -452,15 +473,24 @@ int run_xlstm(Engine& e, int l, const Runs& r, const std::vector<int>& act, hipS
   const float* win = F32(e, kXLSTM, l, X_S_IN_W);
   for (int g = 0; g < 4; ++g) {  // i, f from the conv path; z, o from LN(x)
     const float* src = g < 2 ? w.XCA : w.XN;
-    HK_TRY(block_linear(w, src, H, win + (int64_t)g * H * d.bs_s, d.nh_s, d.bs_s, n, nullptr,
+    HK_TRY(block_linear(e, w, src, H, win + (int64_t)g * H * d.bs_s, d.nh_s, d.bs_s, n, nullptr,
                         w.GIN + (int64_t)g * H, 4 * H, s));
   }
-  for (size_t t = 0; t < act.size(); ++t) {
-    HK_TRY(slstm_round(r, (int)t, act[t], w.GIN, H, d.nh_s, F32(e, kXLSTM, l, X_S_ST_W),
-                       F32(e, kXLSTM, l, X_S_ST_B), st[XS_S_H], st[XS_S_C], st[XS_S_N],
-                       st[XS_S_M], w.SY, s));
+  if (slstm_persist_supported(H, d.nh_s)) {
+    HK_TRY(timed(e, 3, s, [&] {
+      return slstm_persist(r, e.d_act, (int)act.size(), w.GIN, H, d.nh_s,
+                           F32(e, kXLSTM, l, X_S_ST_W), F32(e, kXLSTM, l, X_S_ST_B), st[XS_S_H],
+                           st[XS_S_C], st[XS_S_N], st[XS_S_M], w.SY, e.d_counters, e.d_err,
+                           l == 0 ? e.d_trace : nullptr, s);
+    }));
+  } else {
+    for (size_t t = 0; t < act.size(); ++t) {
+      HK_TRY(slstm_round(r, (int)t, act[t], w.GIN, H, d.nh_s, F32(e, kXLSTM, l, X_S_ST_W),
+                         F32(e, kXLSTM, l, X_S_ST_B), st[XS_S_H], st[XS_S_C], st[XS_S_N],
+                         st[XS_S_M], w.SY, s));
+    }
+    HK_TRY(slstm_final(r, w.SY, H, st[XS_S_H], s));
   }
-  HK_TRY(slstm_final(r, w.SY, H, st[XS_S_H], s));
   HK_TRY(slstm_post(w.SY, w.A.f, F32(e, kXLSTM, l, X_S_GN_W), F32(e, kXLSTM, l, X_S_GN_B), d.nh_s,
                     F32(e, kXLSTM, l, X_L_NORM), n, H, w.X1, w.XN2.f, w.XN2.l, s));
   // mLSTM block (model/xlstm.py:298-325).
@@ -606,7 +636,7 @@ int run_hawk(Engine& e, int l, const Runs& r, hipStream_t s) {
                    F32(e, kHawk, l, K_CONV_B), 0, w.KXC, H, s));
   const float* gw = F32(e, kHawk, l, K_GATES_W);
   for (int g = 0; g < 2; ++g)
-    HK_TRY(block_linear(w, w.KXC, H, gw + (int64_t)g * H * d.bs_h, d.nb_h, d.bs_h, n, nullptr,
+    HK_TRY(block_linear(e, w, w.KXC, H, gw + (int64_t)g * H * d.bs_h, d.nb_h, d.bs_h, n, nullptr,
                         w.GATES + (int64_t)g * H, 2 * H, s));
   HK_TRY(rglru_scan(r, w.KXC, w.GATES, w.GATES + H, 2 * H, w.GRP, 2 * H, F32(e, kHawk, l, K_A),
                     8.0f, H, st[KS_H], w.GH.f, w.GH.l, s));
@@ -873,8 +903,50 @@ int hk_engine_reset_slots(void* h, const int* slots_host, int n, void* stream) {
   return HK_OK;
 }
 
-// Per-launch timing of the matrix-state scans (kind 0 mLSTM, 1 Mamba2,
-// 2 RetNet). enable != 0 starts recording (and clears earlier records).
+// Synchronises the device and reports a step barrier that timed out in any
+// earlier tick (then returns -2 and clears the flag).
+int hk_engine_check(void* h) {
+  HK_REQUIRE(h, "hk_engine_check: null handle");
+  Engine& e = *static_cast<Engine*>(h);
+  HK_CHECK_HIP(hipDeviceSynchronize());
+  int flag = 0;
+  HK_CHECK_HIP(hipMemcpy(&flag, e.d_err, 4, hipMemcpyDeviceToHost));
+  if (e.d_trace) {
+    // Phases of the last tick's layer-0 sLSTM steps in microseconds
+    // (s_memrealtime runs at 100 MHz); the first chunk's stage / dot / cell.
+    std::vector<uint64_t> tr((size_t)e.max_rows * 8);
+    HK_CHECK_HIP(hipMemcpy(tr.data(), e.d_trace, tr.size() * 8, hipMemcpyDeviceToHost));
+    double tot[6] = {0, 0, 0, 0, 0, 0};
+    int n = 0;
+    for (int t = 0; t < e.max_rows && tr[t * 8 + 6] > tr[t * 8 + 0]; ++t, ++n) {
+      double ph[6];
+      for (int k = 0; k < 6; ++k) ph[k] = (double)(tr[t * 8 + k + 1] - tr[t * 8 + k]) * 0.01;
+      for (int k = 0; k < 6; ++k) tot[k] += ph[k];
+      if (t < 3 || t % 10 == 0)
+        fprintf(stderr,
+                "slstm step %d: stage %.2f dot %.2f cell %.2f rest-chunks %.2f wait %.2f "
+                "barrier %.2f us\n", t, ph[0], ph[1], ph[2], ph[3], ph[4], ph[5]);
+    }
+    fprintf(stderr,
+            "slstm %d steps: stage %.1f dot %.1f cell %.1f rest-chunks %.1f wait %.1f "
+            "barrier %.1f us\n", n, tot[0], tot[1], tot[2], tot[3], tot[4], tot[5]);
+    HK_CHECK_HIP(hipMemset(e.d_trace, 0, tr.size() * 8));
+  }
+  if (flag) {
+    HK_CHECK_HIP(hipMemset(e.d_err, 0, 4));
+  if (std::getenv("HK_TRACE_SLSTM")) {
+    e.d_trace = static_cast<uint64_t*>(e.alloc_bytes((size_t)e.max_rows * 8 * 8));
+    if (!e.d_trace) return HK_ERR_HIP;
+  }
+    hk::set_error("hk_engine_check: a kernel step barrier timed out (results invalid)");
+    return HK_ERR_HIP;
+  }
+  return HK_OK;
+}
+
+// Per-launch timing (kind 0 mLSTM scan, 1 Mamba2 scan, 2 RetNet scan,
+// 3 sLSTM recurrence, 4 GEMM). enable != 0 starts recording (and clears
+// earlier records).
 int hk_engine_profile(void* h, int enable) {
   HK_REQUIRE(h, "hk_engine_profile: null handle");
   Engine& e = *static_cast<Engine*>(h);
@@ -888,7 +960,7 @@ int hk_engine_profile(void* h, int enable) {
 int hk_engine_profile_read(void* h, int kind, int* count, double* total_ms) {
   HK_REQUIRE(h && count && total_ms, "hk_engine_profile_read: null argument");
   Engine& e = *static_cast<Engine*>(h);
-  HK_REQUIRE(kind >= 0 && kind < 3, "hk_engine_profile_read: bad kind %d", kind);
+  HK_REQUIRE(kind >= 0 && kind < 5, "hk_engine_profile_read: bad kind %d", kind);
   double tot = 0.0;
   for (size_t i = 0; i < e.prof_used[kind]; ++i) {
     auto& pr = e.prof_ev[kind][i];
@@ -953,20 +1025,24 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   const int k = e.stage_idx;
   e.stage_idx ^= 1;
   HK_CHECK_HIP(hipEventSynchronize(e.stage_done[k]));
-  int* stage = e.h_stage + (size_t)k * (2 * e.max_runs + 1);
+  std::vector<int> act(run_off_host[1] - run_off_host[0]);
+  {
+    int c = n_runs;
+    for (size_t t = 0; t < act.size(); ++t) {
+      while (c > 0 && run_off_host[c] - run_off_host[c - 1] <= (int)t) --c;
+      act[t] = c;
+    }
+  }
+  int* stage = e.h_stage + (size_t)k * e.stage_ints();
   std::memcpy(stage, slot_ids_host, (size_t)n_runs * 4);
   std::memcpy(stage + n_runs, run_off_host, (size_t)(n_runs + 1) * 4);
+  std::memcpy(stage + 2 * n_runs + 1, act.data(), act.size() * 4);
   HK_CHECK_HIP(hipMemcpyAsync(e.d_slots, stage, (size_t)n_runs * 4, hipMemcpyHostToDevice, s));
   HK_CHECK_HIP(
       hipMemcpyAsync(e.d_off, stage + n_runs, (size_t)(n_runs + 1) * 4, hipMemcpyHostToDevice, s));
+  HK_CHECK_HIP(hipMemcpyAsync(e.d_act, stage + 2 * n_runs + 1, act.size() * 4,
+                              hipMemcpyHostToDevice, s));
   HK_CHECK_HIP(hipEventRecord(e.stage_done[k], s));
-
-  std::vector<int> act(run_off_host[1] - run_off_host[0]);
-  for (size_t t = 0; t < act.size(); ++t) {
-    int c = 0;
-    while (c < n_runs && run_off_host[c + 1] - run_off_host[c] > (int)t) ++c;
-    act[t] = c;
-  }
   hk::Runs r{e.d_slots, e.d_off, n_runs, n_rows};
   HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, s));
   for (int t = 0; t < hk::kTowers; ++t) HK_TRY(hk::run_tower(e, t, r, act, preds_dev, s));

@@ -222,6 +222,269 @@ __global__ __launch_bounds__(256) void slstm_round_kernel(
   y[(int64_t)row * hidden + col] = og * cn / (nn + 1e-6f);
 }
 
+// Persistent sLSTM recurrence for a whole tick: one cooperative launch per
+// layer instead of one launch per step. Work-group g (512 threads, 8 waves)
+// owns 16 units of one head: 64 gate rows (unit*4 + gate) x hs inputs of the
+// recurrent weights, held in VGPRs for every step as fp32 MFMA A fragments
+// (wave = (16-row tile, k half)). Step t, per chunk of up to 16 runs: stage
+// h_{t-1} in LDS, G[64 rows x 16 runs] = W . H on v_mfma_f32_16x16x4_f32
+// (fp32 products and sums), add the two k halves through LDS, then the cell
+// update, one (run, unit) per thread. The head's work-groups then meet at a
+// counter barrier before step t+1 reads the h_t they wrote. h_t crosses
+// work-groups (and XCDs) only through agent-scope atomic stores and loads,
+// which are coherent without the L2-wide writeback and invalidate that an
+// agent-scope fence costs; each wave waits for its stores to complete before
+// its work-group arrives at the counter. Every spin is bounded: on timeout
+// an error flag is set and every wave leaves.
+constexpr int kPersistRuns = 16;   // runs per chunk = one MFMA n-tile
+constexpr int kPersistThreads = 512;
+constexpr int kSpinLimit = 1 << 22;
+
+struct SlstmPersistArgs {
+  const int* slot_ids;
+  const int* run_off;
+  const int* act;      // act[t] = runs with length > t (runs sorted by length)
+  int n_rounds;
+  int n_runs;
+  const float* gin;    // [rows][4*hidden] input-side gate pre-activations
+  int hidden;
+  int heads;
+  const float* w_state;  // [4][heads][hs][hs]
+  const float* b_state;  // [4][hidden]
+  float* h_state;
+  float* c_state;
+  float* n_state;
+  float* m_state;
+  float* y;            // [rows][hidden]
+  int* counters;       // [heads], zero at launch
+  int* err;            // set to 1 on a barrier timeout
+  uint64_t* trace;     // optional [n_rounds][8] wall-clock stamps of work-group 0
+};
+
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+template <int HS>
+__global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPersistArgs a) {
+  extern __shared__ float smem[];
+  constexpr int hs = HS;
+  constexpr int wpg = hs / 16;      // work-groups per head
+  constexpr int NT = kPersistThreads;
+  constexpr int PAD = hs + 8;       // LDS row stride of h (spreads runs over banks)
+  constexpr int KH = hs / 2;        // k per wave
+  constexpr int KG = KH / 16;       // groups of 4 MFMA k-steps per wave
+  float* hbuf = smem;                               // [16][PAD]
+  float* gsum = hbuf + kPersistRuns * PAD;          // [16 runs][64 rows]
+  float* xbuf = gsum + kPersistRuns * 64;           // [16 runs][64 rows], k-half 1
+  __shared__ int s_abort;
+  const int H = a.hidden;
+  const int head = blockIdx.x / wpg;
+  const int u0 = (blockIdx.x % wpg) * 16;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int mt = wave & 3;          // rows 16*mt .. +15
+  const int kh = wave >> 2;         // k half
+  const int fr = lane & 15;         // A row / B column (run) / C column
+  const int fk = lane >> 4;         // k sub-group / C row group
+
+  // A fragments: for k-step group g and step c, this lane covers
+  // k = kh*KH + 16*g + 4*fk + c of row 16*mt + fr (A and B use the same map).
+  float w[4 * KG];
+  {
+    const int row = 16 * mt + fr;
+    const int unit = row >> 2, gate = row & 3;
+    const float* src = a.w_state + (((int64_t)gate * a.heads + head) * hs + (u0 + unit)) * hs +
+                       kh * KH + 4 * fk;
+#pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      const float4 v = *reinterpret_cast<const float4*>(src + 16 * g);
+      w[4 * g + 0] = v.x;
+      w[4 * g + 1] = v.y;
+      w[4 * g + 2] = v.z;
+      w[4 * g + 3] = v.w;
+    }
+  }
+  // Cell-update role (threads 0..255): unit uu, run jr of each chunk.
+  const int uu = tid & 15;
+  const int jr = tid >> 4;
+  const int ccol = head * hs + u0 + uu;
+  float bi = 0.f, bf = 0.f, bz = 0.f, bo = 0.f;
+  if (tid < 256) {
+    bi = a.b_state[ccol];
+    bf = a.b_state[H + ccol];
+    bz = a.b_state[2 * H + ccol];
+    bo = a.b_state[3 * H + ccol];
+  }
+  if (tid == 0) s_abort = 0;
+  __syncthreads();
+
+  const bool tr = a.trace != nullptr && blockIdx.x == 0 && tid == 0;
+  for (int t = 0; t < a.n_rounds; ++t) {
+    const int na = a.act[t];
+    if (tr) a.trace[t * 8 + 0] = __builtin_amdgcn_s_memrealtime();
+    for (int c0 = 0; c0 < na; c0 += kPersistRuns) {
+      const int nj = min(kPersistRuns, na - c0);
+      // Operands of this thread's cell update, fetched before the h staging
+      // so their latency overlaps it.
+      const bool cell = tid < 256 && jr < nj;
+      float pi = 0.f, pf = 0.f, pz = 0.f, po = 0.f, pc = 0.f, pn = 0.f, pm = 0.f;
+      int64_t psi = 0, prow = 0;
+      if (cell) {
+        const int run = c0 + jr;
+        const int row = a.run_off[run] + t;
+        const float* gr = a.gin + (int64_t)row * 4 * H;
+        psi = (int64_t)a.slot_ids[run] * H + ccol;
+        prow = row;
+        pi = gr[ccol];
+        pf = gr[H + ccol];
+        pz = gr[2 * H + ccol];
+        po = gr[3 * H + ccol];
+        pc = a.c_state[psi];
+        pn = a.n_state[psi];
+        pm = a.m_state[psi];
+      }
+      // Stage h_{t-1} of the chunk's runs into hbuf[j][k]. Loads are
+      // unconditional (index clamped to a valid element) so the staging
+      // registers never go to scratch; only the LDS stores are predicated.
+      if (t == 0) {
+        // from the state store (written before this launch)
+        constexpr int vph = hs / 4;
+        constexpr int kV = (kPersistRuns * vph + NT - 1) / NT;
+        const int nvec = nj * vph;
+        float4 v[kV];
+#pragma unroll
+        for (int u = 0; u < kV; ++u) {
+          const int i = min(u * NT + tid, nvec - 1);
+          const int j = i / vph;
+          v[u] = reinterpret_cast<const float4*>(a.h_state + (int64_t)a.slot_ids[c0 + j] * H +
+                                                 head * hs)[i - j * vph];
+        }
+#pragma unroll
+        for (int u = 0; u < kV; ++u) {
+          const int i = u * NT + tid;
+          if (i < nvec) {
+            const int j = i / vph;
+            *reinterpret_cast<float4*>(hbuf + j * PAD + 4 * (i - j * vph)) = v[u];
+          }
+        }
+      } else {
+        // written by the head's work-groups this launch: coherent loads
+        constexpr int kS = (kPersistRuns * hs + NT - 1) / NT;
+        const int nel = nj * hs;
+        float v[kS];
+#pragma unroll
+        for (int u = 0; u < kS; ++u) {
+          const int i = min(u * NT + tid, nel - 1);
+          const int j = i / hs;
+          v[u] = __hip_atomic_load(
+              a.y + (int64_t)(a.run_off[c0 + j] + t - 1) * H + head * hs + (i - j * hs),
+              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < kS; ++u) {
+          const int i = u * NT + tid;
+          if (i < nel) {
+            const int j = i / hs;
+            hbuf[j * PAD + (i - j * hs)] = v[u];
+          }
+        }
+      }
+      __syncthreads();
+      if (tr && c0 == 0) a.trace[t * 8 + 1] = __builtin_amdgcn_s_memrealtime();
+      {
+        // Columns fr >= nj read stale LDS rows; their results are dropped.
+        // Four independent accumulator chains (one per step c of a group),
+        // summed at the end, so consecutive MFMAs do not wait on each other.
+        floatx4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, a2 = a0, a3 = a0;
+        const float* hb = hbuf + fr * PAD + kh * KH + 4 * fk;
+#pragma unroll
+        for (int g = 0; g < KG; ++g) {
+          const float4 hv = *reinterpret_cast<const float4*>(hb + 16 * g);
+          a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * g + 0], hv.x, a0, 0, 0, 0);
+          a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * g + 1], hv.y, a1, 0, 0, 0);
+          a2 = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * g + 2], hv.z, a2, 0, 0, 0);
+          a3 = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * g + 3], hv.w, a3, 0, 0, 0);
+        }
+        const floatx4_t acc = (a0 + a1) + (a2 + a3);
+        // acc[e] = G[row 16*mt + 4*fk + e][run fr], partial over this k half.
+        if (kh == 1) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xbuf[fr * 64 + 16 * mt + 4 * fk + e] = acc[e];
+        }
+        __syncthreads();
+        if (kh == 0) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 16 * mt + 4 * fk + e;
+            gsum[fr * 64 + r] = acc[e] + xbuf[fr * 64 + r];
+          }
+        }
+      }
+      __syncthreads();
+      if (tr && c0 == 0) a.trace[t * 8 + 2] = __builtin_amdgcn_s_memrealtime();
+      if (cell) {
+        const float* gs = gsum + jr * 64 + uu * 4;
+        const float ip = pi + (gs[0] + bi);
+        const float fp = pf + (gs[1] + bf);
+        const float zp = pz + (gs[2] + bz);
+        const float op = po + (gs[3] + bo);
+        const float lfm = pm + logsigmoid(fp);
+        const float mn = fmaxf(ip, lfm);
+        const float og = sigmoid(op);
+        const float ig = expf(ip - mn);
+        const float fg = expf(lfm - mn);
+        const float cn = fg * pc + ig * tanhf(zp);
+        const float nn = fg * pn + ig;
+        a.c_state[psi] = cn;
+        a.n_state[psi] = nn;
+        a.m_state[psi] = mn;
+        // h_t is published with a coherent (agent-scope) store, so the head's
+        // other work-groups can read it without a cache-wide flush.
+        __hip_atomic_store(a.y + prow * H + ccol, og * cn / (nn + 1e-6f), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (tr && c0 == 0) a.trace[t * 8 + 3] = __builtin_amdgcn_s_memrealtime();
+      __syncthreads();
+    }
+    // Head barrier: every wave waits for its h_t stores to complete, then one
+    // arrival per work-group; wait for the head's other work-groups.
+    if (tr) a.trace[t * 8 + 4] = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tr) a.trace[t * 8 + 5] = __builtin_amdgcn_s_memrealtime();
+    if (tid == 0) {
+      __hip_atomic_fetch_add(a.counters + head, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int target = (t + 1) * wpg;
+      int spins = 0;
+      while (__hip_atomic_load(a.counters + head, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+             target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > kSpinLimit ||
+            __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+          __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          s_abort = 1;
+          break;
+        }
+      }
+    }
+    __syncthreads();
+    if (tr) a.trace[t * 8 + 6] = __builtin_amdgcn_s_memrealtime();
+    if (s_abort) return;
+  }
+  // h_state <- h of each run's last step, for this work-group's units.
+  for (int i = tid; i < a.n_runs * 16; i += NT) {
+    const int run = i >> 4;
+    const int col = head * hs + u0 + (i & 15);
+    const int last = a.run_off[run + 1] - 1;
+    a.h_state[(int64_t)a.slot_ids[run] * H + col] = a.y[(int64_t)last * H + col];
+  }
+}
+
+__global__ void zero_i32_kernel(int* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 __global__ void slstm_final_kernel(const int* __restrict__ slot_ids,
                                    const int* __restrict__ run_off, const float* __restrict__ y,
                                    int hidden, float* __restrict__ h_state) {
@@ -343,6 +606,42 @@ int slstm_round(const Runs& r, int step, int n_active, const float* gin, int hid
                      n_active, gin, hidden, hs, w_state, b_state, h_state, c_state, n_state,
                      m_state, y);
   HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+bool slstm_persist_supported(int hidden, int heads) {
+  const int hs = hidden / heads;
+  return hs * heads == hidden && (hs == 32 || hs == 64 || hs == 128 || hs == 256 || hs == 512);
+}
+
+int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* gin, int hidden,
+                  int heads, const float* w_state, const float* b_state, float* h_state,
+                  float* c_state, float* n_state, float* m_state, float* y, int* counters,
+                  int* err, uint64_t* trace, hipStream_t s) {
+  if (r.n_runs == 0 || n_rounds == 0) return HK_OK;
+  HK_REQUIRE(slstm_persist_supported(hidden, heads), "slstm_persist: head size unsupported");
+  HK_REQUIRE(heads <= 16, "slstm_persist: at most 16 heads (barrier counters)");
+  const int hs = hidden / heads;
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, counters, heads);
+  HK_LAUNCH_CHECK();
+  SlstmPersistArgs a{r.slot_ids, r.run_off, act_dev, n_rounds, r.n_runs, gin, hidden, heads,
+                     w_state, b_state, h_state, c_state, n_state, m_state, y, counters, err,
+                     trace};
+  void* args[] = {&a};
+  const size_t smem = (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float);
+  const dim3 grid(heads * (hs / 16)), block(kPersistThreads);
+  hipError_t e;
+  switch (hs) {
+    case 32: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<32>, grid, block, args, smem, s); break;
+    case 64: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<64>, grid, block, args, smem, s); break;
+    case 128: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<128>, grid, block, args, smem, s); break;
+    case 256: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<256>, grid, block, args, smem, s); break;
+    default: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<512>, grid, block, args, smem, s); break;
+  }
+  if (e != hipSuccess) {
+    set_error("slstm_persist: cooperative launch failed: %s", hipGetErrorString(e));
+    return HK_ERR_HIP;
+  }
   return HK_OK;
 }
 

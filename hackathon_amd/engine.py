@@ -35,11 +35,12 @@ _lib.register(
 _lib.register("hk_engine_reset_slots", c_int, [c_void_p, c_void_p, c_int, c_void_p])
 _lib.register("hk_engine_tick", c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p])
 
+_lib.register("hk_engine_check", c_int, [c_void_p])
 _lib.register("hk_engine_profile", c_int, [c_void_p, c_int])
 _lib.register("hk_engine_profile_read", c_int, [c_void_p, c_int, ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_double)])
 
 LINEAR_DTYPES = ("bf16", "fp32")
-SCAN_KINDS = {"mlstm": 0, "mamba2": 1, "retnet": 2}
+SCAN_KINDS = {"mlstm": 0, "mamba2": 1, "retnet": 2, "slstm": 3, "gemm": 4}
 
 # Slot order per tower type; must match the enums in csrc/engine.hip.
 _COMMON = ["norm1.weight", "norm2.weight", "mlp.fc1.weight", "mlp.fc1.bias", "mlp.fc2.weight", "mlp.fc2.bias"]
@@ -327,6 +328,10 @@ class Engine:
         )
         _lib.check(st, "hk_engine_tick")
         return preds
+
+    def check(self):
+        """Synchronise and raise if any in-kernel step barrier timed out."""
+        _lib.check(_lib.lib().hk_engine_check(self._h), "hk_engine_check")
 
     # -- measurement ---------------------------------------------------------------
     def profile(self, enable: bool):

@@ -129,10 +129,15 @@ int hk_engine_reset_slots(void* handle, const int* slots_host, int n, void* stre
 int hk_engine_tick(void* handle, const int* slot_ids_host, const int* run_off_host, int n_runs,
                    const float* features_dev, float* preds_dev, void* stream);
 
+/* Synchronises the device; returns -2 if a persistent kernel's step barrier
+ * timed out in an earlier tick (its results are then invalid), else 0. No
+ * reference counterpart: the reference has no in-kernel barriers. */
+int hk_engine_check(void* handle);
+
 /* Measurement hook (no reference counterpart; the reference times with CUDA
  * events and torch.profiler, profile_step.py:337-397): when enabled, every
- * matrix-state scan launch (kind 0 mLSTM, 1 Mamba2, 2 RetNet) is bracketed by
- * HIP events on its stream. */
+ * launch of kind 0 mLSTM scan, 1 Mamba2 scan, 2 RetNet scan, 3 sLSTM
+ * recurrence, 4 projection GEMM is bracketed by HIP events on its stream. */
 int hk_engine_profile(void* handle, int enable);
 
 /* Waits for the recorded launches of `kind`, returns their count and summed

@@ -57,6 +57,7 @@ def test_small_fixture_masked_steps_fp32(dev, small_params):
         want = torch.from_numpy(fx[f"preds/{t}"])
         _close(preds.cpu()[mask], want[mask], P_RTOL, P_ATOL, f"step {t} preds")
         assert torch.all(preds.cpu()[~mask] == 0)
+    e.check()
     state = list(om.flatten(e.export_state(0, 6)))
     for i, leaf in enumerate(state):
         want = torch.from_numpy(fx[f"state/{i}"])
@@ -163,6 +164,7 @@ def test_default_dims_fp32_golden(dev):
         preds = e.forward_masked(x, None)
         torch.cuda.synchronize()
         _close(preds, torch.from_numpy(fx[f"preds/{t}"]), P_RTOL, P_ATOL, f"default step {t}")
+    e.check()
     e.close()
 
 
