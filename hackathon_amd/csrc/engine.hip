@@ -231,6 +231,11 @@ struct Engine {
   int stage_ints() const { return 2 * max_runs + 1 + max_rows; }
   hipEvent_t stage_done[2] = {nullptr, nullptr};
   int stage_idx = 0;
+  // The four towers are independent: each runs on its own stream (default
+  // priority), forked from and joined back to the caller's stream per tick.
+  hipStream_t tstream[kTowers] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t fork_ev = nullptr;
+  hipEvent_t join_ev[kTowers] = {nullptr, nullptr, nullptr, nullptr};
   std::vector<char> seen;
   // Optional per-launch timing of the matrix-state scans (kind 0 mLSTM,
   // 1 Mamba2, 2 RetNet): event pairs recorded on the launch stream.
@@ -239,6 +244,11 @@ struct Engine {
   size_t prof_used[5] = {0, 0, 0, 0, 0};
 
   ~Engine() {
+    for (auto& st : tstream)
+      if (st) (void)hipStreamDestroy(st);
+    if (fork_ev) (void)hipEventDestroy(fork_ev);
+    for (auto& ev : join_ev)
+      if (ev) (void)hipEventDestroy(ev);
     for (auto& v : prof_ev)
       for (auto& pr : v) {
         (void)hipEventDestroy(pr.first);
@@ -365,6 +375,11 @@ int build_workspace(Engine& e) {
   HK_CHECK_HIP(hipHostMalloc((void**)&e.h_stage, (size_t)2 * e.stage_ints() * 4,
                              hipHostMallocDefault));
   for (auto& ev : e.stage_done) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  for (int t = 0; t < kTowers; ++t) {
+    HK_CHECK_HIP(hipStreamCreateWithFlags(&e.tstream[t], hipStreamNonBlocking));
+    HK_CHECK_HIP(hipEventCreateWithFlags(&e.join_ev[t], hipEventDisableTiming));
+  }
+  HK_CHECK_HIP(hipEventCreateWithFlags(&e.fork_ev, hipEventDisableTiming));
   return HK_OK;
 }
 
@@ -1045,7 +1060,14 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   HK_CHECK_HIP(hipEventRecord(e.stage_done[k], s));
   hk::Runs r{e.d_slots, e.d_off, n_runs, n_rows};
   HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, s));
-  for (int t = 0; t < hk::kTowers; ++t) HK_TRY(hk::run_tower(e, t, r, act, preds_dev, s));
+  HK_CHECK_HIP(hipEventRecord(e.fork_ev, s));
+  for (int t = 0; t < hk::kTowers; ++t) {
+    hipStream_t ts = e.tstream[t];
+    HK_CHECK_HIP(hipStreamWaitEvent(ts, e.fork_ev, 0));
+    HK_TRY(hk::run_tower(e, t, r, act, preds_dev, ts));
+    HK_CHECK_HIP(hipEventRecord(e.join_ev[t], ts));
+  }
+  for (int t = 0; t < hk::kTowers; ++t) HK_CHECK_HIP(hipStreamWaitEvent(s, e.join_ev[t], 0));
   return HK_OK;
 }
 

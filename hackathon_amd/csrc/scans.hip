@@ -238,7 +238,9 @@ __global__ __launch_bounds__(256) void slstm_round_kernel(
 // an error flag is set and every wave leaves.
 constexpr int kPersistRuns = 16;   // runs per chunk = one MFMA n-tile
 constexpr int kPersistThreads = 512;
-constexpr int kSpinLimit = 1 << 22;
+// Bounded wait: ~0.5 s of polling, far above a legitimate step (a few us)
+// even when other streams' kernels delay some work-groups' start.
+constexpr int kSpinLimit = 1 << 24;
 
 struct SlstmPersistArgs {
   const int* slot_ids;
