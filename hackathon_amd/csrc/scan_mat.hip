@@ -5,26 +5,44 @@
 // wave w holds rows [w*RPW, (w+1)*RPW) of the tile in VGPRs for the whole run,
 // so the state crosses HBM exactly twice per tick however long the run is.
 // The contraction over rows is in-lane (RPW FMAs into 4 accumulators), then a
-// 4-way cross-wave sum through LDS. Per-step row vectors (scale*beta, w) are
-// staged once into LDS and read back as broadcasts.
+// 4-way cross-wave sum through LDS. Per-step row vectors (scale*beta, w),
+// gamma and alpha are staged into LDS eight steps at a time with all loads in
+// flight together, so a long run pays one load latency per eight steps.
+#include <cstdint>
+
 #include "scan_mat.h"
 
 namespace hk {
 namespace {
 
-template <int RPW>
-__global__ __launch_bounds__(256) void mat_scan_kernel(MatScanDesc d) {
-  constexpr int kRows = 4 * RPW;
-  __shared__ __align__(16) float sb[kRows];
-  __shared__ __align__(16) float sw[kRows];
-  __shared__ float red[4][64];
+constexpr int kSteps = 8;  // steps whose row vectors are staged per LDS block
 
-  const int run = blockIdx.x;
+// NW waves split the tile's rows (RPW each); every lane owns VW adjacent
+// columns, so a work-group covers 64*VW columns and each wave instruction
+// moves 256*VW contiguous bytes of a state row.
+template <int RPW, int NW, int VW, bool VEC>
+__global__ __launch_bounds__(64 * NW) void mat_scan_kernel(MatScanDesc d) {
+  constexpr int kRows = NW * RPW;
+  constexpr int NT = 64 * NW;
+  constexpr int CW = 64 * VW;  // columns per work-group
+  __shared__ __align__(16) float sb[kSteps][kRows];  // scale * beta
+  __shared__ __align__(16) float sw[kSteps][kRows];  // w
+  __shared__ __align__(16) float sg[kSteps][CW];     // gamma of this column tile
+  __shared__ float sa[kSteps];                       // alpha
+  __shared__ __align__(16) float red[2][NW][CW];
+
+  // Column tile varies fastest in dispatch order: the work-groups of one
+  // (run, head) tile stream adjacent segments of the same rows together.
+  const int run = blockIdx.z;
   const int head = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = blockIdx.z * 64 + lane;
-  const bool col_ok = col < d.cols;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col0 = blockIdx.x * CW;
+  const int colv = col0 + lane * VW;  // first of this lane's VW columns
+  bool cok[VW];
+#pragma unroll
+  for (int v = 0; v < VW; ++v) cok[v] = colv + v < d.cols;
 
   int slot, r0, len;
   if (d.per_row) {
@@ -39,68 +57,163 @@ __global__ __launch_bounds__(256) void mat_scan_kernel(MatScanDesc d) {
   float* out_base = d.out + (int64_t)head * d.out_head_stride;
   if (len == 0) {
     // Idle row (reference API): state untouched, output defined as zero.
-    if (wave == 0 && col_ok) out_base[(int64_t)r0 * d.out_row_stride + col] = 0.0f;
+    if (wave == 0) {
+#pragma unroll
+      for (int v = 0; v < VW; ++v)
+        if (cok[v]) out_base[(int64_t)r0 * d.out_row_stride + colv + v] = 0.0f;
+    }
     return;
   }
 
   // Rows past d.rows hold zero in LDS and in the tile, so they contribute
   // nothing and need no branch in the inner loop.
-  for (int i = d.rows + threadIdx.x; i < kRows; i += 256) {
-    sb[i] = 0.0f;
-    sw[i] = 0.0f;
+  for (int i = tid; i < kSteps * kRows; i += NT) {
+    const int r = i % kRows;
+    if (r >= d.rows) {
+      sb[i / kRows][r] = 0.0f;
+      sw[i / kRows][r] = 0.0f;
+    }
   }
 
-  float* base = d.state + (int64_t)slot * d.slot_stride + (int64_t)head * d.head_stride +
-                (int64_t)col * d.col_stride;
+  // Uniform tile base (scalar registers) + 32-bit per-lane offsets: a tile
+  // spans well under 2^32 elements, and this keeps 64-bit address math out
+  // of the unrolled row loops.
+  float* tbase = d.state + (int64_t)slot * d.slot_stride + (int64_t)head * d.head_stride;
   const int rbase = wave * RPW;
-  float s[RPW];
+  const uint32_t rstride = (uint32_t)d.row_stride;
+  const uint32_t off0 = (uint32_t)colv * (uint32_t)d.col_stride + (uint32_t)rbase * rstride;
+  const int rlim = d.rows - rbase;  // rows of this wave's slice that exist
+  float s[RPW][VW];
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
-    const int r = rbase + i;
-    s[i] = (col_ok && r < d.rows) ? base[(int64_t)r * d.row_stride] : 0.0f;
-  }
-
-  for (int t = 0; t < len; ++t) {
-    const int64_t row = r0 + t;
-    const float a = d.alpha.ptr[row * d.alpha.row_stride + head * d.alpha.head_stride];
-    const float sc =
-        d.scale.ptr ? d.scale.ptr[row * d.scale.row_stride + head * d.scale.head_stride] : 1.0f;
-    const float g =
-        col_ok ? d.gamma.ptr[row * d.gamma.row_stride + head * d.gamma.head_stride + col] : 0.0f;
-    const float* bsrc = d.beta.ptr + row * d.beta.row_stride + head * d.beta.head_stride;
-    const float* wsrc = d.w.ptr + row * d.w.row_stride + head * d.w.head_stride;
-    for (int i = threadIdx.x; i < d.rows; i += 256) {
-      sb[i] = sc * bsrc[i];  // (i*k), (dt*b): the association the reference uses
-      sw[i] = wsrc[i];
-    }
-    __syncthreads();
-
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t o = off0 + (uint32_t)i * rstride;
+    if constexpr (VW == 2) {
+      float2 v2 = make_float2(0.0f, 0.0f);
+      if (cok[0] && cok[1] && i < rlim) v2 = *reinterpret_cast<const float2*>(tbase + o);
+      s[i][0] = v2.x;
+      s[i][1] = v2.y;
+    } else {
 #pragma unroll
-    for (int i = 0; i < RPW; i += 4) {
-      const float4 bv = *reinterpret_cast<const float4*>(&sb[rbase + i]);
-      const float4 wv = *reinterpret_cast<const float4*>(&sw[rbase + i]);
-      s[i + 0] = a * s[i + 0] + bv.x * g;
-      s[i + 1] = a * s[i + 1] + bv.y * g;
-      s[i + 2] = a * s[i + 2] + bv.z * g;
-      s[i + 3] = a * s[i + 3] + bv.w * g;
-      acc[0] += wv.x * s[i + 0];
-      acc[1] += wv.y * s[i + 1];
-      acc[2] += wv.z * s[i + 2];
-      acc[3] += wv.w * s[i + 3];
-    }
-    red[wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    __syncthreads();
-    if (wave == 0 && col_ok) {
-      out_base[row * d.out_row_stride + col] =
-          (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+      for (int v = 0; v < VW; ++v)
+        s[i][v] = (cok[v] && i < rlim) ? tbase[o + (uint32_t)v * (uint32_t)d.col_stride] : 0.0f;
     }
   }
 
+  const float* beta_h = d.beta.ptr + (int64_t)head * d.beta.head_stride;
+  const float* w_h = d.w.ptr + (int64_t)head * d.w.head_stride;
+  for (int t0 = 0; t0 < len; t0 += kSteps) {
+    const int ns = min(kSteps, len - t0);
+    const int64_t row0 = r0 + t0;
+    // ---- stage ns steps of row vectors, all loads in flight at once
+    if constexpr (VEC) {
+      constexpr int V = (kSteps * kRows / 4 + NT - 1) / NT;
+      const int vpr = d.rows >> 2;  // float4 per step
+      const int nv = ns * vpr;
+      float4 vb[V], vw[V];
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const int i = min(u * NT + tid, nv - 1);
+        const int st = i / vpr;
+        const int k4 = i - st * vpr;
+        const int64_t row = row0 + st;
+        vb[u] = reinterpret_cast<const float4*>(beta_h + row * d.beta.row_stride)[k4];
+        vw[u] = reinterpret_cast<const float4*>(w_h + row * d.w.row_stride)[k4];
+      }
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const int i = u * NT + tid;
+        if (i < nv) {
+          const int st = i / vpr;
+          const int k4 = i - st * vpr;
+          const int64_t row = row0 + st;
+          const float sc = d.scale.ptr ? d.scale.ptr[row * d.scale.row_stride +
+                                                     head * d.scale.head_stride]
+                                       : 1.0f;
+          // (i*k), (dt*b): the association the reference uses
+          float4 b4 = vb[u];
+          b4.x = sc * b4.x;
+          b4.y = sc * b4.y;
+          b4.z = sc * b4.z;
+          b4.w = sc * b4.w;
+          *reinterpret_cast<float4*>(&sb[st][4 * k4]) = b4;
+          *reinterpret_cast<float4*>(&sw[st][4 * k4]) = vw[u];
+        }
+      }
+    } else {
+      for (int i = tid; i < ns * d.rows; i += NT) {
+        const int st = i / d.rows;
+        const int k = i - st * d.rows;
+        const int64_t row = row0 + st;
+        const float sc = d.scale.ptr ? d.scale.ptr[row * d.scale.row_stride +
+                                                   head * d.scale.head_stride]
+                                     : 1.0f;
+        sb[st][k] = sc * beta_h[row * d.beta.row_stride + k];
+        sw[st][k] = w_h[row * d.w.row_stride + k];
+      }
+    }
+    for (int i = tid; i < ns * CW; i += NT) {
+      const int st = i / CW;
+      const int c = col0 + (i - st * CW);
+      const int64_t row = row0 + st;
+      sg[st][i - st * CW] = c < d.cols ? d.gamma.ptr[row * d.gamma.row_stride +
+                                                     head * d.gamma.head_stride + c]
+                                       : 0.0f;
+    }
+    if (tid < ns) {
+      const int64_t row = row0 + tid;
+      sa[tid] = d.alpha.ptr[row * d.alpha.row_stride + head * d.alpha.head_stride];
+    }
+    __syncthreads();
+
+    // ---- advance the tile through the staged steps
+    for (int st = 0; st < ns; ++st) {
+      const float a = sa[st];
+      float g[VW];
+#pragma unroll
+      for (int v = 0; v < VW; ++v) g[v] = sg[st][lane * VW + v];
+      float acc[VW][2];
+#pragma unroll
+      for (int v = 0; v < VW; ++v) acc[v][0] = acc[v][1] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < RPW; i += 4) {
+        const float4 bv = *reinterpret_cast<const float4*>(&sb[st][rbase + i]);
+        const float4 wv = *reinterpret_cast<const float4*>(&sw[st][rbase + i]);
+        const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+        const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+          for (int v = 0; v < VW; ++v) {
+            s[i + k][v] = a * s[i + k][v] + bb[k] * g[v];
+            acc[v][k & 1] += ww[k] * s[i + k][v];
+          }
+        }
+      }
+      const int par = st & 1;
+#pragma unroll
+      for (int v = 0; v < VW; ++v) red[par][wave][lane * VW + v] = acc[v][0] + acc[v][1];
+      __syncthreads();
+      if (tid < CW && col0 + tid < d.cols) {
+        float o = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) o += red[par][w2][tid];
+        out_base[(row0 + st) * d.out_row_stride + col0 + tid] = o;
+      }
+    }
+    __syncthreads();  // the next block's staging overwrites sb/sw/sg/sa
+  }
+
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
-    const int r = rbase + i;
-    if (col_ok && r < d.rows) base[(int64_t)r * d.row_stride] = s[i];
+    const uint32_t o = off0 + (uint32_t)i * rstride;
+    if constexpr (VW == 2) {
+      if (cok[0] && cok[1] && i < rlim)
+        *reinterpret_cast<float2*>(tbase + o) = make_float2(s[i][0], s[i][1]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VW; ++v)
+        if (cok[v] && i < rlim) tbase[o + (uint32_t)v * (uint32_t)d.col_stride] = s[i][v];
+    }
   }
 }
 
@@ -113,22 +226,42 @@ int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
              d.rows, d.cols, d.heads);
   HK_REQUIRE(d.per_row || (d.slot_ids && d.run_off), "mat_scan: need run descriptors");
   HK_REQUIRE(d.heads <= 65535, "mat_scan: too many heads");
+  HK_REQUIRE((int64_t)d.rows * d.row_stride + (int64_t)d.cols * d.col_stride < (1LL << 32),
+             "mat_scan: tile too large for 32-bit offsets");
   if (d.n_runs == 0) return HK_OK;
-  dim3 grid(d.n_runs, d.heads, (d.cols + 63) / 64);
-  dim3 block(256);
+  HK_REQUIRE(d.n_runs <= 65535, "mat_scan: at most 65535 runs per launch");
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool vec = d.rows % 4 == 0 && al16(d.beta.ptr) && al16(d.w.ptr) &&
+                   d.beta.row_stride % 4 == 0 && d.beta.head_stride % 4 == 0 &&
+                   d.w.row_stride % 4 == 0 && d.w.head_stride % 4 == 0;
+  // 256-row tiles with whole 128-column tiles, unit column stride and 8-byte
+  // aligned rows: 8 waves x float2 columns. 512-row tiles: 8 waves x 64 rows
+  // (wider tiles there exceed the register file of an 8-wave work-group).
+  const bool wide = d.rows > 128 && d.cols % 128 == 0 && d.col_stride == 1 &&
+                    d.row_stride % 2 == 0 && d.head_stride % 2 == 0 && d.slot_stride % 2 == 0 &&
+                    (reinterpret_cast<uintptr_t>(d.state) & 7) == 0;
+#define HK_SCAN_LAUNCH(R, NW, VW)                                                          \
+  {                                                                                        \
+    dim3 grid((d.cols + 64 * VW - 1) / (64 * VW), d.heads, d.n_runs);                      \
+    if (vec)                                                                               \
+      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, true>), grid, dim3(64 * NW), 0, stream, d); \
+    else                                                                                   \
+      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, false>), grid, dim3(64 * NW), 0, stream, d); \
+  }
   if (d.rows <= 32) {
-    hipLaunchKernelGGL(mat_scan_kernel<8>, grid, block, 0, stream, d);
+    HK_SCAN_LAUNCH(8, 4, 1)
   } else if (d.rows <= 64) {
-    hipLaunchKernelGGL(mat_scan_kernel<16>, grid, block, 0, stream, d);
+    HK_SCAN_LAUNCH(16, 4, 1)
   } else if (d.rows <= 128) {
-    hipLaunchKernelGGL(mat_scan_kernel<32>, grid, block, 0, stream, d);
+    HK_SCAN_LAUNCH(32, 4, 1)
   } else if (d.rows <= 256) {
-    hipLaunchKernelGGL(mat_scan_kernel<64>, grid, block, 0, stream, d);
+    if (wide) HK_SCAN_LAUNCH(32, 8, 2) else HK_SCAN_LAUNCH(64, 4, 1)
   } else if (d.rows <= 512) {
-    hipLaunchKernelGGL(mat_scan_kernel<128>, grid, block, 0, stream, d);
+    HK_SCAN_LAUNCH(64, 8, 1)
   } else {
     HK_REQUIRE(false, "mat_scan: %d rows exceeds the 512-row tile", d.rows);
   }
+#undef HK_SCAN_LAUNCH
   HK_LAUNCH_CHECK();
   return HK_OK;
 }

@@ -4,7 +4,13 @@ the oracle and the reference's golden vectors.
 fp32 path: predictions within rtol 1e-5 of the reference with an absolute
 floor of 2e-5 for predictions near zero (|d| <= 2e-5 + 1e-5 |ref|); state
 leaves within the same bound scaled by 10 (the state accumulates 16 steps of
-reassociated sums). bf16 path (CastLinear semantics): mean squared error
+reassociated sums). At the default dimensions the RetNet tower is
+ill-conditioned in fp32 (per-head RMSNorm of near-cancelling contractions):
+independent fp32 evaluations of the reference algorithm scatter by up to
+~1e-4 around the float64 result. There a prediction also passes when its
+distance to the reference's float64 result is within 4x the scatter of two
+independent fp32 evaluations (the reference's own fp32 run and the oracle's)
+at that tower and step. bf16 path (CastLinear semantics): mean squared error
 against the fp32 reference below 1e-3 of the predictions' mean square.
 """
 
@@ -155,15 +161,28 @@ def test_bf16_path_mse(dev, small_params):
 
 def test_default_dims_fp32_golden(dev):
     # The reference's CPU-runnable configuration at default dims (4 symbols),
-    # first 4 steps, against the reference's own predictions.
+    # first 4 steps, against the reference's own predictions (fp32 and
+    # float64, tests/golden/make_golden.py).
     fx = np.load(GOLDEN / "default.npz")
     cfg = spec.DEFAULT
-    e = _engine(cfg, weights.generate(cfg, 0), capacity=4, max_rows=16)
+    params = weights.generate(cfg, 0)
+    e = _engine(cfg, params, capacity=4, max_rows=16)
+    P32 = om.Params(params)
+    s32 = om.init_state(cfg, 4)
     for t in range(4):
-        x = torch.from_numpy(fx[f"x/{t}"]).to(dev)
-        preds = e.forward_masked(x, None)
-        torch.cuda.synchronize()
-        _close(preds, torch.from_numpy(fx[f"preds/{t}"]), P_RTOL, P_ATOL, f"default step {t}")
+        x = torch.from_numpy(fx[f"x/{t}"])
+        preds = e.forward_masked(x.to(dev), None).cpu().double()
+        ref32 = torch.from_numpy(fx[f"preds/{t}"]).double()
+        ref64 = torch.from_numpy(fx[f"preds64/{t}"]).double()
+        with torch.inference_mode():
+            o32, s32 = om.forward(P32, cfg, x, s32)
+        spread = torch.maximum((ref32 - ref64).abs(), (o32.double() - ref64).abs()).max(0).values
+        near_ref = (preds - ref32).abs() <= P_ATOL + P_RTOL * ref32.abs()
+        near_exact = (preds - ref64).abs() <= 4 * spread[None, :]
+        ok = near_ref | near_exact
+        assert bool(ok.all()), (
+            f"default step {t}: |gpu-ref32| {(preds - ref32).abs().max(0).values.tolist()}, "
+            f"|gpu-ref64| {(preds - ref64).abs().max(0).values.tolist()}, fp32 spread {spread.tolist()}")
     e.check()
     e.close()
 

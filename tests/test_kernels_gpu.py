@@ -3,8 +3,11 @@ oracle, with the invariants the reference's own suite checks
 (check_kernels.py:161-198, :201-236, :272-293):
 
 - idle state rows bit-identical; output a contiguous fp32 of the right shape;
-- state (all rows) and active outputs within rtol 1e-5 / atol 1e-5 of the
-  fp32 oracle (tighter than the reference's 1e-4);
+- state (all rows) and active outputs within the reference's own kernel
+  tolerance, rtol 1e-4 / atol 1e-5 (check_kernels.py:78-87): outputs are
+  512-term fp32 contractions whose terms reach ~20 while single outputs can
+  cancel to ~0.1, so reassociation alone moves them by ~1e-5 absolute (the
+  end-to-end predictions are held to 1e-5 relative in test_engine_gpu.py);
 - idle outputs exactly zero; masks mixed / all-true / all-false / None;
 - strided operands with NaN in the gaps; refusal of bad dtype/shape/layout.
 Shapes: the real per-block shapes at B=39 and B=20 plus the small, cell and
@@ -18,7 +21,7 @@ from oracle import kernels as ok
 
 pytestmark = pytest.mark.gpu
 
-RTOL, ATOL = 1e-5, 1e-5
+RTOL, ATOL = 1e-4, 1e-5
 
 
 def make_mlstm(batch, dims, g):
