@@ -59,6 +59,36 @@ __host__ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_bits_to_f32(f32_to_bf16_bits(f));
 }
 
+// Global-memory loads through explicit address-space-1 pointers. Pointers
+// that reach a kernel inside an argument struct are generic to the compiler,
+// which then emits flat loads (slower, and their waits also cover LDS);
+// these helpers give global_load_* with scalar base addressing.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 gload16(const void* p) {
+  return *(const __attribute__((address_space(1))) u32x4*)(p);
+}
+__device__ __forceinline__ float4 gload_f4(const float* p) {
+  const u32x4 v = gload16(p);
+  return make_float4(__builtin_bit_cast(float, v.x), __builtin_bit_cast(float, v.y),
+                     __builtin_bit_cast(float, v.z), __builtin_bit_cast(float, v.w));
+}
+__device__ __forceinline__ float gload(const float* p) {
+  return *(const __attribute__((address_space(1))) float*)(p);
+}
+__device__ __forceinline__ void gstore(float* p, float v) {
+  *(__attribute__((address_space(1))) float*)(p) = v;
+}
+
+// Work-group barrier for communication through LDS only. __syncthreads()
+// also orders global memory, which on gfx950 means waiting for every
+// outstanding vector-memory load of the wave (s_waitcnt vmcnt(0)) and so
+// drains any prefetch in flight; this one waits only for LDS operations.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Wave-wide sum with DPP-free shuffles (xor butterfly over 64 lanes).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -73,9 +103,9 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
   v = wave_sum(v);
-  __syncthreads();
+  lds_barrier();
   if (lane == 0) red[wave] = v;
-  __syncthreads();
+  lds_barrier();
   float t = 0.0f;
   for (int i = 0; i < nw; ++i) t += red[i];
   return t;

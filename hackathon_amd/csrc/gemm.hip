@@ -76,21 +76,31 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
   const int n0 = tn * BN;
   const E* Ab = static_cast<const E*>(g.A) + (int64_t)b * g.a_bstride;
   const E* Wb = static_cast<const E*>(g.W) + (int64_t)b * g.w_bstride;
-  const bool a_ok = (m0 + lrow) < g.M;
-  const bool w_ok = (n0 + lrow) < g.N;
-  const E* a_src = Ab + (int64_t)(a_ok ? m0 + lrow : 0) * g.lda + lchk * EPC;
-  const E* w_src = Wb + (int64_t)(w_ok ? n0 + lrow : 0) * g.ldw + lchk * EPC;
+  const int a_row = (m0 + lrow) < g.M ? m0 + lrow : 0;
+  const int w_row = (n0 + lrow) < g.N ? n0 + lrow : 0;
+  const E* a_src = Ab + (int64_t)a_row * g.lda + lchk * EPC;
+  const E* w_src = Wb + (int64_t)w_row * g.ldw + lchk * EPC;
 
   const int ktiles = g.K / BK;
   const int per = (ktiles + splits - 1) / splits;
   const int kt0 = split * per;
   const int kt1 = min(ktiles, kt0 + per);
 
-  const uint4 zero = {0u, 0u, 0u, 0u};
-  uint4 ra = zero, rw = zero;
-  if (kt0 < kt1) {
-    if (a_ok) ra = *reinterpret_cast<const uint4*>(a_src + (int64_t)kt0 * BK);
-    if (w_ok) rw = *reinterpret_cast<const uint4*>(w_src + (int64_t)kt0 * BK);
+  // Register ring of kRing K-slabs: the load of slab kt+kRing is issued when
+  // slab kt is consumed, so each load has kRing-1 slabs of MFMA work to land.
+  // The loop is unrolled by kRing so every ring index is a compile-time
+  // constant (the ring stays in VGPRs), and the barriers wait on LDS only.
+  constexpr int kRing = 4;
+  // Loads are unconditional so the wait counts stay static: rows past M or N
+  // read row 0 (their products land only in output rows/columns that are
+  // never stored), and slabs past the split's end re-read its last slab.
+  const int kt_last = max(kt1 - 1, 0);
+  u32x4 ra[kRing], rw[kRing];
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) {
+    const int kt = min(kt0 + j, kt_last);
+    ra[j] = gload16(a_src + (int64_t)kt * BK);
+    rw[j] = gload16(w_src + (int64_t)kt * BK);
   }
 
   const int lane = tid & 63;
@@ -105,43 +115,50 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int kt = kt0; kt < kt1; ++kt) {
-    *reinterpret_cast<uint4*>(&As[lrow * LROW + lchk * EPC]) = ra;
-    *reinterpret_cast<uint4*>(&Bs[lrow * LROW + lchk * EPC]) = rw;
-    __syncthreads();
-    if (kt + 1 < kt1) {
-      ra = a_ok ? *reinterpret_cast<const uint4*>(a_src + (int64_t)(kt + 1) * BK) : zero;
-      rw = w_ok ? *reinterpret_cast<const uint4*>(w_src + (int64_t)(kt + 1) * BK) : zero;
-    }
-    if constexpr (T == GemmType::kBF16) {
-      bf16x8 af[2], bfr[2];
+  for (int kb = kt0; kb < kt1; kb += kRing) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(&As[(wm * 32 + i * 16 + fr) * LROW + fk * 8]);
+    for (int j = 0; j < kRing; ++j) {
+      const int kt = kb + j;
+      if (kt < kt1) {
+        *reinterpret_cast<u32x4*>(&As[lrow * LROW + lchk * EPC]) = ra[j];
+        *reinterpret_cast<u32x4*>(&Bs[lrow * LROW + lchk * EPC]) = rw[j];
+        lds_barrier();
+        {
+          const int nk = min(kt + kRing, kt_last);
+          ra[j] = gload16(a_src + (int64_t)nk * BK);
+          rw[j] = gload16(w_src + (int64_t)nk * BK);
+        }
+        if constexpr (T == GemmType::kBF16) {
+          bf16x8 af[2], bfr[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[(wn * 32 + j * 16 + fr) * LROW + fk * 8]);
+          for (int i = 0; i < 2; ++i)
+            af[i] = *reinterpret_cast<const bf16x8*>(&As[(wm * 32 + i * 16 + fr) * LROW + fk * 8]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+          for (int q = 0; q < 2; ++q)
+            bfr[q] = *reinterpret_cast<const bf16x8*>(&Bs[(wn * 32 + q * 16 + fr) * LROW + fk * 8]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    } else {
+          for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float af[2], bfr[2];
+            for (int q = 0; q < 2; ++q)
+              acc[i][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[q], acc[i][q], 0, 0, 0);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) af[i] = As[(wm * 32 + i * 16 + fr) * LROW + s * 4 + fk];
+          for (int s4 = 0; s4 < 4; ++s4) {
+            float af[2], bfr[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) bfr[j] = Bs[(wn * 32 + j * 16 + fr) * LROW + s * 4 + fk];
+            for (int i = 0; i < 2; ++i) af[i] = As[(wm * 32 + i * 16 + fr) * LROW + s4 * 4 + fk];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+            for (int q = 0; q < 2; ++q) bfr[q] = Bs[(wn * 32 + q * 16 + fr) * LROW + s4 * 4 + fk];
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bfr[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+              for (int q = 0; q < 2; ++q)
+                acc[i][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bfr[q], acc[i][q], 0, 0, 0);
+          }
+        }
+        lds_barrier();
       }
     }
-    __syncthreads();
   }
 
   // Fragment (i, j): lane holds rows 4*fk + e, column fr.

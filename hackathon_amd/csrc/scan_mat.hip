@@ -163,7 +163,7 @@ __global__ __launch_bounds__(64 * NW) void mat_scan_kernel(MatScanDesc d) {
       const int64_t row = row0 + tid;
       sa[tid] = d.alpha.ptr[row * d.alpha.row_stride + head * d.alpha.head_stride];
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- advance the tile through the staged steps
     for (int st = 0; st < ns; ++st) {
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(64 * NW) void mat_scan_kernel(MatScanDesc d) {
       const int par = st & 1;
 #pragma unroll
       for (int v = 0; v < VW; ++v) red[par][wave][lane * VW + v] = acc[v][0] + acc[v][1];
-      __syncthreads();
+      lds_barrier();
       if (tid < CW && col0 + tid < d.cols) {
         float o = 0.0f;
 #pragma unroll
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(64 * NW) void mat_scan_kernel(MatScanDesc d) {
         out_base[(row0 + st) * d.out_row_stride + col0 + tid] = o;
       }
     }
-    __syncthreads();  // the next block's staging overwrites sb/sw/sg/sa
+    lds_barrier();  // the next block's staging overwrites sb/sw/sg/sa
   }
 
 #pragma unroll

@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256) void slstm_round_kernel(
     }
     hp[i] = v;
   }
-  __syncthreads();
+  lds_barrier();
 
   const int g = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -191,7 +191,7 @@ __global__ __launch_bounds__(256) void slstm_round_kernel(
 #pragma unroll
     for (int i = 0; i < kSlRuns; ++i) gsum[(g * kSlRuns + i) * kSlUnits + u] = acc[i];
   }
-  __syncthreads();
+  lds_barrier();
 
   const int rr = threadIdx.x / kSlUnits;
   const int uu = threadIdx.x % kSlUnits;
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
     bo = a.b_state[3 * H + ccol];
   }
   if (tid == 0) s_abort = 0;
-  __syncthreads();
+  lds_barrier();
 
   const bool tr = a.trace != nullptr && blockIdx.x == 0 && tid == 0;
   for (int t = 0; t < a.n_rounds; ++t) {
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
           }
         }
       }
-      __syncthreads();
+      lds_barrier();
       if (tr && c0 == 0) a.trace[t * 8 + 1] = __builtin_amdgcn_s_memrealtime();
       {
         // Columns fr >= nj read stale LDS rows; their results are dropped.
@@ -413,7 +413,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
 #pragma unroll
           for (int e = 0; e < 4; ++e) xbuf[fr * 64 + 16 * mt + 4 * fk + e] = acc[e];
         }
-        __syncthreads();
+        lds_barrier();
         if (kh == 0) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
           }
         }
       }
-      __syncthreads();
+      lds_barrier();
       if (tr && c0 == 0) a.trace[t * 8 + 2] = __builtin_amdgcn_s_memrealtime();
       if (cell) {
         const float* gs = gsum + jr * 64 + uu * 4;
@@ -446,13 +446,14 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
                            __HIP_MEMORY_SCOPE_AGENT);
       }
       if (tr && c0 == 0) a.trace[t * 8 + 3] = __builtin_amdgcn_s_memrealtime();
-      __syncthreads();
+      lds_barrier();
     }
-    // Head barrier: every wave waits for its h_t stores to complete, then one
-    // arrival per work-group; wait for the head's other work-groups.
+    // Head barrier: every wave waits for all its memory operations (the h_t
+    // stores included) to complete, then one arrival per work-group; wait
+    // for the head's other work-groups.
     if (tr) a.trace[t * 8 + 4] = __builtin_amdgcn_s_memrealtime();
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    lds_barrier();
     if (tr) a.trace[t * 8 + 5] = __builtin_amdgcn_s_memrealtime();
     if (tid == 0) {
       __hip_atomic_fetch_add(a.counters + head, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (tr) a.trace[t * 8 + 6] = __builtin_amdgcn_s_memrealtime();
     if (s_abort) return;
   }
@@ -478,7 +479,9 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
     const int run = i >> 4;
     const int col = head * hs + u0 + (i & 15);
     const int last = a.run_off[run + 1] - 1;
-    a.h_state[(int64_t)a.slot_ids[run] * H + col] = a.y[(int64_t)last * H + col];
+    // written by another thread of this work-group with a coherent store
+    a.h_state[(int64_t)a.slot_ids[run] * H + col] = __hip_atomic_load(
+        a.y + (int64_t)last * H + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
