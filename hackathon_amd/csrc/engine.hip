@@ -224,7 +224,8 @@ struct Engine {
   int* d_slots = nullptr;
   int* d_off = nullptr;
   int* d_act = nullptr;      // [max_rows]: runs active at each step
-  int* d_counters = nullptr; // [16]: sLSTM step-barrier counters
+  unsigned long long* d_xch = nullptr;  // [max_rows][H]: sLSTM h exchange words
+  unsigned int xch_tag = 0;             // tag of the last sLSTM launch
   int* d_err = nullptr;      // [1]: set by a kernel whose barrier timed out
   uint64_t* d_trace = nullptr;  // HK_TRACE_SLSTM: per-step stamps of layer 0's sLSTM
   int* h_stage = nullptr;    // pinned [2][stage_ints()]
@@ -363,15 +364,15 @@ int build_workspace(Engine& e) {
   e.d_slots = static_cast<int*>(e.alloc_bytes((size_t)e.max_runs * 4));
   e.d_off = static_cast<int*>(e.alloc_bytes((size_t)(e.max_runs + 1) * 4));
   e.d_act = static_cast<int*>(e.alloc_bytes((size_t)e.max_rows * 4));
-  e.d_counters = static_cast<int*>(e.alloc_bytes(16 * 4));
+  e.d_xch = static_cast<unsigned long long*>(e.alloc_bytes((size_t)e.max_rows * d.H * 8));
   e.d_err = static_cast<int*>(e.alloc_bytes(4));
-  if (!e.d_slots || !e.d_off || !e.d_act || !e.d_counters || !e.d_err) return HK_ERR_HIP;
+  if (!e.d_slots || !e.d_off || !e.d_act || !e.d_xch || !e.d_err) return HK_ERR_HIP;
   HK_CHECK_HIP(hipMemset(e.d_err, 0, 4));
   if (std::getenv("HK_TRACE_SLSTM")) {
     e.d_trace = static_cast<uint64_t*>(e.alloc_bytes((size_t)e.max_rows * 8 * 8));
     if (!e.d_trace) return HK_ERR_HIP;
   }
-  HK_CHECK_HIP(hipMemset(e.d_counters, 0, 16 * 4));
+  HK_CHECK_HIP(hipMemset(e.d_xch, 0, (size_t)e.max_rows * d.H * 8));
   HK_CHECK_HIP(hipHostMalloc((void**)&e.h_stage, (size_t)2 * e.stage_ints() * 4,
                              hipHostMallocDefault));
   for (auto& ev : e.stage_done) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
@@ -492,11 +493,16 @@ int run_xlstm(Engine& e, int l, const Runs& r, const std::vector<int>& act, hipS
                         w.GIN + (int64_t)g * H, 4 * H, s));
   }
   if (slstm_persist_supported(H, d.nh_s)) {
+    if (++e.xch_tag == 0) {
+      // tags wrapped: clear words that could carry a reused tag
+      HK_CHECK_HIP(hipMemsetAsync(e.d_xch, 0, (size_t)e.max_rows * H * 8, s));
+      e.xch_tag = 1;
+    }
     HK_TRY(timed(e, 3, s, [&] {
       return slstm_persist(r, e.d_act, (int)act.size(), w.GIN, H, d.nh_s,
                            F32(e, kXLSTM, l, X_S_ST_W), F32(e, kXLSTM, l, X_S_ST_B), st[XS_S_H],
-                           st[XS_S_C], st[XS_S_N], st[XS_S_M], w.SY, e.d_counters, e.d_err,
-                           l == 0 ? e.d_trace : nullptr, s);
+                           st[XS_S_C], st[XS_S_N], st[XS_S_M], w.SY, e.d_xch, e.xch_tag,
+                           e.d_err, l == 0 ? e.d_trace : nullptr, s);
     }));
   } else {
     for (size_t t = 0; t < act.size(); ++t) {
@@ -949,10 +955,6 @@ int hk_engine_check(void* h) {
   }
   if (flag) {
     HK_CHECK_HIP(hipMemset(e.d_err, 0, 4));
-  if (std::getenv("HK_TRACE_SLSTM")) {
-    e.d_trace = static_cast<uint64_t*>(e.alloc_bytes((size_t)e.max_rows * 8 * 8));
-    if (!e.d_trace) return HK_ERR_HIP;
-  }
     hk::set_error("hk_engine_check: a kernel step barrier timed out (results invalid)");
     return HK_ERR_HIP;
   }

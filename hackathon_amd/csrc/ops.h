@@ -97,14 +97,16 @@ int rglru_scan(const Runs& r, const float* x, const float* gi, const float* gr, 
 int slstm_round(const Runs& r, int step, int n_active, const float* gin, int hidden, int heads,
                 const float* w_state, const float* b_state, const float* h_state, float* c_state,
                 float* n_state, float* m_state, float* y, hipStream_t s);
-// The whole tick's sLSTM recurrence in one cooperative launch (all steps);
-// also writes h_state. act_dev[t] = runs active at step t. counters: `heads`
-// ints of scratch; err: set to 1 if a step barrier timed out.
+// The whole tick's sLSTM recurrence in one persistent launch (all steps);
+// also writes h_state. act_dev[t] = runs active at step t. xch: [n_rows]
+// [hidden] 64-bit exchange words; tag: nonzero and different from every
+// earlier launch's on the same buffer; err: set to 1 if a poll timed out.
 bool slstm_persist_supported(int hidden, int heads);
 int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* gin, int hidden,
                   int heads, const float* w_state, const float* b_state, float* h_state,
-                  float* c_state, float* n_state, float* m_state, float* y, int* counters,
-                  int* err, uint64_t* trace, hipStream_t s);
+                  float* c_state, float* n_state, float* m_state, float* y,
+                  unsigned long long* xch, unsigned int tag, int* err, uint64_t* trace,
+                  hipStream_t s);
 // After the last round: h_state[slot] = y[last row of the run].
 int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipStream_t s);
 

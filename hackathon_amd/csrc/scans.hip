@@ -222,25 +222,32 @@ __global__ __launch_bounds__(256) void slstm_round_kernel(
   y[(int64_t)row * hidden + col] = og * cn / (nn + 1e-6f);
 }
 
-// Persistent sLSTM recurrence for a whole tick: one cooperative launch per
-// layer instead of one launch per step. Work-group g (512 threads, 8 waves)
-// owns 16 units of one head: 64 gate rows (unit*4 + gate) x hs inputs of the
-// recurrent weights, held in VGPRs for every step as fp32 MFMA A fragments
-// (wave = (16-row tile, k half)). Step t, per chunk of up to 16 runs: stage
-// h_{t-1} in LDS, G[64 rows x 16 runs] = W . H on v_mfma_f32_16x16x4_f32
-// (fp32 products and sums), add the two k halves through LDS, then the cell
-// update, one (run, unit) per thread. The head's work-groups then meet at a
-// counter barrier before step t+1 reads the h_t they wrote. h_t crosses
-// work-groups (and XCDs) only through agent-scope atomic stores and loads,
-// which are coherent without the L2-wide writeback and invalidate that an
-// agent-scope fence costs; each wave waits for its stores to complete before
-// its work-group arrives at the counter. Every spin is bounded: on timeout
-// an error flag is set and every wave leaves.
+// Persistent sLSTM recurrence for a whole tick: one launch per layer instead
+// of one launch per step. Work-group g (512 threads, 8 waves) owns 16 units
+// of one head: 64 gate rows (unit*4 + gate) x hs inputs of the recurrent
+// weights, held in VGPRs for every step as fp32 MFMA A fragments (wave =
+// (16-row tile, k half)). Step t, per chunk of up to 16 active runs: stage
+// h_{t-1} of the chunk's runs in LDS; G[64 rows x runs] = W . H, on
+// v_mfma_f32_16x16x4_f32 when the chunk has more than kValuRuns runs, else
+// as VALU dot products over the same register-resident weights (past the
+// first steps of a skewed tick only a few long runs remain); add the two k
+// halves through LDS; then the cell update, one (run, unit) per thread.
+//
+// h_t crosses work-groups (and XCDs) through an exchange buffer of 64-bit
+// words (value bits | tag << 32) stored and loaded with agent-scope atomics.
+// The tag is this launch's number, so a reader that sees its tag in a word
+// also sees that word's value: no barrier between the head's work-groups is
+// needed, and each row of the buffer is written once per launch. A reader
+// polls with a bounded spin; on timeout it sets the error flag and every
+// wave of every work-group leaves.
 constexpr int kPersistRuns = 16;   // runs per chunk = one MFMA n-tile
+constexpr int kValuRuns = 4;       // chunks up to this size use the VALU product
 constexpr int kPersistThreads = 512;
-// Bounded wait: ~0.5 s of polling, far above a legitimate step (a few us)
-// even when other streams' kernels delay some work-groups' start.
-constexpr int kSpinLimit = 1 << 24;
+// Bounded wait: each poll re-reads a wave's words (a memory round trip of a
+// microsecond or more), so this bounds a wait to well under a few seconds,
+// far above a legitimate step even when other streams' kernels delay some
+// work-groups' start.
+constexpr int kSpinLimit = 1 << 19;
 
 struct SlstmPersistArgs {
   const int* slot_ids;
@@ -257,13 +264,46 @@ struct SlstmPersistArgs {
   float* c_state;
   float* n_state;
   float* m_state;
-  float* y;            // [rows][hidden]
-  int* counters;       // [heads], zero at launch
-  int* err;            // set to 1 on a barrier timeout
-  uint64_t* trace;     // optional [n_rounds][8] wall-clock stamps of work-group 0
+  float* y;                 // [rows][hidden]
+  unsigned long long* xch;  // [rows][hidden] exchange words
+  unsigned int tag;         // nonzero; differs from the tags of earlier launches
+  int* err;                 // set to 1 on a poll timeout
+  uint64_t* trace;          // optional [n_rounds][8] wall-clock stamps of work-group 0
 };
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ unsigned long long xch_word(float v, unsigned int tag) {
+  return (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32);
+}
+
+// Waits until every word of this wave at offs[u] (u < N) carries `tag`; the
+// words' values land in val[]. Returns false on timeout or a raised error
+// flag (then the flag is set).
+template <int N>
+__device__ __forceinline__ bool poll_words(const unsigned long long* base, const uint32_t* offs,
+                                           unsigned int tag, int* err, float* val) {
+  int spins = 0;
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const unsigned long long w = __hip_atomic_load(base + offs[u], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+      ok = ok && (unsigned int)(w >> 32) == tag;
+      val[u] = __uint_as_float((unsigned int)w);
+    }
+    if (__all(ok)) return true;
+    __builtin_amdgcn_s_sleep(1);
+    ++spins;
+    if (spins > kSpinLimit ||
+        ((spins & 255) == 0 &&
+         __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) {
+      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+  }
+}
 
 template <int HS>
 __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPersistArgs a) {
@@ -370,18 +410,19 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
           }
         }
       } else {
-        // written by the head's work-groups this launch: coherent loads
+        // written by the head's work-groups at step t-1 of this launch
         constexpr int kS = (kPersistRuns * hs + NT - 1) / NT;
         const int nel = nj * hs;
+        uint32_t offs[kS];
         float v[kS];
 #pragma unroll
         for (int u = 0; u < kS; ++u) {
           const int i = min(u * NT + tid, nel - 1);
           const int j = i / hs;
-          v[u] = __hip_atomic_load(
-              a.y + (int64_t)(a.run_off[c0 + j] + t - 1) * H + head * hs + (i - j * hs),
-              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          offs[u] = (uint32_t)(a.run_off[c0 + j] + t - 1) * (uint32_t)H + head * hs + (i - j * hs);
         }
+        // Waves whose words all lie past the chunk poll the clamped last word.
+        if (!poll_words<kS>(a.xch, offs, a.tag, a.err, v)) s_abort = 1;
 #pragma unroll
         for (int u = 0; u < kS; ++u) {
           const int i = u * NT + tid;
@@ -392,8 +433,9 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         }
       }
       lds_barrier();
+      if (s_abort) return;
       if (tr && c0 == 0) a.trace[t * 8 + 1] = __builtin_amdgcn_s_memrealtime();
-      {
+      if (nj > kValuRuns) {
         // Columns fr >= nj read stale LDS rows; their results are dropped.
         // Four independent accumulator chains (one per step c of a group),
         // summed at the end, so consecutive MFMAs do not wait on each other.
@@ -421,6 +463,43 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
             gsum[fr * 64 + r] = acc[e] + xbuf[fr * 64 + r];
           }
         }
+      } else {
+        // VALU product for up to kValuRuns runs: lane (fr, fk) dots its
+        // register row slice with run j's h (one LDS word per k, shared by
+        // the 16 lanes of a k group), then the four k groups are summed
+        // across lanes.
+        float part[kValuRuns];
+        const float* hb = hbuf + kh * KH + 4 * fk;
+#pragma unroll
+        for (int j = 0; j < kValuRuns; ++j) {
+          part[j] = 0.0f;
+          if (j < nj) {
+            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+            for (int g = 0; g < KG; ++g) {
+              const float4 hv = *reinterpret_cast<const float4*>(hb + j * PAD + 16 * g);
+              s0 = fmaf(w[4 * g + 0], hv.x, s0);
+              s1 = fmaf(w[4 * g + 1], hv.y, s1);
+              s2 = fmaf(w[4 * g + 2], hv.z, s2);
+              s3 = fmaf(w[4 * g + 3], hv.w, s3);
+            }
+            float p = (s0 + s1) + (s2 + s3);
+            p += __shfl_xor(p, 16);
+            p += __shfl_xor(p, 32);
+            part[j] = p;
+          }
+        }
+        if (kh == 1 && fk == 0) {
+#pragma unroll
+          for (int j = 0; j < kValuRuns; ++j)
+            if (j < nj) xbuf[j * 64 + 16 * mt + fr] = part[j];
+        }
+        lds_barrier();
+        if (kh == 0 && fk == 0) {
+#pragma unroll
+          for (int j = 0; j < kValuRuns; ++j)
+            if (j < nj) gsum[j * 64 + 16 * mt + fr] = part[j] + xbuf[j * 64 + 16 * mt + fr];
+        }
       }
       lds_barrier();
       if (tr && c0 == 0) a.trace[t * 8 + 2] = __builtin_amdgcn_s_memrealtime();
@@ -437,57 +516,54 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         const float fg = expf(lfm - mn);
         const float cn = fg * pc + ig * tanhf(zp);
         const float nn = fg * pn + ig;
+        const float h = og * cn / (nn + 1e-6f);
         a.c_state[psi] = cn;
         a.n_state[psi] = nn;
         a.m_state[psi] = mn;
-        // h_t is published with a coherent (agent-scope) store, so the head's
-        // other work-groups can read it without a cache-wide flush.
-        __hip_atomic_store(a.y + prow * H + ccol, og * cn / (nn + 1e-6f), __ATOMIC_RELAXED,
+        a.y[prow * H + ccol] = h;
+        __hip_atomic_store(a.xch + prow * H + ccol, xch_word(h, a.tag), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       }
       if (tr && c0 == 0) a.trace[t * 8 + 3] = __builtin_amdgcn_s_memrealtime();
-      lds_barrier();
+      // The next chunk's staging writes hbuf only (read before the barrier
+      // above); gsum and xbuf are rewritten only after its staging barrier.
     }
-    // Head barrier: every wave waits for all its memory operations (the h_t
-    // stores included) to complete, then one arrival per work-group; wait
-    // for the head's other work-groups.
-    if (tr) a.trace[t * 8 + 4] = __builtin_amdgcn_s_memrealtime();
-    __builtin_amdgcn_s_waitcnt(0);
-    lds_barrier();
-    if (tr) a.trace[t * 8 + 5] = __builtin_amdgcn_s_memrealtime();
-    if (tid == 0) {
-      __hip_atomic_fetch_add(a.counters + head, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int target = (t + 1) * wpg;
-      int spins = 0;
-      while (__hip_atomic_load(a.counters + head, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-             target) {
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins > kSpinLimit ||
-            __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-          __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          s_abort = 1;
-          break;
-        }
-      }
+    if (tr) {
+      const uint64_t now = __builtin_amdgcn_s_memrealtime();
+      a.trace[t * 8 + 4] = now;
+      a.trace[t * 8 + 5] = now;
+      a.trace[t * 8 + 6] = now;
     }
+  }
+  // h_state <- h of each run's last step, for this work-group's units. Step
+  // 0 of every work-group of the head reads h_state (chunk by chunk), so it
+  // is written only once all of them are past that staging: each writes the
+  // step-0 words of the last run in its last step-0 chunk, after all of its
+  // step-0 staging, so wait for those words.
+  {
+    constexpr int kS = (hs + NT - 1) / NT;
+    uint32_t offs[kS];
+    float v[kS];
+    const uint32_t row = (uint32_t)a.run_off[a.n_runs - 1];
+#pragma unroll
+    for (int u = 0; u < kS; ++u)
+      offs[u] = row * (uint32_t)H + head * hs + min(u * NT + tid, hs - 1);
+    if (!poll_words<kS>(a.xch, offs, a.tag, a.err, v)) s_abort = 1;
     lds_barrier();
-    if (tr) a.trace[t * 8 + 6] = __builtin_amdgcn_s_memrealtime();
     if (s_abort) return;
   }
-  // h_state <- h of each run's last step, for this work-group's units.
-  for (int i = tid; i < a.n_runs * 16; i += NT) {
+  // The words were written by other threads of this work-group: read them
+  // through the tag as well (the loop count is uniform so every lane polls).
+  const int total = a.n_runs * 16;
+  for (int base = 0; base < total; base += NT) {
+    const int i = min(base + tid, total - 1);
     const int run = i >> 4;
     const int col = head * hs + u0 + (i & 15);
-    const int last = a.run_off[run + 1] - 1;
-    // written by another thread of this work-group with a coherent store
-    a.h_state[(int64_t)a.slot_ids[run] * H + col] = __hip_atomic_load(
-        a.y + (int64_t)last * H + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t off = (uint32_t)(a.run_off[run + 1] - 1) * (uint32_t)H + col;
+    float hv;
+    if (!poll_words<1>(a.xch, &off, a.tag, a.err, &hv)) return;
+    if (base + tid < total) a.h_state[(int64_t)a.slot_ids[run] * H + col] = hv;
   }
-}
-
-__global__ void zero_i32_kernel(int* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
 }
 
 __global__ void slstm_final_kernel(const int* __restrict__ slot_ids,
@@ -619,35 +695,53 @@ bool slstm_persist_supported(int hidden, int heads) {
   return hs * heads == hidden && (hs == 32 || hs == 64 || hs == 128 || hs == 256 || hs == 512);
 }
 
+// The step barriers need every work-group of the launch resident at once.
+// The grid (heads * hs/16 <= 128 work-groups of one CU each) is checked
+// against the device's CU count times the kernel's occupancy per CU; given
+// that, an ordinary launch is enough: work-groups that cannot start yet wait
+// only for other kernels' work-groups, which never wait on this kernel. (A
+// cooperative launch would also exclude concurrent kernels of the other
+// streams for the whole recurrence.)
+template <int HS>
+int launch_persist(const SlstmPersistArgs& a, size_t smem, hipStream_t s) {
+  const dim3 grid(a.heads * (HS / 16)), block(kPersistThreads);
+  static int fits = -1;  // per process: one device type
+  if (fits < 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    HK_CHECK_HIP(hipGetDevice(&dev));
+    HK_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    HK_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, slstm_persist_kernel<HS>, kPersistThreads, smem));
+    fits = (int64_t)cus * per_cu;
+  }
+  HK_REQUIRE((int64_t)grid.x <= fits, "slstm_persist: %u work-groups cannot be co-resident (%d)",
+             grid.x, fits);
+  hipLaunchKernelGGL(slstm_persist_kernel<HS>, grid, block, smem, s, a);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
 int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* gin, int hidden,
                   int heads, const float* w_state, const float* b_state, float* h_state,
-                  float* c_state, float* n_state, float* m_state, float* y, int* counters,
-                  int* err, uint64_t* trace, hipStream_t s) {
+                  float* c_state, float* n_state, float* m_state, float* y,
+                  unsigned long long* xch, unsigned int tag, int* err, uint64_t* trace,
+                  hipStream_t s) {
   if (r.n_runs == 0 || n_rounds == 0) return HK_OK;
   HK_REQUIRE(slstm_persist_supported(hidden, heads), "slstm_persist: head size unsupported");
-  HK_REQUIRE(heads <= 16, "slstm_persist: at most 16 heads (barrier counters)");
+  HK_REQUIRE(tag != 0 && xch != nullptr, "slstm_persist: exchange buffer and nonzero tag needed");
+  HK_REQUIRE((int64_t)r.n_rows * hidden < (1LL << 32), "slstm_persist: exchange buffer too large");
   const int hs = hidden / heads;
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, counters, heads);
-  HK_LAUNCH_CHECK();
   SlstmPersistArgs a{r.slot_ids, r.run_off, act_dev, n_rounds, r.n_runs, gin, hidden, heads,
-                     w_state, b_state, h_state, c_state, n_state, m_state, y, counters, err,
+                     w_state, b_state, h_state, c_state, n_state, m_state, y, xch, tag, err,
                      trace};
-  void* args[] = {&a};
   const size_t smem = (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float);
-  const dim3 grid(heads * (hs / 16)), block(kPersistThreads);
-  hipError_t e;
   switch (hs) {
-    case 32: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<32>, grid, block, args, smem, s); break;
-    case 64: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<64>, grid, block, args, smem, s); break;
-    case 128: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<128>, grid, block, args, smem, s); break;
-    case 256: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<256>, grid, block, args, smem, s); break;
-    default: e = hipLaunchCooperativeKernel((const void*)slstm_persist_kernel<512>, grid, block, args, smem, s); break;
+    case 32: return launch_persist<32>(a, smem, s);
+    case 64: return launch_persist<64>(a, smem, s);
+    case 128: return launch_persist<128>(a, smem, s);
+    case 256: return launch_persist<256>(a, smem, s);
+    default: return launch_persist<512>(a, smem, s);
   }
-  if (e != hipSuccess) {
-    set_error("slstm_persist: cooperative launch failed: %s", hipGetErrorString(e));
-    return HK_ERR_HIP;
-  }
-  return HK_OK;
 }
 
 int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipStream_t s) {

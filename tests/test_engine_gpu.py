@@ -133,6 +133,57 @@ def test_long_runs_chunked_fp32(dev, small_params):
     eng.close()
 
 
+MID = spec.ModelConfig(hidden_size=256, proj_size=512, tower_depth=2, num_heads=8,
+                       num_features=7)
+
+
+def test_persistent_slstm_skewed_runs_fp32(dev):
+    # Hidden 256 with 4 sLSTM heads of 64 runs the persistent sLSTM kernel.
+    # Batches shaped like a skewed tick: 40 runs at step 0 (three 16-run
+    # chunks), 5-8 runs at the next steps (MFMA product), then 1-4 runs
+    # (VALU product); then launches with one and with two steps. Predictions
+    # and every state leaf against the oracle's reference rounds.
+    from hackathon_amd.client import NnInferenceClient, PendingRequest
+
+    cfg = MID
+    params = weights.generate(cfg, 0)
+    capacity = 48
+    eng = _engine(cfg, params, capacity=capacity, max_rows=128)
+    client = NnInferenceClient(capacity, engine=eng)
+    oracle = OracleClient(om.Params(params), cfg, capacity)
+    rng = np.random.default_rng(5)
+    symbols = [f"S{i:02d}" for i in range(40)]
+    shapes = [
+        [24, 9, 7, 6, 5, 3, 2, 2] + [1] * 32,
+        [1] * 40,
+        [2, 2, 2] + [1] * 20,
+        [13, 1, 1, 6, 5, 5, 5, 5, 5, 2] + [1] * 10,
+    ]
+    uid = 0
+    for b, counts in enumerate(shapes):
+        order = rng.permutation(len(symbols))
+        reqs = {}
+        for sym_i, n in zip(order, counts):
+            reqs[symbols[sym_i]] = []
+            for _ in range(n):
+                feats = np.clip(rng.standard_normal(cfg.num_features), -5, 5).astype(np.float32)
+                reqs[symbols[sym_i]].append(PendingRequest(uid, symbols[sym_i], feats.tolist()))
+                uid += 1
+        got = client.process_batch(reqs)
+        want_ids, want_preds = oracle.process_batch(reqs)
+        assert got.unique_ids == want_ids
+        _close(torch.tensor(got.predictions), torch.tensor(want_preds), P_RTOL, P_ATOL,
+               f"batch {b} preds")
+    eng.check()
+    for i, (leaf, want) in enumerate(zip(om.flatten(eng.export_state(0, capacity)),
+                                         om.flatten(oracle.state))):
+        if want.dtype == torch.int32:
+            assert torch.equal(leaf.cpu(), want), f"leaf {i}"
+        else:
+            _close(leaf, want, 10 * P_RTOL, 10 * P_ATOL, f"state leaf {i} {tuple(want.shape)}")
+    eng.close()
+
+
 def test_bf16_path_mse(dev, small_params):
     from hackathon_amd.client import NnInferenceClient
 
