@@ -934,23 +934,34 @@ int hk_engine_check(void* h) {
   HK_CHECK_HIP(hipMemcpy(&flag, e.d_err, 4, hipMemcpyDeviceToHost));
   if (e.d_trace) {
     // Phases of the last tick's layer-0 sLSTM steps in microseconds
-    // (s_memrealtime runs at 100 MHz); the first chunk's stage / dot / cell.
+    // (s_memrealtime runs at 100 MHz), work-group 0, first chunk: poll for
+    // h_{t-1}, staging barrier, product, cell update, later chunks, and the
+    // gap to the next step.
     std::vector<uint64_t> tr((size_t)e.max_rows * 8);
     HK_CHECK_HIP(hipMemcpy(tr.data(), e.d_trace, tr.size() * 8, hipMemcpyDeviceToHost));
+    static const char* names[6] = {"poll", "stage", "dot", "cell", "rest-chunks", "next"};
     double tot[6] = {0, 0, 0, 0, 0, 0};
     int n = 0;
-    for (int t = 0; t < e.max_rows && tr[t * 8 + 6] > tr[t * 8 + 0]; ++t, ++n) {
+    for (int t = 0; t < e.max_rows && tr[t * 8 + 5] > tr[t * 8 + 0]; ++t, ++n) {
       double ph[6];
-      for (int k = 0; k < 6; ++k) ph[k] = (double)(tr[t * 8 + k + 1] - tr[t * 8 + k]) * 0.01;
+      for (int k = 0; k < 5; ++k)
+        ph[k] = tr[t * 8 + k + 1] > tr[t * 8 + k] ? (double)(tr[t * 8 + k + 1] - tr[t * 8 + k]) * 0.01 : 0.0;
+      ph[5] = (t + 1 < e.max_rows && tr[(t + 1) * 8] > tr[t * 8 + 5])
+                  ? (double)(tr[(t + 1) * 8] - tr[t * 8 + 5]) * 0.01 : 0.0;
       for (int k = 0; k < 6; ++k) tot[k] += ph[k];
-      if (t < 3 || t % 10 == 0)
-        fprintf(stderr,
-                "slstm step %d: stage %.2f dot %.2f cell %.2f rest-chunks %.2f wait %.2f "
-                "barrier %.2f us\n", t, ph[0], ph[1], ph[2], ph[3], ph[4], ph[5]);
+      if (t < 3 || t % 10 == 0) {
+        fprintf(stderr, "slstm step %d:", t);
+        for (int k = 0; k < 6; ++k) fprintf(stderr, " %s %.2f", names[k], ph[k]);
+        const uint64_t* q = &tr[t * 8];
+        if (q[2] <= q[6] && q[6] <= q[7] && q[7] <= q[3])  // VALU product sub-phases
+          fprintf(stderr, " [fma %.2f xbuf %.2f gsum %.2f]", (q[6] - q[2]) * 0.01,
+                  (q[7] - q[6]) * 0.01, (q[3] - q[7]) * 0.01);
+        fprintf(stderr, " us\n");
+      }
     }
-    fprintf(stderr,
-            "slstm %d steps: stage %.1f dot %.1f cell %.1f rest-chunks %.1f wait %.1f "
-            "barrier %.1f us\n", n, tot[0], tot[1], tot[2], tot[3], tot[4], tot[5]);
+    fprintf(stderr, "slstm %d steps:", n);
+    for (int k = 0; k < 6; ++k) fprintf(stderr, " %s %.1f", names[k], tot[k]);
+    fprintf(stderr, " us\n");
     HK_CHECK_HIP(hipMemset(e.d_trace, 0, tr.size() * 8));
   }
   if (flag) {

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void slstm_round_kernel(
     const float* __restrict__ b_state, const float* __restrict__ h_state,
     float* __restrict__ c_state, float* __restrict__ n_state, float* __restrict__ m_state,
     float* __restrict__ y) {
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   float* hp = smem;                            // [kSlRuns][hs]
   float* gsum = smem + kSlRuns * hs;           // [4][kSlRuns][kSlUnits]
   const int head = blockIdx.x;
@@ -279,19 +279,22 @@ __device__ __forceinline__ unsigned long long xch_word(float v, unsigned int tag
 
 // Waits until every word of this wave at offs[u] (u < N) carries `tag`; the
 // words' values land in val[]. Returns false on timeout or a raised error
-// flag (then the flag is set).
+// flag (then the flag is set). All N loads of a poll are issued before the
+// first wait.
 template <int N>
 __device__ __forceinline__ bool poll_words(const unsigned long long* base, const uint32_t* offs,
                                            unsigned int tag, int* err, float* val) {
   int spins = 0;
   for (;;) {
+    unsigned long long w[N];
+#pragma unroll
+    for (int u = 0; u < N; ++u)
+      w[u] = __hip_atomic_load(base + offs[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     bool ok = true;
 #pragma unroll
     for (int u = 0; u < N; ++u) {
-      const unsigned long long w = __hip_atomic_load(base + offs[u], __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-      ok = ok && (unsigned int)(w >> 32) == tag;
-      val[u] = __uint_as_float((unsigned int)w);
+      ok = ok && (unsigned int)(w[u] >> 32) == tag;
+      val[u] = __uint_as_float((unsigned int)w[u]);
     }
     if (__all(ok)) return true;
     __builtin_amdgcn_s_sleep(1);
@@ -305,9 +308,20 @@ __device__ __forceinline__ bool poll_words(const unsigned long long* base, const
   }
 }
 
+// poll_words over the first n (uniform, 1 <= n <= N) of N offsets, with the
+// load count rounded up to a power of two (the extra offsets are valid).
+template <int N>
+__device__ __forceinline__ bool poll_first(const unsigned long long* base, const uint32_t* offs,
+                                           unsigned int tag, int* err, float* val, int n) {
+  if constexpr (N >= 2) {
+    if (n <= N / 2) return poll_first<N / 2>(base, offs, tag, err, val, n);
+  }
+  return poll_words<N>(base, offs, tag, err, val);
+}
+
 template <int HS>
 __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPersistArgs a) {
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   constexpr int hs = HS;
   constexpr int wpg = hs / 16;      // work-groups per head
   constexpr int NT = kPersistThreads;
@@ -315,9 +329,12 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
   constexpr int KH = hs / 2;        // k per wave
   constexpr int KG = KH / 16;       // groups of 4 MFMA k-steps per wave
   float* hbuf = smem;                               // [16][PAD]
-  float* gsum = hbuf + kPersistRuns * PAD;          // [16 runs][64 rows]
-  float* xbuf = gsum + kPersistRuns * 64;           // [16 runs][64 rows], k-half 1
+  float* gsum = hbuf + kPersistRuns * PAD;          // [16 runs][64 rows], k half 0
+  float* xbuf = gsum + kPersistRuns * 64;           // [16 runs][64 rows], k half 1
   __shared__ int s_abort;
+  // The recurrence is latency-bound and shares its CUs with other streams'
+  // kernels: its waves take instruction-issue priority over theirs.
+  __builtin_amdgcn_s_setprio(3);
   const int H = a.hidden;
   const int head = blockIdx.x / wpg;
   const int u0 = (blockIdx.x % wpg) * 16;
@@ -360,10 +377,13 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
   if (tid == 0) s_abort = 0;
   lds_barrier();
 
+  // Optional phase stamps of work-group 0 (thread 0), kept in LDS during the
+  // recurrence so that taking them adds no memory waits, stored at the end.
   const bool tr = a.trace != nullptr && blockIdx.x == 0 && tid == 0;
+  uint64_t* ltr = reinterpret_cast<uint64_t*>(xbuf + kPersistRuns * 64);
   for (int t = 0; t < a.n_rounds; ++t) {
     const int na = a.act[t];
-    if (tr) a.trace[t * 8 + 0] = __builtin_amdgcn_s_memrealtime();
+    if (tr) ltr[t * 8 + 0] = __builtin_amdgcn_s_memrealtime();
     for (int c0 = 0; c0 < na; c0 += kPersistRuns) {
       const int nj = min(kPersistRuns, na - c0);
       // Operands of this thread's cell update, fetched before the h staging
@@ -422,7 +442,8 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
           offs[u] = (uint32_t)(a.run_off[c0 + j] + t - 1) * (uint32_t)H + head * hs + (i - j * hs);
         }
         // Waves whose words all lie past the chunk poll the clamped last word.
-        if (!poll_words<kS>(a.xch, offs, a.tag, a.err, v)) s_abort = 1;
+        if (!poll_first<kS>(a.xch, offs, a.tag, a.err, v, (nel + NT - 1) / NT)) s_abort = 1;
+        if (tr && c0 == 0) ltr[t * 8 + 1] = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
         for (int u = 0; u < kS; ++u) {
           const int i = u * NT + tid;
@@ -434,7 +455,10 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
       }
       lds_barrier();
       if (s_abort) return;
-      if (tr && c0 == 0) a.trace[t * 8 + 1] = __builtin_amdgcn_s_memrealtime();
+      if (tr && c0 == 0) ltr[t * 8 + 2] = __builtin_amdgcn_s_memrealtime();
+      // Each k half writes its partial gate sums to its own LDS plane
+      // (gsum: k half 0, xbuf: k half 1); the cell update adds the two.
+      float* half = kh == 0 ? gsum : xbuf;
       if (nj > kValuRuns) {
         // Columns fr >= nj read stale LDS rows; their results are dropped.
         // Four independent accumulator chains (one per step c of a group),
@@ -451,64 +475,41 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         }
         const floatx4_t acc = (a0 + a1) + (a2 + a3);
         // acc[e] = G[row 16*mt + 4*fk + e][run fr], partial over this k half.
-        if (kh == 1) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) xbuf[fr * 64 + 16 * mt + 4 * fk + e] = acc[e];
-        }
-        lds_barrier();
-        if (kh == 0) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 16 * mt + 4 * fk + e;
-            gsum[fr * 64 + r] = acc[e] + xbuf[fr * 64 + r];
-          }
-        }
+        *reinterpret_cast<float4*>(half + fr * 64 + 16 * mt + 4 * fk) =
+            make_float4(acc[0], acc[1], acc[2], acc[3]);
       } else {
-        // VALU product for up to kValuRuns runs: lane (fr, fk) dots its
-        // register row slice with run j's h (one LDS word per k, shared by
-        // the 16 lanes of a k group), then the four k groups are summed
-        // across lanes.
-        float part[kValuRuns];
+        // VALU product, one run at a time (a rolled loop keeps the code
+        // small: this runs once per step and must stay in the instruction
+        // cache): lane (fr, fk) dots its register row slice with run j's h
+        // (one LDS word per k, shared by the 16 lanes of a k group), then
+        // the four k groups are summed across lanes.
         const float* hb = hbuf + kh * KH + 4 * fk;
+#pragma unroll 1
+        for (int j = 0; j < nj; ++j) {
+          float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
-        for (int j = 0; j < kValuRuns; ++j) {
-          part[j] = 0.0f;
-          if (j < nj) {
-            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-            for (int g = 0; g < KG; ++g) {
-              const float4 hv = *reinterpret_cast<const float4*>(hb + j * PAD + 16 * g);
-              s0 = fmaf(w[4 * g + 0], hv.x, s0);
-              s1 = fmaf(w[4 * g + 1], hv.y, s1);
-              s2 = fmaf(w[4 * g + 2], hv.z, s2);
-              s3 = fmaf(w[4 * g + 3], hv.w, s3);
-            }
-            float p = (s0 + s1) + (s2 + s3);
-            p += __shfl_xor(p, 16);
-            p += __shfl_xor(p, 32);
-            part[j] = p;
+          for (int g = 0; g < KG; ++g) {
+            const float4 hv = *reinterpret_cast<const float4*>(hb + j * PAD + 16 * g);
+            s0 = fmaf(w[4 * g + 0], hv.x, s0);
+            s1 = fmaf(w[4 * g + 1], hv.y, s1);
+            s2 = fmaf(w[4 * g + 2], hv.z, s2);
+            s3 = fmaf(w[4 * g + 3], hv.w, s3);
           }
-        }
-        if (kh == 1 && fk == 0) {
-#pragma unroll
-          for (int j = 0; j < kValuRuns; ++j)
-            if (j < nj) xbuf[j * 64 + 16 * mt + fr] = part[j];
-        }
-        lds_barrier();
-        if (kh == 0 && fk == 0) {
-#pragma unroll
-          for (int j = 0; j < kValuRuns; ++j)
-            if (j < nj) gsum[j * 64 + 16 * mt + fr] = part[j] + xbuf[j * 64 + 16 * mt + fr];
+          float p = (s0 + s1) + (s2 + s3);
+          p += __shfl_xor(p, 16);
+          p += __shfl_xor(p, 32);
+          if (fk == 0) half[j * 64 + 16 * mt + fr] = p;
         }
       }
       lds_barrier();
-      if (tr && c0 == 0) a.trace[t * 8 + 2] = __builtin_amdgcn_s_memrealtime();
+      if (tr && c0 == 0) ltr[t * 8 + 3] = __builtin_amdgcn_s_memrealtime();
       if (cell) {
-        const float* gs = gsum + jr * 64 + uu * 4;
-        const float ip = pi + (gs[0] + bi);
-        const float fp = pf + (gs[1] + bf);
-        const float zp = pz + (gs[2] + bz);
-        const float op = po + (gs[3] + bo);
+        const float4 g0 = *reinterpret_cast<const float4*>(gsum + jr * 64 + uu * 4);
+        const float4 g1 = *reinterpret_cast<const float4*>(xbuf + jr * 64 + uu * 4);
+        const float ip = pi + ((g0.x + g1.x) + bi);
+        const float fp = pf + ((g0.y + g1.y) + bf);
+        const float zp = pz + ((g0.z + g1.z) + bz);
+        const float op = po + ((g0.w + g1.w) + bo);
         const float lfm = pm + logsigmoid(fp);
         const float mn = fmaxf(ip, lfm);
         const float og = sigmoid(op);
@@ -524,16 +525,15 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         __hip_atomic_store(a.xch + prow * H + ccol, xch_word(h, a.tag), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       }
-      if (tr && c0 == 0) a.trace[t * 8 + 3] = __builtin_amdgcn_s_memrealtime();
+      if (tr && c0 == 0) ltr[t * 8 + 4] = __builtin_amdgcn_s_memrealtime();
       // The next chunk's staging writes hbuf only (read before the barrier
       // above); gsum and xbuf are rewritten only after its staging barrier.
     }
-    if (tr) {
-      const uint64_t now = __builtin_amdgcn_s_memrealtime();
-      a.trace[t * 8 + 4] = now;
-      a.trace[t * 8 + 5] = now;
-      a.trace[t * 8 + 6] = now;
-    }
+    if (tr) ltr[t * 8 + 5] = __builtin_amdgcn_s_memrealtime();
+  }
+  if (a.trace != nullptr && blockIdx.x == 0) {
+    lds_barrier();
+    for (int i = tid; i < a.n_rounds * 8; i += NT) a.trace[i] = ltr[i];
   }
   // h_state <- h of each run's last step, for this work-group's units. Step
   // 0 of every work-group of the head reads h_state (chunk by chunk), so it
@@ -734,7 +734,11 @@ int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* 
   SlstmPersistArgs a{r.slot_ids, r.run_off, act_dev, n_rounds, r.n_runs, gin, hidden, heads,
                      w_state, b_state, h_state, c_state, n_state, m_state, y, xch, tag, err,
                      trace};
-  const size_t smem = (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float);
+  size_t smem = (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float);
+  if (trace != nullptr) {
+    HK_REQUIRE(n_rounds <= 512, "slstm_persist: tracing supports at most 512 steps");
+    smem += (size_t)n_rounds * 8 * sizeof(uint64_t);
+  }
   switch (hs) {
     case 32: return launch_persist<32>(a, smem, s);
     case 64: return launch_persist<64>(a, smem, s);
