@@ -220,23 +220,40 @@ struct Engine {
   std::vector<std::vector<std::vector<float*>>> state;
   std::vector<std::vector<int64_t>> leaf_elems;
   TowerWS ws[kTowers];
+  TowerWS ws_x2;             // xLSTM workspace of the second run group
   Act FE;
+  // Tick descriptors, one device block (layout of stage_ints()): slot ids,
+  // run offsets and active-run counts of the whole tick, run offsets of the
+  // second xLSTM group (relative to its first row) and per-group counts.
+  int* d_desc = nullptr;
   int* d_slots = nullptr;
   int* d_off = nullptr;
   int* d_act = nullptr;      // [max_rows]: runs active at each step
-  unsigned long long* d_xch = nullptr;  // [max_rows][H]: sLSTM h exchange words
-  unsigned int xch_tag = 0;             // tag of the last sLSTM launch
+  int* d_off2 = nullptr;     // [max_runs + 1]
+  int* d_act1 = nullptr;     // [max_rows]
+  int* d_act2 = nullptr;     // [max_rows]
+  unsigned long long* d_xch = nullptr;   // [max_rows][H]: sLSTM h exchange words
+  unsigned long long* d_xch2 = nullptr;  // the same for the second xLSTM group
+  unsigned int xch_tag = 0;              // tag of the last sLSTM launch
   int* d_err = nullptr;      // [1]: set by a kernel whose barrier timed out
   uint64_t* d_trace = nullptr;  // HK_TRACE_SLSTM: per-step stamps of layer 0's sLSTM
   int* h_stage = nullptr;    // pinned [2][stage_ints()]
-  int stage_ints() const { return 2 * max_runs + 1 + max_rows; }
+  int stage_ints() const { return 3 * max_runs + 2 + 3 * max_rows; }
   hipEvent_t stage_done[2] = {nullptr, nullptr};
   int stage_idx = 0;
-  // The four towers are independent: each runs on its own stream (default
-  // priority), forked from and joined back to the caller's stream per tick.
-  hipStream_t tstream[kTowers] = {nullptr, nullptr, nullptr, nullptr};
+  // The towers are independent and run concurrently, forked from and joined
+  // back to the caller's stream per tick (all streams at default priority).
+  // Four streams in all, one per hardware queue of a default HIP process:
+  // the caller's stream runs the xLSTM tower's first run group (the longest
+  // runs), side[0] its second group, side[1] Mamba2, side[2] RetNet then
+  // Hawk.
+  static constexpr int kSide = 3;
+  hipStream_t side[kSide] = {nullptr, nullptr, nullptr};
   hipEvent_t fork_ev = nullptr;
-  hipEvent_t join_ev[kTowers] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t join_ev[kSide] = {nullptr, nullptr, nullptr};
+  // Per layer, the two xLSTM groups' persistent sLSTM launches alternate
+  // (group 2 then group 1): two such launches never share the GPU.
+  std::vector<hipEvent_t> sl_ev[2];
   std::vector<char> seen;
   // Optional per-launch timing of the matrix-state scans (kind 0 mLSTM,
   // 1 Mamba2, 2 RetNet): event pairs recorded on the launch stream.
@@ -245,11 +262,14 @@ struct Engine {
   size_t prof_used[5] = {0, 0, 0, 0, 0};
 
   ~Engine() {
-    for (auto& st : tstream)
+    for (auto& st : side)
       if (st) (void)hipStreamDestroy(st);
     if (fork_ev) (void)hipEventDestroy(fork_ev);
     for (auto& ev : join_ev)
       if (ev) (void)hipEventDestroy(ev);
+    for (auto& v : sl_ev)
+      for (auto& ev : v)
+        if (ev) (void)hipEventDestroy(ev);
     for (auto& v : prof_ev)
       for (auto& pr : v) {
         (void)hipEventDestroy(pr.first);
@@ -289,14 +309,15 @@ bool any_null(const Act& a, bool need_f32, bool lowp) {
 int build_workspace(Engine& e) {
   const Dims& d = e.d;
   const int64_t R = e.max_rows;
-  for (int t = 0; t < kTowers; ++t) {
-    TowerWS& w = e.ws[t];
+  for (int t = 0; t <= kTowers; ++t) {
+    // t == kTowers: the second xLSTM group's workspace
+    TowerWS& w = t < kTowers ? e.ws[t] : e.ws_x2;
     w.X.f = e.alloc_f(R * d.H);
     w.A = e.alloc_act(R * d.H, true);
     w.H1 = e.alloc_act(R * d.P, false);
     if (!w.X.f || any_null(w.A, true, e.lowp) || any_null(w.H1, false, e.lowp)) return HK_ERR_HIP;
     int64_t max_n = std::max<int64_t>(d.P, d.H);
-    switch (t) {
+    switch (t < kTowers ? t : (int)kXLSTM) {
       case kXLSTM:
         w.XN = e.alloc_f(R * d.H);
         w.XCA = e.alloc_f(R * d.H);
@@ -361,26 +382,36 @@ int build_workspace(Engine& e) {
   }
   e.FE = e.alloc_act(R * d.Fpad, false);
   if (any_null(e.FE, false, e.lowp)) return HK_ERR_HIP;
-  e.d_slots = static_cast<int*>(e.alloc_bytes((size_t)e.max_runs * 4));
-  e.d_off = static_cast<int*>(e.alloc_bytes((size_t)(e.max_runs + 1) * 4));
-  e.d_act = static_cast<int*>(e.alloc_bytes((size_t)e.max_rows * 4));
+  e.d_desc = static_cast<int*>(e.alloc_bytes((size_t)e.stage_ints() * 4));
   e.d_xch = static_cast<unsigned long long*>(e.alloc_bytes((size_t)e.max_rows * d.H * 8));
+  e.d_xch2 = static_cast<unsigned long long*>(e.alloc_bytes((size_t)e.max_rows * d.H * 8));
   e.d_err = static_cast<int*>(e.alloc_bytes(4));
-  if (!e.d_slots || !e.d_off || !e.d_act || !e.d_xch || !e.d_err) return HK_ERR_HIP;
+  if (!e.d_desc || !e.d_xch || !e.d_xch2 || !e.d_err) return HK_ERR_HIP;
+  e.d_slots = e.d_desc;
+  e.d_off = e.d_slots + e.max_runs;
+  e.d_act = e.d_off + e.max_runs + 1;
+  e.d_off2 = e.d_act + e.max_rows;
+  e.d_act1 = e.d_off2 + e.max_runs + 1;
+  e.d_act2 = e.d_act1 + e.max_rows;
   HK_CHECK_HIP(hipMemset(e.d_err, 0, 4));
   if (std::getenv("HK_TRACE_SLSTM")) {
     e.d_trace = static_cast<uint64_t*>(e.alloc_bytes((size_t)e.max_rows * 8 * 8));
     if (!e.d_trace) return HK_ERR_HIP;
   }
   HK_CHECK_HIP(hipMemset(e.d_xch, 0, (size_t)e.max_rows * d.H * 8));
+  HK_CHECK_HIP(hipMemset(e.d_xch2, 0, (size_t)e.max_rows * d.H * 8));
   HK_CHECK_HIP(hipHostMalloc((void**)&e.h_stage, (size_t)2 * e.stage_ints() * 4,
                              hipHostMallocDefault));
   for (auto& ev : e.stage_done) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
-  for (int t = 0; t < kTowers; ++t) {
-    HK_CHECK_HIP(hipStreamCreateWithFlags(&e.tstream[t], hipStreamNonBlocking));
-    HK_CHECK_HIP(hipEventCreateWithFlags(&e.join_ev[t], hipEventDisableTiming));
+  for (int i = 0; i < Engine::kSide; ++i) {
+    HK_CHECK_HIP(hipStreamCreateWithFlags(&e.side[i], hipStreamNonBlocking));
+    HK_CHECK_HIP(hipEventCreateWithFlags(&e.join_ev[i], hipEventDisableTiming));
   }
   HK_CHECK_HIP(hipEventCreateWithFlags(&e.fork_ev, hipEventDisableTiming));
+  for (auto& v : e.sl_ev) {
+    v.assign(d.D, nullptr);
+    for (auto& ev : v) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  }
   return HK_OK;
 }
 
@@ -475,9 +506,28 @@ const float* F32(Engine& e, int t, int l, int i) {
   return static_cast<const float*>(e.slots[t][l + 1][i].ptr);
 }
 
-int run_xlstm(Engine& e, int l, const Runs& r, const std::vector<int>& act, hipStream_t s) {
+// A group of consecutive runs of the tick handled as a batch of its own: its
+// rows are rows row0 .. row0 + r.n_rows - 1 of the tick, and r.run_off,
+// act_dev and act count from its first row and run.
+struct Group {
+  Runs r;
+  const int* act_dev = nullptr;  // [steps] runs of the group active per step
+  std::vector<int> act;          // host copy
+  int row0 = 0;
+};
+
+// Ordering of a persistent sLSTM launch against another group's: wait for
+// `wait` (if any) before it, record `rec` (if any) after it.
+struct SlOrder {
+  hipEvent_t wait = nullptr;
+  hipEvent_t rec = nullptr;
+};
+
+int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* xch,
+              const SlOrder& ord, hipStream_t s) {
   const Dims& d = e.d;
-  TowerWS& w = e.ws[kXLSTM];
+  const Runs& r = g.r;
+  const std::vector<int>& act = g.act;
   const int n = r.n_rows;
   const int H = d.H, I = d.I;
   float** st = e.state[kXLSTM][l].data();
@@ -493,17 +543,22 @@ int run_xlstm(Engine& e, int l, const Runs& r, const std::vector<int>& act, hipS
                         w.GIN + (int64_t)g * H, 4 * H, s));
   }
   if (slstm_persist_supported(H, d.nh_s)) {
+    if (ord.wait) HK_CHECK_HIP(hipStreamWaitEvent(s, ord.wait, 0));
     if (++e.xch_tag == 0) {
-      // tags wrapped: clear words that could carry a reused tag
+      // Tags wrapped: clear both exchange buffers (words that could carry a
+      // reused tag). Every earlier sLSTM launch is ordered before this point:
+      // this stream's by stream order, the other group's by the wait above.
       HK_CHECK_HIP(hipMemsetAsync(e.d_xch, 0, (size_t)e.max_rows * H * 8, s));
+      HK_CHECK_HIP(hipMemsetAsync(e.d_xch2, 0, (size_t)e.max_rows * H * 8, s));
       e.xch_tag = 1;
     }
     HK_TRY(timed(e, 3, s, [&] {
-      return slstm_persist(r, e.d_act, (int)act.size(), w.GIN, H, d.nh_s,
+      return slstm_persist(r, g.act_dev, (int)act.size(), w.GIN, H, d.nh_s,
                            F32(e, kXLSTM, l, X_S_ST_W), F32(e, kXLSTM, l, X_S_ST_B), st[XS_S_H],
-                           st[XS_S_C], st[XS_S_N], st[XS_S_M], w.SY, e.d_xch, e.xch_tag,
-                           e.d_err, l == 0 ? e.d_trace : nullptr, s);
+                           st[XS_S_C], st[XS_S_N], st[XS_S_M], w.SY, xch, e.xch_tag, e.d_err,
+                           (l == 0 && xch == e.d_xch) ? e.d_trace : nullptr, s);
     }));
+    if (ord.rec) HK_CHECK_HIP(hipEventRecord(ord.rec, s));
   } else {
     for (size_t t = 0; t < act.size(); ++t) {
       HK_TRY(slstm_round(r, (int)t, act[t], w.GIN, H, d.nh_s, F32(e, kXLSTM, l, X_S_ST_W),
@@ -666,38 +721,96 @@ int run_hawk(Engine& e, int l, const Runs& r, hipStream_t s) {
   return HK_OK;
 }
 
-int run_tower(Engine& e, int t, const Runs& r, const std::vector<int>& act, float* preds,
-              hipStream_t s) {
+// input_up -> relu -> input_down (model/inference_model.py:88-90)
+int tower_head(Engine& e, int t, TowerWS& w, const Group& g, hipStream_t s) {
   const Dims& d = e.d;
-  TowerWS& w = e.ws[t];
-  const int n = r.n_rows;
+  const int n = g.r.n_rows;
+  const int64_t off = (int64_t)g.row0 * d.Fpad;
+  const Act fe{e.FE.f ? e.FE.f + off : nullptr, e.FE.l ? e.FE.l + off : nullptr};
+  HK_TRY(linear(e, w, fe, d.Fpad, {S(e, t, -1, T_UP_W), S(e, t, -1, T_UP_B)}, n, d.P, d.Fpad, 1,
+                nullptr, 0, w.H1.f, d.P, w.H1.l, d.P, s));
+  return linear(e, w, w.H1, d.P, {S(e, t, -1, T_DOWN_W), S(e, t, -1, T_DOWN_B)}, n, d.H, d.P, 0,
+                nullptr, 0, w.X.f, d.H, nullptr, 0, s);
+}
+
+// Block l (model/inference_model.py:63-68).
+int tower_layer(Engine& e, int t, TowerWS& w, const Group& g, int l, unsigned long long* xch,
+                const SlOrder& ord, hipStream_t s) {
+  const Dims& d = e.d;
+  const int n = g.r.n_rows;
   const int H = d.H, P = d.P;
-  // input_up -> relu -> input_down (model/inference_model.py:88-90)
-  HK_TRY(linear(e, w, e.FE, d.Fpad, {S(e, t, -1, T_UP_W), S(e, t, -1, T_UP_B)}, n, P, d.Fpad, 1,
-                nullptr, 0, w.H1.f, P, w.H1.l, P, s));
-  HK_TRY(linear(e, w, w.H1, P, {S(e, t, -1, T_DOWN_W), S(e, t, -1, T_DOWN_B)}, n, H, P, 0, nullptr,
-                0, w.X.f, H, nullptr, 0, s));
-  for (int l = 0; l < d.D; ++l) {
-    // Block (model/inference_model.py:63-68)
-    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM1), 1.1920928955078125e-07f, n, H, w.A.f, H,
-                        w.A.l, H, s));
-    switch (t) {
-      case kXLSTM: HK_TRY(run_xlstm(e, l, r, act, s)); break;
-      case kMamba2: HK_TRY(run_mamba2(e, l, r, s)); break;
-      case kRetNet: HK_TRY(run_retnet(e, l, r, s)); break;
-      default: HK_TRY(run_hawk(e, l, r, s)); break;
-    }
-    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM2), 1.1920928955078125e-07f, n, H, w.A.f, H,
-                        w.A.l, H, s));
-    HK_TRY(linear(e, w, w.A, H, {S(e, t, l, B_FC1_W), S(e, t, l, B_FC1_B)}, n, P, H, 1, nullptr, 0,
-                  w.H1.f, P, w.H1.l, P, s));
-    HK_TRY(linear(e, w, w.H1, P, {S(e, t, l, B_FC2_W), S(e, t, l, B_FC2_B)}, n, H, P, 0, w.X.f, H,
-                  w.X.f, H, nullptr, 0, s));
+  HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM1), 1.1920928955078125e-07f, n, H, w.A.f, H,
+                      w.A.l, H, s));
+  switch (t) {
+    case kXLSTM: HK_TRY(run_xlstm(e, w, l, g, xch, ord, s)); break;
+    case kMamba2: HK_TRY(run_mamba2(e, l, g.r, s)); break;
+    case kRetNet: HK_TRY(run_retnet(e, l, g.r, s)); break;
+    default: HK_TRY(run_hawk(e, l, g.r, s)); break;
   }
-  HK_TRY(output_proj(w.X.f, static_cast<const float*>(e.gslots[G_OUT_W].ptr),
-                     static_cast<const float*>(e.gslots[G_OUT_B].ptr), n, H, preds, kTowers, t,
-                     s));
-  return HK_OK;
+  HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM2), 1.1920928955078125e-07f, n, H, w.A.f, H,
+                      w.A.l, H, s));
+  HK_TRY(linear(e, w, w.A, H, {S(e, t, l, B_FC1_W), S(e, t, l, B_FC1_B)}, n, P, H, 1, nullptr, 0,
+                w.H1.f, P, w.H1.l, P, s));
+  return linear(e, w, w.H1, P, {S(e, t, l, B_FC2_W), S(e, t, l, B_FC2_B)}, n, H, P, 0, w.X.f, H,
+                w.X.f, H, nullptr, 0, s);
+}
+
+// Shared output_proj into column t of preds (model/inference_model.py:142).
+int tower_tail(Engine& e, int t, TowerWS& w, const Group& g, float* preds, hipStream_t s) {
+  return output_proj(w.X.f, static_cast<const float*>(e.gslots[G_OUT_W].ptr),
+                     static_cast<const float*>(e.gslots[G_OUT_B].ptr), g.r.n_rows, e.d.H,
+                     preds + (int64_t)g.row0 * kTowers, kTowers, t, s);
+}
+
+int run_tower(Engine& e, int t, const Group& g, float* preds, hipStream_t s) {
+  TowerWS& w = e.ws[t];
+  HK_TRY(tower_head(e, t, w, g, s));
+  for (int l = 0; l < e.d.D; ++l) HK_TRY(tower_layer(e, t, w, g, l, e.d_xch, SlOrder{}, s));
+  return tower_tail(e, t, w, g, preds, s);
+}
+
+// The xLSTM tower over two run groups on two streams, enqueued layer by
+// layer so that each persistent sLSTM launch waits on the other group's
+// previous one (g2 layer l after g1 layer l-1, g1 layer l after g2 layer l).
+int run_xlstm_split(Engine& e, const Group& g1, hipStream_t s1, const Group& g2, hipStream_t s2,
+                    float* preds) {
+  TowerWS& w1 = e.ws[kXLSTM];
+  TowerWS& w2 = e.ws_x2;
+  HK_TRY(tower_head(e, kXLSTM, w1, g1, s1));
+  HK_TRY(tower_head(e, kXLSTM, w2, g2, s2));
+  for (int l = 0; l < e.d.D; ++l) {
+    SlOrder o2{l > 0 ? e.sl_ev[0][l - 1] : nullptr, e.sl_ev[1][l]};
+    HK_TRY(tower_layer(e, kXLSTM, w2, g2, l, e.d_xch2, o2, s2));
+    SlOrder o1{e.sl_ev[1][l], e.sl_ev[0][l]};
+    HK_TRY(tower_layer(e, kXLSTM, w1, g1, l, e.d_xch, o1, s1));
+  }
+  HK_TRY(tower_tail(e, kXLSTM, w1, g1, preds, s1));
+  return tower_tail(e, kXLSTM, w2, g2, preds, s2);
+}
+
+// Where to split the length-sorted runs into two xLSTM groups (returns
+// n_runs for no split). Per layer a group costs about kStepUs per sLSTM step
+// of its longest run plus kSymbolUs per symbol for the mLSTM state traffic;
+// the two groups run concurrently, so a split pays when the larger of the
+// two costs is well below the unsplit cost (each group also reads every
+// projection weight, hence the margin).
+int xlstm_split_point(const int* run_off, int n_runs) {
+  constexpr double kStepUs = 3.0, kSymbolUs = 5.0, kGain = 0.8;
+  if (n_runs < 2) return n_runs;
+  const int len0 = run_off[1] - run_off[0];
+  const double whole = kStepUs * len0 + kSymbolUs * n_runs;
+  double best = whole;
+  int best_k = n_runs;
+  for (int k = 1; k < n_runs; ++k) {
+    const int lenk = run_off[k + 1] - run_off[k];
+    const double c = std::max(kStepUs * len0 + kSymbolUs * k,
+                              kStepUs * lenk + kSymbolUs * (n_runs - k));
+    if (c < best) {
+      best = c;
+      best_k = k;
+    }
+  }
+  return best < kGain * whole ? best_k : n_runs;
 }
 
 Slot* find_slot(Engine& e, int tower, int layer, int slot) {
@@ -1049,38 +1162,66 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   for (int i = 0; i < n_runs; ++i) e.seen[slot_ids_host[i]] = 0;
 
   // Descriptors through a two-deep pinned ring (the copy of tick k-2 must be
-  // done before its staging area is rewritten).
+  // done before its staging area is rewritten), one copy per tick.
   const int k = e.stage_idx;
   e.stage_idx ^= 1;
   HK_CHECK_HIP(hipEventSynchronize(e.stage_done[k]));
-  std::vector<int> act(run_off_host[1] - run_off_host[0]);
+  const int steps = run_off_host[1] - run_off_host[0];
+  // xLSTM run groups: runs [0, split) and [split, n_runs).
+  const int split = hk::xlstm_split_point(run_off_host, n_runs);
+  const int row_split = run_off_host[split];
+  const int steps2 = split < n_runs ? run_off_host[split + 1] - run_off_host[split] : 0;
+  int* stage = e.h_stage + (size_t)k * e.stage_ints();
+  int* h_slots = stage;
+  int* h_off = h_slots + e.max_runs;
+  int* h_act = h_off + e.max_runs + 1;
+  int* h_off2 = h_act + e.max_rows;
+  int* h_act1 = h_off2 + e.max_runs + 1;
+  int* h_act2 = h_act1 + e.max_rows;
+  std::memcpy(h_slots, slot_ids_host, (size_t)n_runs * 4);
+  std::memcpy(h_off, run_off_host, (size_t)(n_runs + 1) * 4);
   {
     int c = n_runs;
-    for (size_t t = 0; t < act.size(); ++t) {
-      while (c > 0 && run_off_host[c] - run_off_host[c - 1] <= (int)t) --c;
-      act[t] = c;
+    for (int t = 0; t < steps; ++t) {
+      while (c > 0 && run_off_host[c] - run_off_host[c - 1] <= t) --c;
+      h_act[t] = c;
+      h_act1[t] = std::min(c, split);
+      if (t < steps2) h_act2[t] = c - split;
     }
   }
-  int* stage = e.h_stage + (size_t)k * e.stage_ints();
-  std::memcpy(stage, slot_ids_host, (size_t)n_runs * 4);
-  std::memcpy(stage + n_runs, run_off_host, (size_t)(n_runs + 1) * 4);
-  std::memcpy(stage + 2 * n_runs + 1, act.data(), act.size() * 4);
-  HK_CHECK_HIP(hipMemcpyAsync(e.d_slots, stage, (size_t)n_runs * 4, hipMemcpyHostToDevice, s));
-  HK_CHECK_HIP(
-      hipMemcpyAsync(e.d_off, stage + n_runs, (size_t)(n_runs + 1) * 4, hipMemcpyHostToDevice, s));
-  HK_CHECK_HIP(hipMemcpyAsync(e.d_act, stage + 2 * n_runs + 1, act.size() * 4,
-                              hipMemcpyHostToDevice, s));
+  for (int i = split; i <= n_runs; ++i) h_off2[i - split] = run_off_host[i] - row_split;
+  HK_CHECK_HIP(hipMemcpyAsync(e.d_desc, stage, (size_t)e.stage_ints() * 4, hipMemcpyHostToDevice,
+                              s));
   HK_CHECK_HIP(hipEventRecord(e.stage_done[k], s));
-  hk::Runs r{e.d_slots, e.d_off, n_runs, n_rows};
+
+  hk::Group all;
+  all.r = hk::Runs{e.d_slots, e.d_off, n_runs, n_rows};
+  all.act_dev = e.d_act;
+  all.act.assign(h_act, h_act + steps);
   HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, s));
   HK_CHECK_HIP(hipEventRecord(e.fork_ev, s));
-  for (int t = 0; t < hk::kTowers; ++t) {
-    hipStream_t ts = e.tstream[t];
-    HK_CHECK_HIP(hipStreamWaitEvent(ts, e.fork_ev, 0));
-    HK_TRY(hk::run_tower(e, t, r, act, preds_dev, ts));
-    HK_CHECK_HIP(hipEventRecord(e.join_ev[t], ts));
+  for (int i = 0; i < Engine::kSide; ++i) HK_CHECK_HIP(hipStreamWaitEvent(e.side[i], e.fork_ev, 0));
+  // Mamba2 on side[1]; RetNet then Hawk on side[2].
+  HK_TRY(hk::run_tower(e, hk::kMamba2, all, preds_dev, e.side[1]));
+  HK_TRY(hk::run_tower(e, hk::kRetNet, all, preds_dev, e.side[2]));
+  HK_TRY(hk::run_tower(e, hk::kHawk, all, preds_dev, e.side[2]));
+  if (split < n_runs) {
+    hk::Group g1, g2;
+    g1.r = hk::Runs{e.d_slots, e.d_off, split, row_split};
+    g1.act_dev = e.d_act1;
+    g1.act.assign(h_act1, h_act1 + steps);
+    g2.r = hk::Runs{e.d_slots + split, e.d_off2, n_runs - split, n_rows - row_split};
+    g2.act_dev = e.d_act2;
+    g2.act.assign(h_act2, h_act2 + steps2);
+    g2.row0 = row_split;
+    HK_TRY(hk::run_xlstm_split(e, g1, s, g2, e.side[0], preds_dev));
+  } else {
+    HK_TRY(hk::run_tower(e, hk::kXLSTM, all, preds_dev, s));
   }
-  for (int t = 0; t < hk::kTowers; ++t) HK_CHECK_HIP(hipStreamWaitEvent(s, e.join_ev[t], 0));
+  for (int i = 0; i < Engine::kSide; ++i) {
+    HK_CHECK_HIP(hipEventRecord(e.join_ev[i], e.side[i]));
+    HK_CHECK_HIP(hipStreamWaitEvent(s, e.join_ev[i], 0));
+  }
   return HK_OK;
 }
 
