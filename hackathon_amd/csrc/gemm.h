@@ -45,7 +45,7 @@ struct GemmWorkspace {
   int64_t partial_elems = 0;
 };
 
-// K must be a multiple of 32 (bf16) or 16 (fp32); lda/ldw multiples of 8 / 4.
+// K must be a multiple of 64 (bf16) or 16 (fp32); lda/ldw multiples of 8 / 4.
 int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int splits_hint = 0);
 
 }  // namespace hk

@@ -2,10 +2,11 @@
 //
 // 64x64 output tile per 256-thread work-group, 4 wave64s in a 2x2 layout,
 // each wave owning a 32x32 sub-tile = 2x2 MFMA 16x16 fragments. K advances in
-// 64-byte slabs (32 bf16 or 16 fp32) staged through LDS; the next slab is
-// fetched into registers while the current one is multiplied. Rows are padded
-// by 16 bytes in LDS so the 16-byte fragment reads of one wave spread over
-// the banks.
+// 128-byte slabs (64 bf16 or 32 fp32) through a ring of eight slabs in
+// registers (the memory latency is covered by bytes in flight, not by
+// occupancy: at M <= 256 there is about one work-group per CU) and two LDS
+// stages with one barrier per slab. Rows are padded by 16 bytes in LDS so the
+// 16-byte fragment reads of one wave spread over the banks.
 //
 // The flat work-group id is remapped so that consecutive tiles (the M tiles
 // that share one slab of W) land on the same XCD and therefore the same L2:
@@ -25,18 +26,23 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 64;
 constexpr int BN = 64;
+#ifndef HK_GEMM_STAGES
+#define HK_GEMM_STAGES 4
+#endif
+constexpr int kStages = HK_GEMM_STAGES;  // LDS ring depth (16 KB per stage)
 
 template <GemmType T>
 struct Tr;
 template <>
 struct Tr<GemmType::kBF16> {
   using E = uint16_t;
-  static constexpr int BK = 32;
+  static constexpr int BK = 64;       // 128-byte slab rows
 };
 template <>
 struct Tr<GemmType::kF32> {
   using E = float;
-  static constexpr int BK = 16;
+  static constexpr int BK = 32;       // 128-byte slab rows
+  static constexpr int BK_NARROW = 16;  // for K a multiple of 16 only
 };
 
 __device__ __forceinline__ void apply_store(const GemmEpilogue& ep, float v, int m, int nc) {
@@ -48,15 +54,57 @@ __device__ __forceinline__ void apply_store(const GemmEpilogue& ep, float v, int
   if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_bf16_bits(v);
 }
 
-template <GemmType T>
+typedef const __attribute__((address_space(1))) void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+// LDS address (byte offset) of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16-byte LDS read issued as inline asm: LDS written by global_load_lds
+// transfers is outside what the compiler can order exactly across the
+// pipelined loop (it would wait for every transfer in flight before each
+// read), so the reads are hidden from it and ordered by hand: the transfers
+// by the counted vmcnt wait before the stage's barrier, the reads by
+// ds_wait4 below, which also ties the read registers to their uses.
+__device__ __forceinline__ u32x4 ds_read16(uint32_t addr) {
+  u32x4 v;
+  __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ void ds_wait4(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : : "memory");
+}
+
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <GemmType T, int BK, int S>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, int splits,
                                                     int tiles_m, int tiles_n) {
   using E = typename Tr<T>::E;
-  constexpr int BK = Tr<T>::BK;
-  constexpr int EPC = 16 / sizeof(E);     // elements per 16-byte chunk
-  constexpr int LROW = BK + EPC;          // padded LDS row, elements
-  __shared__ __align__(16) E As[BM * LROW];
-  __shared__ __align__(16) E Bs[BN * LROW];
+  constexpr int EPC = 16 / sizeof(E);   // elements per 16-byte chunk
+  constexpr int CPR = BK / EPC;         // chunks per slab row (8, or 4 when narrow)
+  constexpr int ROWB = CPR * 16;        // bytes per slab row
+  constexpr int OPB = BM * ROWB;        // bytes of one operand's slab
+  constexpr int STB = 2 * OPB;          // one stage: the A and the W slab
+  constexpr int RPC = 64 / CPR;         // slab rows per 1 KB wave transfer
+  constexpr int CPW = BM / RPC / 4;     // transfers per wave per operand
+  constexpr int SWM = CPR - 1;          // swizzle mask
+  constexpr int D = 2 * CPW;            // transfers per wave per slab
+  static_assert(S >= 3 && S <= 6, "stages");
+  // One LDS array per stage: with the stage index a compile-time constant
+  // the compiler can tell a read of one stage from a transfer into another
+  // and adds no wait of its own.
+  __shared__ __align__(16) unsigned char st0[STB], st1[STB], st2[STB], st3[STB], st4[STB],
+      st5[STB];
+  unsigned char* const stage[6] = {st0, st1, st2, st3, st4, st5};
 
   const int nwg = gridDim.x;
   int bid = blockIdx.x;
@@ -70,96 +118,134 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
   const int b = rest / splits;
 
   const int tid = threadIdx.x;
-  const int lrow = tid >> 2;
-  const int lchk = tid & 3;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int m0 = tm * BM;
   const int n0 = tn * BN;
   const E* Ab = static_cast<const E*>(g.A) + (int64_t)b * g.a_bstride;
   const E* Wb = static_cast<const E*>(g.W) + (int64_t)b * g.w_bstride;
-  const int a_row = (m0 + lrow) < g.M ? m0 + lrow : 0;
-  const int w_row = (n0 + lrow) < g.N ? n0 + lrow : 0;
-  const E* a_src = Ab + (int64_t)a_row * g.lda + lchk * EPC;
-  const E* w_src = Wb + (int64_t)w_row * g.ldw + lchk * EPC;
+
+  // Slabs travel global -> LDS directly (global_load_lds_dwordx4): lane l of
+  // a wave's 1 KB transfer lands at byte 16*l, i.e. slab row q*RPC + l/CPR,
+  // physical chunk l % CPR, which holds logical chunk
+  // (l % CPR) ^ ((row >> 1) & SWM). The XOR spreads the 16 rows one MFMA
+  // fragment read touches over distinct banks. Rows past M or N read row 0
+  // (their products reach only outputs that are never stored).
+  const E* a_src[CPW];
+  const E* w_src[CPW];
+  int xoff[CPW];  // LDS byte offset of the wave's transfer within an operand slab
+#pragma unroll
+  for (int h = 0; h < CPW; ++h) {
+    const int q = wave * CPW + h;
+    const int row = q * RPC + lane / CPR;
+    const int lc = (lane % CPR) ^ ((row >> 1) & SWM);
+    const int ar = m0 + row, wr = n0 + row;
+    a_src[h] = Ab + (int64_t)(ar < g.M ? ar : 0) * g.lda + lc * EPC;
+    w_src[h] = Wb + (int64_t)(wr < g.N ? wr : 0) * g.ldw + lc * EPC;
+    xoff[h] = q * 1024;
+  }
 
   const int ktiles = g.K / BK;
   const int per = (ktiles + splits - 1) / splits;
   const int kt0 = split * per;
   const int kt1 = min(ktiles, kt0 + per);
-
-  // Register ring of kRing K-slabs: the load of slab kt+kRing is issued when
-  // slab kt is consumed, so each load has kRing-1 slabs of MFMA work to land.
-  // The loop is unrolled by kRing so every ring index is a compile-time
-  // constant (the ring stays in VGPRs), and the barriers wait on LDS only.
-  constexpr int kRing = 4;
-  // Loads are unconditional so the wait counts stay static: rows past M or N
-  // read row 0 (their products land only in output rows/columns that are
-  // never stored), and slabs past the split's end re-read its last slab.
+  const int nslab = max(kt1 - kt0, 0);
   const int kt_last = max(kt1 - 1, 0);
-  u32x4 ra[kRing], rw[kRing];
+  // Every slab issues exactly D transfers per wave (past the end: the last
+  // slab again, into a stage never read), so the counted waits are exact.
+  auto issue = [&](unsigned char* st, int kt) {
 #pragma unroll
-  for (int j = 0; j < kRing; ++j) {
-    const int kt = min(kt0 + j, kt_last);
-    ra[j] = gload16(a_src + (int64_t)kt * BK);
-    rw[j] = gload16(w_src + (int64_t)kt * BK);
-  }
+    for (int h = 0; h < CPW; ++h) {
+      __builtin_amdgcn_global_load_lds((gptr_t)(a_src[h] + (int64_t)kt * BK),
+                                       (lptr_t)(st + xoff[h]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gptr_t)(w_src[h] + (int64_t)kt * BK),
+                                       (lptr_t)(st + OPB + xoff[h]), 16, 0, 0);
+    }
+  };
 
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
   const int fr = lane & 15;   // fragment row (A) / column (B)
   const int fk = lane >> 4;   // k group within the MFMA
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  // Byte offsets of this lane's fragment rows within a stage, and their
+  // swizzle keys.
+  uint32_t arow[2], brow[2];
+  int akey[2], bkey[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ra = wm * 32 + i * 16 + fr, rb = wn * 32 + i * 16 + fr;
+    arow[i] = ra * ROWB;
+    brow[i] = OPB + rb * ROWB;
+    akey[i] = (ra >> 1) & SWM;
+    bkey[i] = (rb >> 1) & SWM;
+  }
   floatx4 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int kb = kt0; kb < kt1; kb += kRing) {
 #pragma unroll
-    for (int j = 0; j < kRing; ++j) {
-      const int kt = kb + j;
-      if (kt < kt1) {
-        *reinterpret_cast<u32x4*>(&As[lrow * LROW + lchk * EPC]) = ra[j];
-        *reinterpret_cast<u32x4*>(&Bs[lrow * LROW + lchk * EPC]) = rw[j];
-        lds_barrier();
-        {
-          const int nk = min(kt + kRing, kt_last);
-          ra[j] = gload16(a_src + (int64_t)nk * BK);
-          rw[j] = gload16(w_src + (int64_t)nk * BK);
-        }
-        if constexpr (T == GemmType::kBF16) {
-          bf16x8 af[2], bfr[2];
+  for (int s2 = 0; s2 < S - 1; ++s2) issue(stage[s2], min(kt0 + s2, kt_last));
+
+  for (int kb = 0; kb < nslab; kb += S) {
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
-            af[i] = *reinterpret_cast<const bf16x8*>(&As[(wm * 32 + i * 16 + fr) * LROW + fk * 8]);
+    for (int j = 0; j < S; ++j) {
+      const int i = kb + j;
+      if (i < nslab) {
+        // Slab i is complete once at most the S-2 later slabs' transfers are
+        // outstanding; the barrier then also shows every wave's transfers and
+        // retires all reads of stage (j - 1) mod S, the next transfer's target.
+        // (A raw s_barrier: a workgroup fence would also wait for every LDS
+        // transfer in flight. The empty asm blocks keep LDS accesses from
+        // moving across it; earlier reads have retired before their MFMAs.)
+        wait_vmcnt<(S - 2) * D>();
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        issue(stage[(j + S - 1) % S], min(kt0 + i + S - 1, kt_last));
+        const uint32_t st = lds_addr(stage[j]);
 #pragma unroll
-          for (int q = 0; q < 2; ++q)
-            bfr[q] = *reinterpret_cast<const bf16x8*>(&Bs[(wn * 32 + q * 16 + fr) * LROW + fk * 8]);
+        for (int ks = 0; ks < BK * (int)sizeof(E) / 64; ++ks) {
+          // Four 16-byte fragment reads (A rows i, B columns i) of one
+          // 64-byte k step, issued together; see ds_read16.
+          u32x4 fa0 = ds_read16(st + arow[0] + (((ks * 4 + fk) ^ akey[0]) << 4));
+          u32x4 fa1 = ds_read16(st + arow[1] + (((ks * 4 + fk) ^ akey[1]) << 4));
+          u32x4 fb0 = ds_read16(st + brow[0] + (((ks * 4 + fk) ^ bkey[0]) << 4));
+          u32x4 fb1 = ds_read16(st + brow[1] + (((ks * 4 + fk) ^ bkey[1]) << 4));
+          ds_wait4(fa0, fa1, fb0, fb1);
+          const u32x4 fa[2] = {fa0, fa1}, fb[2] = {fb0, fb1};
+          if constexpr (T == GemmType::kBF16) {
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-              acc[i][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[q], acc[i][q], 0, 0, 0);
-        } else {
-#pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) {
-            float af[2], bfr[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) af[i] = As[(wm * 32 + i * 16 + fr) * LROW + s4 * 4 + fk];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) bfr[q] = Bs[(wn * 32 + q * 16 + fr) * LROW + s4 * 4 + fk];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
               for (int q = 0; q < 2; ++q)
-                acc[i][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bfr[q], acc[i][q], 0, 0, 0);
+                acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, fa[ii]), __builtin_bit_cast(bf16x8, fb[q]),
+                    acc[ii][q], 0, 0, 0);
+          } else {
+            // k-step (ks, c) of a lane in k group fk covers k = 16*ks + 4*fk
+            // + c for A and B alike, so one 16-byte read feeds four MFMAs.
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+              const floatx4 av = __builtin_bit_cast(floatx4, fa[ii]);
+#pragma unroll
+              for (int q = 0; q < 2; ++q) {
+                const floatx4 bv = __builtin_bit_cast(floatx4, fb[q]);
+                acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc[ii][q], 0, 0, 0);
+                acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc[ii][q], 0, 0, 0);
+                acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc[ii][q], 0, 0, 0);
+                acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc[ii][q], 0, 0, 0);
+              }
+            }
           }
         }
-        lds_barrier();
       }
     }
   }
+  // Transfers past the end may still be in flight into this work-group's
+  // LDS: drain them before the work-group can retire.
+  wait_vmcnt<0>();
 
   // Fragment (i, j): lane holds rows 4*fk + e, column fr.
 #pragma unroll
@@ -205,7 +291,10 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
   HK_REQUIRE(g.A && g.W && (g.ep.out || g.ep.out_lp), "gemm: null operand");
   HK_REQUIRE(g.M >= 0 && g.N > 0 && g.K > 0 && g.batch > 0, "gemm: bad shape M=%d N=%d K=%d",
              g.M, g.N, g.K);
-  const int BK = g.type == GemmType::kBF16 ? Tr<GemmType::kBF16>::BK : Tr<GemmType::kF32>::BK;
+  const bool narrow = g.type == GemmType::kF32 && g.K % Tr<GemmType::kF32>::BK != 0;
+  const int BK = g.type == GemmType::kBF16 ? Tr<GemmType::kBF16>::BK
+                 : narrow                  ? Tr<GemmType::kF32>::BK_NARROW
+                                           : Tr<GemmType::kF32>::BK;
   const int align = g.type == GemmType::kBF16 ? 8 : 4;
   HK_REQUIRE(g.K % BK == 0, "gemm: K=%d is not a multiple of %d", g.K, BK);
   HK_REQUIRE(g.lda % align == 0 && g.ldw % align == 0 && g.a_bstride % align == 0 &&
@@ -218,8 +307,10 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
   const int ktiles = g.K / BK;
   int splits = splits_hint;
   if (splits <= 0) {
-    splits = (int)((1024 + tiles - 1) / tiles);
-    splits = std::min(splits, std::max(1, ktiles / 4));
+    // About one work-group per CU (the slab ring covers the latency), each
+    // split at least 8 slabs long.
+    splits = (int)((256 + tiles - 1) / tiles);
+    splits = std::min(splits, std::max(1, ktiles / 8));
     splits = std::min(splits, 32);
   }
   splits = std::max(1, std::min(splits, ktiles));
@@ -227,11 +318,17 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
   const int64_t nwg = tiles * splits;
   HK_REQUIRE(nwg < (1LL << 31), "gemm: grid too large");
   if (g.type == GemmType::kBF16) {
-    hipLaunchKernelGGL(gemm_kernel<GemmType::kBF16>, dim3((unsigned)nwg), dim3(256), 0, stream,
-                       g, ws.partial, splits, tiles_m, tiles_n);
+    hipLaunchKernelGGL((gemm_kernel<GemmType::kBF16, Tr<GemmType::kBF16>::BK, kStages>),
+                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, splits, tiles_m,
+                       tiles_n);
+  } else if (!narrow) {
+    hipLaunchKernelGGL((gemm_kernel<GemmType::kF32, Tr<GemmType::kF32>::BK, kStages>),
+                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, splits, tiles_m,
+                       tiles_n);
   } else {
-    hipLaunchKernelGGL(gemm_kernel<GemmType::kF32>, dim3((unsigned)nwg), dim3(256), 0, stream, g,
-                       ws.partial, splits, tiles_m, tiles_n);
+    hipLaunchKernelGGL((gemm_kernel<GemmType::kF32, Tr<GemmType::kF32>::BK_NARROW, kStages>),
+                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, splits, tiles_m,
+                       tiles_n);
   }
   HK_LAUNCH_CHECK();
   if (splits > 1) {
