@@ -45,8 +45,9 @@ struct Tr<GemmType::kF32> {
   static constexpr int BK_NARROW = 16;  // for K a multiple of 16 only
 };
 
-__device__ __forceinline__ void apply_store(const GemmEpilogue& ep, float v, int m, int nc) {
-  if (ep.bias) v += ep.bias[nc];
+__device__ __forceinline__ void apply_store(const GemmEpilogue& ep, float v, int m, int nc,
+                                            bool add_bias = true) {
+  if (add_bias && ep.bias) v += ep.bias[nc];
   if (ep.round_lp) v = round_bf16(v);
   if (ep.act == 1) v = fmaxf(v, 0.0f);
   if (ep.residual) v += ep.residual[(int64_t)m * ep.ldr + nc];
@@ -83,6 +84,23 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// vmcnt(k * D) for a runtime k in [0, S-2].
+template <int D, int S>
+__device__ __forceinline__ void wait_slabs(int k) {
+  static_assert(S <= 6, "stages");
+  if (k >= S - 2) {
+    wait_vmcnt<(S - 2) * D>();
+  } else if (k == 3) {
+    wait_vmcnt<3 * D>();
+  } else if (k == 2) {
+    wait_vmcnt<2 * D>();
+  } else if (k == 1) {
+    wait_vmcnt<D>();
+  } else {
+    wait_vmcnt<0>();
+  }
 }
 
 template <GemmType T, int BK, int S>
@@ -150,9 +168,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
   const int kt0 = split * per;
   const int kt1 = min(ktiles, kt0 + per);
   const int nslab = max(kt1 - kt0, 0);
-  const int kt_last = max(kt1 - 1, 0);
-  // Every slab issues exactly D transfers per wave (past the end: the last
-  // slab again, into a stage never read), so the counted waits are exact.
+  // Every slab is D transfers per wave; the wait before slab i allows the
+  // transfers of the slabs issued after it (at most S-2) to stay in flight.
   auto issue = [&](unsigned char* st, int kt) {
 #pragma unroll
     for (int h = 0; h < CPW; ++h) {
@@ -185,8 +202,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // The bias of this lane's two output columns, fetched before the slabs
+  // (older than every transfer, so the counted waits cover it too).
+  float bias_v[2] = {0.0f, 0.0f};
+  if (splits == 1 && g.ep.bias) {
 #pragma unroll
-  for (int s2 = 0; s2 < S - 1; ++s2) issue(stage[s2], min(kt0 + s2, kt_last));
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn * 32 + j * 16 + fr;
+      if (n < g.N) bias_v[j] = g.ep.bias[n + (int)((int64_t)b * g.c_bstride)];
+    }
+  }
+
+#pragma unroll
+  for (int s2 = 0; s2 < S - 1; ++s2)
+    if (s2 < nslab) issue(stage[s2], kt0 + s2);
 
   for (int kb = 0; kb < nslab; kb += S) {
 #pragma unroll
@@ -199,11 +228,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
         // (A raw s_barrier: a workgroup fence would also wait for every LDS
         // transfer in flight. The empty asm blocks keep LDS accesses from
         // moving across it; earlier reads have retired before their MFMAs.)
-        wait_vmcnt<(S - 2) * D>();
+        wait_slabs<D, S>(min(S - 2, nslab - 1 - i));
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
-        issue(stage[(j + S - 1) % S], min(kt0 + i + S - 1, kt_last));
+        if (i + S - 1 < nslab) issue(stage[(j + S - 1) % S], kt0 + i + S - 1);
         const uint32_t st = lds_addr(stage[j]);
 #pragma unroll
         for (int ks = 0; ks < BK * (int)sizeof(E) / 64; ++ks) {
@@ -243,26 +272,69 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
       }
     }
   }
-  // Transfers past the end may still be in flight into this work-group's
-  // LDS: drain them before the work-group can retire.
-  wait_vmcnt<0>();
+  // (Every transfer was waited for before its slab; nothing is in flight.)
 
   // Fragment (i, j): lane holds rows 4*fk + e, column fr.
+  if (splits == 1) {
+    // All residual reads before any store: the residual may be the output
+    // itself (x += f(x)); element by element in place is exact, and issuing
+    // the reads first avoids a store-to-load ordering wait per element.
+    const GemmEpilogue& ep = g.ep;
+    float res[2][2][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn * 32 + j * 16 + fr;
-      if (n >= g.N) continue;
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
-        if (m >= g.M) continue;
-        const float v = acc[i][j][e];
-        if (splits == 1) {
-          apply_store(g.ep, v, m, n + (int)((int64_t)b * g.c_bstride));
-        } else {
-          partial[(((int64_t)b * splits + split) * g.M + m) * g.N + n] = v;
+        for (int e = 0; e < 4; ++e) {
+          const int n = n0 + wn * 32 + j * 16 + fr;
+          const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
+          res[i][j][e] = (ep.residual && n < g.N && m < g.M)
+                             ? ep.residual[(int64_t)m * ep.ldr + n + (int64_t)b * g.c_bstride]
+                             : 0.0f;
+        }
+    // Every value first, then every store (no register of a pending store
+    // is rewritten while stores are in flight).
+    float outv[2][2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[i][j][e] + bias_v[j];
+          if (ep.round_lp) v = round_bf16(v);
+          if (ep.act == 1) v = fmaxf(v, 0.0f);
+          outv[i][j][e] = v + res[i][j][e];
+        }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 32 + j * 16 + fr;
+        if (n >= g.N) continue;
+        const int nc = n + (int)((int64_t)b * g.c_bstride);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
+          if (m >= g.M) continue;
+          if (ep.out) ep.out[(int64_t)m * ep.ldo + nc] = outv[i][j][e];
+          if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_bf16_bits(outv[i][j][e]);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 32 + j * 16 + fr;
+        if (n >= g.N) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
+          if (m >= g.M) continue;
+          partial[(((int64_t)b * splits + split) * g.M + m) * g.N + n] = acc[i][j][e];
         }
       }
     }
