@@ -20,8 +20,12 @@ constexpr int kSteps = 8;  // steps whose row vectors are staged per LDS block
 // NW waves split the tile's rows (RPW each); every lane owns VW adjacent
 // columns, so a work-group covers 64*VW columns and each wave instruction
 // moves 256*VW contiguous bytes of a state row.
+// The 512-row tile (8 waves x 64 rows) is held to 128 VGPRs (4 waves per
+// SIMD) so that two work-groups share a CU: one streams its state tile in or
+// out while the other computes.
 template <int RPW, int NW, int VW, bool VEC>
-__global__ __launch_bounds__(64 * NW) void mat_scan_kernel(MatScanDesc d) {
+__global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_scan_kernel(
+    MatScanDesc d) {
   constexpr int kRows = NW * RPW;
   constexpr int NT = 64 * NW;
   constexpr int CW = 64 * VW;  // columns per work-group
