@@ -468,24 +468,30 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
   return timed(e, 4, s, [&] { return gemm(g, w.gemm_ws, s); });
 }
 
-// Block-diagonal fp32 product (BlockLinear, model/modules.py:71-79):
-// out[:, b*bs + k] = sum_h x[:, b*bs + h] * W[b][k][h], for b < blocks.
-int block_linear(Engine& e, TowerWS& w, const float* x, int64_t ldx, const float* W, int blocks, int bs,
-                 int M, const float* bias, float* out, int64_t ldo, hipStream_t s) {
+// Block-diagonal fp32 products (BlockLinear, model/modules.py:71-79), several
+// in one launch: batch b = j * blocks + k is block k of product j, reading x
+// (or x2 for j >= x2_from) and W[b] = W + b*bs*bs, writing out columns
+// b*bs .. b*bs + bs - 1:
+//   out[:, b*bs + o] = sum_h src[:, k*bs + h] * W[b][o][h].
+int block_linear(Engine& e, TowerWS& w, const float* x, const float* x2, int x2_from, int64_t ldx,
+                 const float* W, int products, int blocks, int bs, int M, float* out, int64_t ldo,
+                 hipStream_t s) {
   GemmArgs g;
   g.type = GemmType::kF32;
   g.A = x;
+  g.A2 = x2;
+  g.a2_from = x2 ? x2_from * blocks : 0;
+  g.a_period = blocks;
   g.lda = ldx;
   g.W = W;
   g.ldw = bs;
   g.M = M;
   g.N = bs;
   g.K = bs;
-  g.batch = blocks;
+  g.batch = products * blocks;
   g.a_bstride = bs;
   g.w_bstride = (int64_t)bs * bs;
   g.c_bstride = bs;
-  g.ep.bias = bias;
   g.ep.out = out;
   g.ep.ldo = ldo;
   return timed(e, 4, s, [&] { return gemm(g, w.gemm_ws, s); });
@@ -536,12 +542,9 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   HK_TRY(layernorm_rows(w.A.f, F32(e, kXLSTM, l, X_S_NORM), nullptr, n, H, w.XN, nullptr, s));
   HK_TRY(conv_scan(r, w.XN, H, H, st[XS_S_CONV], le[XS_S_CONV], F32(e, kXLSTM, l, X_S_CONV_W),
                    F32(e, kXLSTM, l, X_S_CONV_B), 1, w.XCA, H, s));
-  const float* win = F32(e, kXLSTM, l, X_S_IN_W);
-  for (int g = 0; g < 4; ++g) {  // i, f from the conv path; z, o from LN(x)
-    const float* src = g < 2 ? w.XCA : w.XN;
-    HK_TRY(block_linear(e, w, src, H, win + (int64_t)g * H * d.bs_s, d.nh_s, d.bs_s, n, nullptr,
-                        w.GIN + (int64_t)g * H, 4 * H, s));
-  }
+  // i, f from the conv path, z, o from LN(x): one launch of 4 x nh_s blocks
+  HK_TRY(block_linear(e, w, w.XCA, w.XN, 2, H, F32(e, kXLSTM, l, X_S_IN_W), 4, d.nh_s, d.bs_s, n,
+                      w.GIN, 4 * H, s));
   if (slstm_persist_supported(H, d.nh_s)) {
     if (ord.wait) HK_CHECK_HIP(hipStreamWaitEvent(s, ord.wait, 0));
     if (++e.xch_tag == 0) {
@@ -710,10 +713,9 @@ int run_hawk(Engine& e, int l, const Runs& r, hipStream_t s) {
                 w.GRP, 2 * H, nullptr, 0, s));
   HK_TRY(conv_scan(r, w.GRP + H, 2 * H, H, st[KS_CONV], le[KS_CONV], F32(e, kHawk, l, K_CONV_W),
                    F32(e, kHawk, l, K_CONV_B), 0, w.KXC, H, s));
-  const float* gw = F32(e, kHawk, l, K_GATES_W);
-  for (int g = 0; g < 2; ++g)
-    HK_TRY(block_linear(e, w, w.KXC, H, gw + (int64_t)g * H * d.bs_h, d.nb_h, d.bs_h, n, nullptr,
-                        w.GATES + (int64_t)g * H, 2 * H, s));
+  // input and recurrence gates of the RG-LRU, one launch of 2 x nb_h blocks
+  HK_TRY(block_linear(e, w, w.KXC, nullptr, 0, H, F32(e, kHawk, l, K_GATES_W), 2, d.nb_h, d.bs_h,
+                      n, w.GATES, 2 * H, s));
   HK_TRY(rglru_scan(r, w.KXC, w.GATES, w.GATES + H, 2 * H, w.GRP, 2 * H, F32(e, kHawk, l, K_A),
                     8.0f, H, st[KS_H], w.GH.f, w.GH.l, s));
   HK_TRY(linear(e, w, w.GH, H, {S(e, kHawk, l, K_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f, H,

@@ -37,6 +37,12 @@ struct GemmArgs {
   // b*w_bstride, and writes columns offset by b*c_bstride.
   int batch = 1;
   int64_t a_bstride = 0, w_bstride = 0, c_bstride = 0;
+  // Optional, for batches of blocks over two inputs: batch b >= a2_from
+  // reads A2 instead of A, and with a_period > 0 the A offset is
+  // (b % a_period) * a_bstride (W and the output still step by b).
+  const void* A2 = nullptr;
+  int a2_from = 0;
+  int a_period = 0;
   GemmEpilogue ep;
 };
 

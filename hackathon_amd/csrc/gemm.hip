@@ -140,7 +140,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
   const int wave = tid >> 6;
   const int m0 = tm * BM;
   const int n0 = tn * BN;
-  const E* Ab = static_cast<const E*>(g.A) + (int64_t)b * g.a_bstride;
+  const void* Asrc = (g.A2 != nullptr && b >= g.a2_from) ? g.A2 : g.A;
+  const E* Ab = static_cast<const E*>(Asrc) +
+                (int64_t)(g.a_period > 0 ? b % g.a_period : b) * g.a_bstride;
   const E* Wb = static_cast<const E*>(g.W) + (int64_t)b * g.w_bstride;
 
   // Slabs travel global -> LDS directly (global_load_lds_dwordx4): lane l of
@@ -361,6 +363,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, const fl
 
 int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int splits_hint) {
   HK_REQUIRE(g.A && g.W && (g.ep.out || g.ep.out_lp), "gemm: null operand");
+  HK_REQUIRE(g.a_period >= 0 && g.a2_from >= 0, "gemm: bad batch-source description");
   HK_REQUIRE(g.M >= 0 && g.N > 0 && g.K > 0 && g.batch > 0, "gemm: bad shape M=%d N=%d K=%d",
              g.M, g.N, g.K);
   const bool narrow = g.type == GemmType::kF32 && g.K % Tr<GemmType::kF32>::BK != 0;
