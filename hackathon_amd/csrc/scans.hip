@@ -576,60 +576,90 @@ __global__ void slstm_final_kernel(const int* __restrict__ slot_ids,
     h_state[(int64_t)slot * hidden + c] = y[(int64_t)last * hidden + c];
 }
 
-// grid (runs, heads); 256 threads over the head's hs elements of n.
+// mLSTM gate / normaliser recurrence, one wave per (run, head): lane l holds
+// n[e*64 + l] for e < PER (hs <= 64*PER); steps in order, as the reference.
+// The step's q and k rows and gate pre-activations come from a ring of
+// kGateRing prefetched steps in registers (refilled unconditionally with
+// clamped rows, so the compiler's wait counts stay exact), hiding the load
+// latency that a run of many steps would otherwise pay at every step.
+constexpr int kGateRing = 8;
+template <int PER>
 __global__ __launch_bounds__(256) void mlstm_gates_kernel(
-    const int* __restrict__ slot_ids, const int* __restrict__ run_off,
+    const int* __restrict__ slot_ids, const int* __restrict__ run_off, int n_runs,
     const float* __restrict__ if_pre, int heads, const float* __restrict__ qkv, int inner,
     const float* __restrict__ ks, float* __restrict__ n_state, float* __restrict__ m_state,
     float* __restrict__ ig_out, float* __restrict__ fg_out, float* __restrict__ den_out) {
-  __shared__ float red[4];
-  constexpr int kMaxPer = 8;  // head size <= 2048
-  const int run = blockIdx.x;
-  const int head = blockIdx.y;
-  const int hs = inner / heads;
+  const int lane = threadIdx.x & 63;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= n_runs * heads) return;  // whole wave
+  const int run = pair / heads;
+  const int head = pair - run * heads;
+  const int hs = inner / heads;  // at most 64 * PER; lanes past it hold zeros
   const int slot = slot_ids[run];
   const int r0 = run_off[run];
-  const int r1 = run_off[run + 1];
+  const int len = run_off[run + 1] - r0;
+  const int rl = r0 + len - 1;
   float* nst = n_state + ((int64_t)slot * heads + head) * hs;
-  float nv[kMaxPer];
+  // element e*64 + lane of the head; past hs: clamped loads, zero values
+  int hidx[PER];
+  float ok[PER];
 #pragma unroll
-  for (int i = 0; i < kMaxPer; ++i) {
-    const int h = threadIdx.x + i * 256;
-    nv[i] = h < hs ? nst[h] : 0.0f;
+  for (int e = 0; e < PER; ++e) {
+    const int h = e * 64 + lane;
+    hidx[e] = min(h, hs - 1);
+    ok[e] = h < hs ? 1.0f : 0.0f;
   }
+  float nv[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) nv[e] = ok[e] * nst[hidx[e]];
   float m = m_state[(int64_t)slot * heads + head];
-  for (int r = r0; r < r1; ++r) {
-    const float ipre = if_pre[(int64_t)r * 2 * heads + head];
-    const float fpre = if_pre[(int64_t)r * 2 * heads + heads + head];
-    const float log_f = logsigmoid(fpre);
-    const float mn = fmaxf(ipre, m + log_f);
-    const float ig = expf(ipre - mn);
-    const float fg = expf(log_f + m - mn);
-    const float* q = qkv + (int64_t)r * 3 * inner + (int64_t)head * hs;
-    const float* k = ks + (int64_t)r * inner + (int64_t)head * hs;
-    float dot = 0.0f;
+
+  const float* qh = qkv + (int64_t)head * hs;
+  const float* kh = ks + (int64_t)head * hs;
+  float rq[kGateRing][PER], rk[kGateRing][PER], ri[kGateRing], rf[kGateRing];
+  auto fill = [&](int j, int row) {
 #pragma unroll
-    for (int i = 0; i < kMaxPer; ++i) {
-      const int h = threadIdx.x + i * 256;
-      if (h < hs) {
-        nv[i] = fg * nv[i] + ig * k[h];
-        dot += q[h] * nv[i];
+    for (int e = 0; e < PER; ++e) {
+      rq[j][e] = qh[(int64_t)row * 3 * inner + hidx[e]];
+      rk[j][e] = ok[e] * kh[(int64_t)row * inner + hidx[e]];
+    }
+    ri[j] = if_pre[(int64_t)row * 2 * heads + head];
+    rf[j] = if_pre[(int64_t)row * 2 * heads + heads + head];
+  };
+#pragma unroll
+  for (int j = 0; j < kGateRing; ++j) fill(j, min(r0 + j, rl));
+
+  for (int tb = 0; tb < len; tb += kGateRing) {
+#pragma unroll
+    for (int j = 0; j < kGateRing; ++j) {
+      const int t = tb + j;
+      if (t < len) {
+        const float log_f = logsigmoid(rf[j]);
+        const float mn = fmaxf(ri[j], m + log_f);
+        const float ig = expf(ri[j] - mn);
+        const float fg = expf(log_f + m - mn);
+        float dot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          nv[e] = fg * nv[e] + ig * rk[j][e];
+          dot += rq[j][e] * nv[e];
+        }
+        dot = wave_sum(dot);
+        m = mn;
+        if (lane == 0) {
+          const int64_t row = r0 + t;
+          ig_out[row * heads + head] = ig;
+          fg_out[row * heads + head] = fg;
+          den_out[row * heads + head] = fmaxf(fabsf(dot), expf(-mn)) + 1e-6f;
+        }
       }
-    }
-    dot = block_sum(dot, red);
-    m = mn;
-    if (threadIdx.x == 0) {
-      ig_out[(int64_t)r * heads + head] = ig;
-      fg_out[(int64_t)r * heads + head] = fg;
-      den_out[(int64_t)r * heads + head] = fmaxf(fabsf(dot), expf(-mn)) + 1e-6f;
+      fill(j, min(r0 + t + kGateRing, rl));
     }
   }
 #pragma unroll
-  for (int i = 0; i < kMaxPer; ++i) {
-    const int h = threadIdx.x + i * 256;
-    if (h < hs) nst[h] = nv[i];
-  }
-  if (threadIdx.x == 0) m_state[(int64_t)slot * heads + head] = m;
+  for (int e = 0; e < PER; ++e)
+    if (e * 64 + lane < hs) nst[e * 64 + lane] = nv[e];
+  if (lane == 0) m_state[(int64_t)slot * heads + head] = m;
 }
 
 }  // namespace
@@ -760,9 +790,27 @@ int mlstm_gates(const Runs& r, const float* if_pre, int heads, const float* qkv,
                 const float* ks, float* n_state, float* m_state, float* ig, float* fg, float* den,
                 hipStream_t s) {
   if (r.n_runs == 0) return HK_OK;
-  HK_REQUIRE(inner % heads == 0 && inner / heads <= 2048, "mlstm_gates: head size unsupported");
-  hipLaunchKernelGGL(mlstm_gates_kernel, dim3(r.n_runs, heads), dim3(256), 0, s, r.slot_ids,
-                     r.run_off, if_pre, heads, qkv, inner, ks, n_state, m_state, ig, fg, den);
+  const int hs = inner / heads;
+  HK_REQUIRE(inner % heads == 0 && hs >= 1 && hs <= 1024,
+             "mlstm_gates: head size %d unsupported (at most 1024)", hs);
+  const int pairs = r.n_runs * heads;
+  const dim3 grid((pairs + 3) / 4), block(256);
+  const int per = (hs + 63) / 64;
+#define HK_GATES(P)                                                                          \
+  hipLaunchKernelGGL(mlstm_gates_kernel<P>, grid, block, 0, s, r.slot_ids, r.run_off, r.n_runs, \
+                     if_pre, heads, qkv, inner, ks, n_state, m_state, ig, fg, den)
+  if (per <= 1) {
+    HK_GATES(1);
+  } else if (per <= 2) {
+    HK_GATES(2);
+  } else if (per <= 4) {
+    HK_GATES(4);
+  } else if (per <= 8) {
+    HK_GATES(8);
+  } else {
+    HK_GATES(16);
+  }
+#undef HK_GATES
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
