@@ -539,7 +539,7 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   float** st = e.state[kXLSTM][l].data();
   const int64_t* le = e.leaf_elems[kXLSTM].data();
   // sLSTM block (model/xlstm.py:400-424); its input and skip is A = norm1(x).
-  HK_TRY(layernorm_rows(w.A.f, F32(e, kXLSTM, l, X_S_NORM), nullptr, n, H, w.XN, nullptr, s));
+  // (XN = LayerNorm(A) * slstm.norm was computed with A by tower_layer.)
   HK_TRY(conv_scan(r, w.XN, H, H, st[XS_S_CONV], le[XS_S_CONV], F32(e, kXLSTM, l, X_S_CONV_W),
                    F32(e, kXLSTM, l, X_S_CONV_B), 1, w.XCA, H, s));
   // i, f from the conv path, z, o from LN(x): one launch of 4 x nh_s blocks
@@ -610,8 +610,8 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
                     w.HS.l, s));
   HK_TRY(linear(e, w, w.HS, I, {S(e, kXLSTM, l, X_L_DOWN_W), nullptr}, n, H, I, 0, w.X1, H, w.X2,
                 H, nullptr, 0, s));
-  // final_norm, then the Block's residual: x = final_norm(x2) + x.
-  HK_TRY(layernorm_rows(w.X2, F32(e, kXLSTM, l, X_F_NORM), w.X.f, n, H, w.X.f, nullptr, s));
+  // final_norm and the Block's residual (x = final_norm(x2) + x) are applied
+  // by tower_layer together with the next RMSNorm.
   return HK_OK;
 }
 
@@ -741,16 +741,27 @@ int tower_layer(Engine& e, int t, TowerWS& w, const Group& g, int l, unsigned lo
   const Dims& d = e.d;
   const int n = g.r.n_rows;
   const int H = d.H, P = d.P;
-  HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM1), 1.1920928955078125e-07f, n, H, w.A.f, H,
-                      w.A.l, H, s));
+  constexpr float kRmsEps = 1.1920928955078125e-07f;  // torch.finfo(float32).eps
+  if (t == kXLSTM) {
+    // A = RMSNorm(x); XN = slstm.norm(A) (model/xlstm.py:314)
+    HK_TRY(rms_ln_rows(w.X.f, F32(e, t, l, B_NORM1), kRmsEps, F32(e, t, l, X_S_NORM), n, H, w.A.f,
+                       w.A.l, w.XN, s));
+  } else {
+    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM1), kRmsEps, n, H, w.A.f, H, w.A.l, H, s));
+  }
   switch (t) {
     case kXLSTM: HK_TRY(run_xlstm(e, w, l, g, xch, ord, s)); break;
     case kMamba2: HK_TRY(run_mamba2(e, l, g.r, s)); break;
     case kRetNet: HK_TRY(run_retnet(e, l, g.r, s)); break;
     default: HK_TRY(run_hawk(e, l, g.r, s)); break;
   }
-  HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM2), 1.1920928955078125e-07f, n, H, w.A.f, H,
-                      w.A.l, H, s));
+  if (t == kXLSTM) {
+    // x = final_norm(x2) + x (model/xlstm.py:365, inference_model.py:66); A = RMSNorm(x)
+    HK_TRY(ln_res_rms_rows(w.X2, F32(e, t, l, X_F_NORM), w.X.f, F32(e, t, l, B_NORM2), kRmsEps, n,
+                           H, w.A.f, w.A.l, s));
+  } else {
+    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM2), kRmsEps, n, H, w.A.f, H, w.A.l, H, s));
+  }
   HK_TRY(linear(e, w, w.A, H, {S(e, t, l, B_FC1_W), S(e, t, l, B_FC1_B)}, n, P, H, 1, nullptr, 0,
                 w.H1.f, P, w.H1.l, P, s));
   return linear(e, w, w.H1, P, {S(e, t, l, B_FC2_W), S(e, t, l, B_FC2_B)}, n, H, P, 0, w.X.f, H,

@@ -48,6 +48,14 @@ int slstm_post(const float* y, const float* skip, const float* gn_w, const float
                int groups, const float* ln_w, int n_rows, int hidden, float* x1, float* xn,
                uint16_t* xn_lp, hipStream_t s);
 
+// Fused row pairs of the xLSTM block (model/inference_model.py:63-68 around
+// model/xlstm.py:355-367): a = RMSNorm(x) * w_rms, xn = LayerNorm(a) * w_ln;
+// and x = LayerNorm(y) * w_ln + x, a = RMSNorm(x) * w_rms.
+int rms_ln_rows(const float* x, const float* w_rms, float eps, const float* w_ln, int n_rows,
+                int width, float* a, uint16_t* a_lp, float* xn, hipStream_t s);
+int ln_res_rms_rows(const float* y, const float* w_ln, float* x, const float* w_rms, float eps,
+                    int n_rows, int width, float* a, uint16_t* a_lp, hipStream_t s);
+
 // out = LayerNorm(x) * w (+ residual) (no bias; eps 1e-5).
 int layernorm_rows(const float* x, const float* w, const float* residual, int n_rows, int width,
                    float* out, uint16_t* out_lp, hipStream_t s);

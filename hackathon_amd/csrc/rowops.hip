@@ -9,6 +9,42 @@
 namespace hk {
 namespace {
 
+// Row held in registers: thread t owns columns t + 256*i (i < V), loaded
+// together (clamped, masked) before any reduction, so a row costs one load
+// latency instead of one per 256 columns and pass. Per-thread partial sums
+// run in increasing column order, then the block sum.
+template <int V>
+struct RowRegs {
+  float v[V];
+  __device__ __forceinline__ void load(const float* __restrict__ xr, int width) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const float x = xr[min(c, width - 1)];
+      v[i] = c < width ? x : 0.0f;
+    }
+  }
+  __device__ __forceinline__ float sum(int width) const {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (threadIdx.x + 256 * i < width) s += v[i];
+    return s;
+  }
+  __device__ __forceinline__ float sumsq(int width, float mean) const {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (threadIdx.x + 256 * i < width) {
+        const float d = v[i] - mean;
+        s += d * d;
+      }
+    return s;
+  }
+};
+
+// out = x * rsqrt(mean(x^2) + eps) * w
+template <int V>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ w, float eps,
                                                       int width, float* __restrict__ out,
@@ -16,18 +52,110 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
                                                       int64_t ldl) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
-  const float* xr = x + row * ldx;
-  float ss = 0.0f;
-  for (int c = threadIdx.x; c < width; c += 256) {
-    const float v = xr[c];
-    ss += v * v;
-  }
-  ss = block_sum(ss, red);
+  RowRegs<V> r;
+  r.load(x + row * ldx, width);
+  const float ss = block_sum(r.sumsq(width, 0.0f), red);
   const float inv = 1.0f / sqrtf(ss / (float)width + eps);
-  for (int c = threadIdx.x; c < width; c += 256) {
-    const float o = (xr[c] * inv) * w[c];
-    if (out) out[row * ldo + c] = o;
-    if (out_lp) out_lp[row * ldl + c] = f32_to_bf16_bits(o);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < width) {
+      const float o = (r.v[i] * inv) * w[c];
+      if (out) out[row * ldo + c] = o;
+      if (out_lp) out_lp[row * ldl + c] = f32_to_bf16_bits(o);
+    }
+  }
+}
+
+// out = LayerNorm(x) * w (+ residual), eps 1e-5, no bias
+template <int V>
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ residual,
+                                                        int width, float* __restrict__ out,
+                                                        uint16_t* __restrict__ out_lp) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  RowRegs<V> r;
+  r.load(x + row * width, width);
+  const float mean = block_sum(r.sum(width), red) / (float)width;
+  const float rstd = 1.0f / sqrtf(block_sum(r.sumsq(width, mean), red) / (float)width + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < width) {
+      float o = ((r.v[i] - mean) * rstd) * w[c];
+      if (residual) o += residual[row * width + c];
+      if (out) out[row * width + c] = o;
+      if (out_lp) out_lp[row * width + c] = f32_to_bf16_bits(o);
+    }
+  }
+}
+
+// a = RMSNorm(x) * w_rms (fp32 and optional bf16 copy); xn = LayerNorm(a) * w_ln.
+template <int V>
+__global__ __launch_bounds__(256) void rms_ln_kernel(const float* __restrict__ x,
+                                                     const float* __restrict__ w_rms, float eps,
+                                                     const float* __restrict__ w_ln, int width,
+                                                     float* __restrict__ a,
+                                                     uint16_t* __restrict__ a_lp,
+                                                     float* __restrict__ xn) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  RowRegs<V> r;
+  r.load(x + row * width, width);
+  const float ss = block_sum(r.sumsq(width, 0.0f), red);
+  const float inv = 1.0f / sqrtf(ss / (float)width + eps);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    r.v[i] = c < width ? (r.v[i] * inv) * w_rms[min(c, width - 1)] : 0.0f;
+    if (c < width) {
+      a[row * width + c] = r.v[i];
+      if (a_lp) a_lp[row * width + c] = f32_to_bf16_bits(r.v[i]);
+    }
+  }
+  const float mean = block_sum(r.sum(width), red) / (float)width;
+  const float rstd = 1.0f / sqrtf(block_sum(r.sumsq(width, mean), red) / (float)width + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < width) xn[row * width + c] = ((r.v[i] - mean) * rstd) * w_ln[c];
+  }
+}
+
+// x = LayerNorm(y) * w_ln + x (in place); a = RMSNorm(x) * w_rms (fp32, bf16).
+template <int V>
+__global__ __launch_bounds__(256) void ln_res_rms_kernel(const float* __restrict__ y,
+                                                         const float* __restrict__ w_ln,
+                                                         float* __restrict__ x,
+                                                         const float* __restrict__ w_rms,
+                                                         float eps, int width,
+                                                         float* __restrict__ a,
+                                                         uint16_t* __restrict__ a_lp) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  RowRegs<V> r, xr;
+  r.load(y + row * width, width);
+  xr.load(x + row * width, width);
+  const float mean = block_sum(r.sum(width), red) / (float)width;
+  const float rstd = 1.0f / sqrtf(block_sum(r.sumsq(width, mean), red) / (float)width + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    r.v[i] = c < width ? ((r.v[i] - mean) * rstd) * w_ln[min(c, width - 1)] + xr.v[i] : 0.0f;
+    if (c < width) x[row * width + c] = r.v[i];
+  }
+  const float ss = block_sum(r.sumsq(width, 0.0f), red);
+  const float inv = 1.0f / sqrtf(ss / (float)width + eps);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < width) {
+      const float o = (r.v[i] * inv) * w_rms[c];
+      a[row * width + c] = o;
+      if (a_lp) a_lp[row * width + c] = f32_to_bf16_bits(o);
+    }
   }
 }
 
@@ -55,12 +183,14 @@ __global__ __launch_bounds__(256) void mamba2_post_kernel(
   const float* xr = x + row * ldx;
   const float* zr = z + row * ldz;
   float ss = 0.0f;
+#pragma unroll 8
   for (int c = threadIdx.x; c < inner; c += 256) {
     const float y = (so[c] + d[c / head_size] * xr[c]) * silu(zr[c]);
     ss += y * y;
   }
   ss = block_sum(ss, red);
   const float inv = 1.0f / sqrtf(ss / (float)inner + 1e-5f);
+#pragma unroll 8
   for (int c = threadIdx.x; c < inner; c += 256) {
     const float y = (so[c] + d[c / head_size] * xr[c]) * silu(zr[c]);
     const float o = (y * inv) * w[c];
@@ -91,12 +221,14 @@ __global__ void retnet_post_kernel(const float* __restrict__ o, const float* __r
   const float* orow = o + row * hidden + (int64_t)head * head_size;
   const float* grow = g + row * ldg + (int64_t)head * head_size;
   float ss = 0.0f;
+#pragma unroll 8
   for (int j = lane; j < head_size; j += 64) {
     const float v = orow[j];
     ss += v * v;
   }
   ss = wave_sum(ss);
   const float inv = 1.0f / sqrtf(ss / (float)head_size + 1e-6f);
+#pragma unroll 8
   for (int j = lane; j < head_size; j += 64) {
     const float v = silu(grow[j]) * (orow[j] * inv);
     const int64_t idx = row * hidden + (int64_t)head * head_size + j;
@@ -117,15 +249,18 @@ __global__ void slstm_post_kernel(const float* __restrict__ y, const float* __re
   const int lane = threadIdx.x & 63;
   const int64_t base = row * hidden + (int64_t)grp * gsize;
   float s = 0.0f;
+#pragma unroll 8
   for (int j = lane; j < gsize; j += 64) s += y[base + j];
   const float mean = wave_sum(s) / (float)gsize;
   float v = 0.0f;
+#pragma unroll 8
   for (int j = lane; j < gsize; j += 64) {
     const float dlt = y[base + j] - mean;
     v += dlt * dlt;
   }
   const float rstd = 1.0f / sqrtf(wave_sum(v) / (float)gsize + 1e-5f);
   float rs = 0.0f;
+#pragma unroll 8
   for (int j = lane; j < gsize; j += 64) {
     const int c = grp * gsize + j;
     const float o = ((y[base + j] - mean) * rstd) * gn_w[c] + gn_b[c] + skip[base + j];
@@ -135,41 +270,18 @@ __global__ void slstm_post_kernel(const float* __restrict__ y, const float* __re
   __threadfence_block();
   const float rmean = block_sum(rs, red) / (float)hidden;
   float rv = 0.0f;
+#pragma unroll 8
   for (int j = lane; j < gsize; j += 64) {
     const float dlt = x1[base + j] - rmean;
     rv += dlt * dlt;
   }
   const float rrstd = 1.0f / sqrtf(block_sum(rv, red) / (float)hidden + 1e-5f);
+#pragma unroll 8
   for (int j = lane; j < gsize; j += 64) {
     const int c = grp * gsize + j;
     const float o = ((x1[base + j] - rmean) * rrstd) * ln_w[c];
     if (xn) xn[base + j] = o;
     if (xn_lp) xn_lp[base + j] = f32_to_bf16_bits(o);
-  }
-}
-
-__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x,
-                                                        const float* __restrict__ w,
-                                                        const float* __restrict__ residual,
-                                                        int width, float* __restrict__ out,
-                                                        uint16_t* __restrict__ out_lp) {
-  __shared__ float red[4];
-  const int64_t row = blockIdx.x;
-  const float* xr = x + row * width;
-  float s = 0.0f;
-  for (int c = threadIdx.x; c < width; c += 256) s += xr[c];
-  const float mean = block_sum(s, red) / (float)width;
-  float v = 0.0f;
-  for (int c = threadIdx.x; c < width; c += 256) {
-    const float dlt = xr[c] - mean;
-    v += dlt * dlt;
-  }
-  const float rstd = 1.0f / sqrtf(block_sum(v, red) / (float)width + 1e-5f);
-  for (int c = threadIdx.x; c < width; c += 256) {
-    float o = ((xr[c] - mean) * rstd) * w[c];
-    if (residual) o += residual[row * width + c];
-    if (out) out[row * width + c] = o;
-    if (out_lp) out_lp[row * width + c] = f32_to_bf16_bits(o);
   }
 }
 
@@ -186,14 +298,17 @@ __global__ void mlstm_post_kernel(const float* __restrict__ num, const float* __
   const int64_t base = row * inner + (int64_t)head * hs;
   const float dn = den[row * den_ld + head];
   float s = 0.0f;
+#pragma unroll 8
   for (int j = lane; j < hs; j += 64) s += num[base + j] / dn;
   const float mean = wave_sum(s) / (float)hs;
   float v = 0.0f;
+#pragma unroll 8
   for (int j = lane; j < hs; j += 64) {
     const float dlt = num[base + j] / dn - mean;
     v += dlt * dlt;
   }
   const float rstd = 1.0f / sqrtf(wave_sum(v) / (float)hs + 1e-5f);
+#pragma unroll 8
   for (int j = lane; j < hs; j += 64) {
     const int c = head * hs + j;
     const float gnv = ((num[base + j] / dn - mean) * rstd) * gn_w[c] + gn_b[c];
@@ -212,6 +327,7 @@ __global__ void output_proj_kernel(const float* __restrict__ x, const float* __r
   const int lane = threadIdx.x & 63;
   const float* xr = x + row * hidden;
   float s = 0.0f;
+#pragma unroll 8
   for (int c = lane; c < hidden; c += 64) s += xr[c] * w[c];
   s = wave_sum(s);
   if (lane == 0) preds[row * pred_ld + col] = s + b[0];
@@ -268,11 +384,50 @@ inline unsigned grid_for(int64_t total, int block = 256) {
 
 }  // namespace
 
+// Dispatch on the row width: V elements per thread, width <= 256 * V.
+#define HK_ROW_DISPATCH(width, LAUNCH)                                     \
+  do {                                                                     \
+    HK_REQUIRE((width) >= 1 && (width) <= 8192, "row width %d unsupported (at most 8192)", \
+               (int)(width));                                              \
+    if ((width) <= 256) { LAUNCH(1); }                                     \
+    else if ((width) <= 1024) { LAUNCH(4); }                               \
+    else if ((width) <= 2048) { LAUNCH(8); }                               \
+    else if ((width) <= 4096) { LAUNCH(16); }                              \
+    else { LAUNCH(32); }                                                   \
+  } while (0)
+
 int rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, int n_rows, int width,
                  float* out, int64_t ldo, uint16_t* out_lp, int64_t ldl, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_rows), dim3(256), 0, s, x, ldx, w, eps, width, out,
-                     ldo, out_lp, ldl);
+#define L(V)                                                                              \
+  hipLaunchKernelGGL(rmsnorm_kernel<V>, dim3(n_rows), dim3(256), 0, s, x, ldx, w, eps, width, \
+                     out, ldo, out_lp, ldl)
+  HK_ROW_DISPATCH(width, L);
+#undef L
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int rms_ln_rows(const float* x, const float* w_rms, float eps, const float* w_ln, int n_rows,
+                int width, float* a, uint16_t* a_lp, float* xn, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+#define L(V)                                                                                \
+  hipLaunchKernelGGL(rms_ln_kernel<V>, dim3(n_rows), dim3(256), 0, s, x, w_rms, eps, w_ln, width, \
+                     a, a_lp, xn)
+  HK_ROW_DISPATCH(width, L);
+#undef L
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int ln_res_rms_rows(const float* y, const float* w_ln, float* x, const float* w_rms, float eps,
+                    int n_rows, int width, float* a, uint16_t* a_lp, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+#define L(V)                                                                                  \
+  hipLaunchKernelGGL(ln_res_rms_kernel<V>, dim3(n_rows), dim3(256), 0, s, y, w_ln, x, w_rms, eps, \
+                     width, a, a_lp)
+  HK_ROW_DISPATCH(width, L);
+#undef L
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
@@ -332,8 +487,11 @@ int slstm_post(const float* y, const float* skip, const float* gn_w, const float
 int layernorm_rows(const float* x, const float* w, const float* residual, int n_rows, int width,
                    float* out, uint16_t* out_lp, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
-  hipLaunchKernelGGL(layernorm_kernel, dim3(n_rows), dim3(256), 0, s, x, w, residual, width, out,
-                     out_lp);
+#define L(V)                                                                                \
+  hipLaunchKernelGGL(layernorm_kernel<V>, dim3(n_rows), dim3(256), 0, s, x, w, residual, width, \
+                     out, out_lp)
+  HK_ROW_DISPATCH(width, L);
+#undef L
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
