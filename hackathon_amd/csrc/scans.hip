@@ -22,6 +22,8 @@ __global__ __launch_bounds__(256) void conv_scan_kernel(
   float s0 = st[c], s1 = st[channels + c], s2 = st[2 * channels + c];
   const float w0 = w[c], w1 = w[channels + c], w2 = w[2 * channels + c], w3 = w[3 * channels + c];
   const float b = bias[c];
+  // unrolled so that several rows' loads are in flight together
+#pragma unroll 8
   for (int r = r0; r < r1; ++r) {
     const float x = in[(int64_t)r * ld_in + c];
     float v = b + w0 * s0;
@@ -61,6 +63,8 @@ __global__ __launch_bounds__(256) void retnet_prep_kernel(
   float sc = scales[(int64_t)slot * heads + head];
   const float gam = decay[head];
   const float ang = angle[j];
+  // unrolled so that several rows' loads are in flight together
+#pragma unroll 8
   for (int r = r0; r < r1; ++r) {
     const float* row = qkvg + (int64_t)r * ld;
     const float theta = (float)(off0 + (r - r0)) * ang;
@@ -113,6 +117,8 @@ __global__ __launch_bounds__(256) void rglru_scan_kernel(
   const int r1 = run_off[run + 1];
   float h = h_state[(int64_t)slot * hidden + c];
   const float base = a[c];
+  // unrolled so that several rows' loads are in flight together
+#pragma unroll 8
   for (int r = r0; r < r1; ++r) {
     const int64_t ri = (int64_t)r;
     const float it = sigmoid(gi[ri * ldg + c]);
