@@ -378,7 +378,12 @@ int build_workspace(Engine& e) {
     // Split-K partial sums: up to 8 splits of the widest projection.
     w.gemm_ws.partial_elems = std::min<int64_t>(8 * R * max_n, 1LL << 26);
     w.gemm_ws.partial = e.alloc_f(w.gemm_ws.partial_elems);
-    if (!w.gemm_ws.partial) return HK_ERR_HIP;
+    // One arrival counter per output tile of a split GEMM (a GEMM with more
+    // tiles than this runs unsplit).
+    w.gemm_ws.arrival_elems = 1 << 16;
+    w.gemm_ws.arrivals = static_cast<int*>(e.alloc_bytes((size_t)w.gemm_ws.arrival_elems * 4));
+    if (!w.gemm_ws.partial || !w.gemm_ws.arrivals) return HK_ERR_HIP;
+    HK_CHECK_HIP(hipMemset(w.gemm_ws.arrivals, 0, (size_t)w.gemm_ws.arrival_elems * 4));
   }
   e.FE = e.alloc_act(R * d.Fpad, false);
   if (any_null(e.FE, false, e.lowp)) return HK_ERR_HIP;

@@ -46,9 +46,14 @@ struct GemmArgs {
   GemmEpilogue ep;
 };
 
+// Split-K state of one stream's GEMMs (the GEMMs of one workspace must not
+// overlap in time). `arrivals` holds one counter per output tile, zero
+// between launches: the kernel's last split of a tile resets it.
 struct GemmWorkspace {
   float* partial = nullptr;  // split-K partial sums
   int64_t partial_elems = 0;
+  int* arrivals = nullptr;   // zero-initialised by the owner
+  int64_t arrival_elems = 0;
 };
 
 // K must be a multiple of 64 (bf16) or 16 (fp32); lda/ldw multiples of 8 / 4.

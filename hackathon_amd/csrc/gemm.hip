@@ -2,18 +2,24 @@
 //
 // 64x64 output tile per 256-thread work-group, 4 wave64s in a 2x2 layout,
 // each wave owning a 32x32 sub-tile = 2x2 MFMA 16x16 fragments. K advances in
-// 128-byte slabs (64 bf16 or 32 fp32) through a ring of eight slabs in
-// registers (the memory latency is covered by bytes in flight, not by
-// occupancy: at M <= 256 there is about one work-group per CU) and two LDS
-// stages with one barrier per slab. Rows are padded by 16 bytes in LDS so the
-// 16-byte fragment reads of one wave spread over the banks.
+// 128-byte slabs (64 bf16 or 32 fp32 per row) that travel global -> LDS
+// directly (global_load_lds_dwordx4) through a ring of kStages LDS stages,
+// with one barrier per slab and counted vmcnt waits, so kStages - 2 slabs stay
+// in flight behind the one being multiplied (the memory latency is covered by
+// bytes in flight, not by occupancy: at M <= 256 there is about one
+// work-group per CU). Chunks are XOR-swizzled within a row so the 16-byte
+// fragment reads of one wave spread over the LDS banks.
 //
 // The flat work-group id is remapped so that consecutive tiles (the M tiles
 // that share one slab of W) land on the same XCD and therefore the same L2:
 // hardware dispatch sends work-group i to XCD i % 8.
 //
-// Split-K: with splits > 1 each split writes raw partial sums and a second
-// kernel adds them in split order (deterministic) and applies the epilogue.
+// Split-K: with splits > 1 each split writes its raw partial sums with
+// agent-coherent stores, waits until they have landed and counts itself in at
+// the tile's arrival counter. The split that arrives last reads the other
+// partials back (agent-coherent loads), adds all of them in split order
+// (deterministic, independent of arrival order), applies the epilogue and
+// resets the counter for the next launch.
 #include <algorithm>
 
 #include "gemm.h"
@@ -44,16 +50,6 @@ struct Tr<GemmType::kF32> {
   static constexpr int BK = 32;       // 128-byte slab rows
   static constexpr int BK_NARROW = 16;  // for K a multiple of 16 only
 };
-
-__device__ __forceinline__ void apply_store(const GemmEpilogue& ep, float v, int m, int nc,
-                                            bool add_bias = true) {
-  if (add_bias && ep.bias) v += ep.bias[nc];
-  if (ep.round_lp) v = round_bf16(v);
-  if (ep.act == 1) v = fmaxf(v, 0.0f);
-  if (ep.residual) v += ep.residual[(int64_t)m * ep.ldr + nc];
-  if (ep.out) ep.out[(int64_t)m * ep.ldo + nc] = v;
-  if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_bf16_bits(v);
-}
 
 typedef const __attribute__((address_space(1))) void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
@@ -104,8 +100,8 @@ __device__ __forceinline__ void wait_slabs(int k) {
 }
 
 template <GemmType T, int BK, int S>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, int splits,
-                                                    int tiles_m, int tiles_n) {
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, int* arrivals,
+                                                    int splits, int tiles_m, int tiles_n) {
   using E = typename Tr<T>::E;
   constexpr int EPC = 16 / sizeof(E);   // elements per 16-byte chunk
   constexpr int CPR = BK / EPC;         // chunks per slab row (8, or 4 when narrow)
@@ -207,7 +203,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
   // The bias of this lane's two output columns, fetched before the slabs
   // (older than every transfer, so the counted waits cover it too).
   float bias_v[2] = {0.0f, 0.0f};
-  if (splits == 1 && g.ep.bias) {
+  if (g.ep.bias) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int n = n0 + wn * 32 + j * 16 + fr;
@@ -277,12 +273,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
   // (Every transfer was waited for before its slab; nothing is in flight.)
 
   // Fragment (i, j): lane holds rows 4*fk + e, column fr.
-  if (splits == 1) {
-    // All residual reads before any store: the residual may be the output
-    // itself (x += f(x)); element by element in place is exact, and issuing
-    // the reads first avoids a store-to-load ordering wait per element.
-    const GemmEpilogue& ep = g.ep;
-    float res[2][2][4];
+  if (splits > 1) {
+    // (The host keeps splits * batch * M * N within the int range.)
+    const int MN = g.M * g.N;
+    float* const pb = partial + (int64_t)b * splits * MN;
+    int off[2][2][4];  // this lane's elements within one split's [M, N]
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -291,71 +286,115 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
         for (int e = 0; e < 4; ++e) {
           const int n = n0 + wn * 32 + j * 16 + fr;
           const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
-          res[i][j][e] = (ep.residual && n < g.N && m < g.M)
-                             ? ep.residual[(int64_t)m * ep.ldr + n + (int64_t)b * g.c_bstride]
-                             : 0.0f;
+          off[i][j][e] = (n < g.N && m < g.M) ? m * g.N + n : -1;
         }
-    // Every value first, then every store (no register of a pending store
-    // is rewritten while stores are in flight).
-    float outv[2][2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float v = acc[i][j][e] + bias_v[j];
-          if (ep.round_lp) v = round_bf16(v);
-          if (ep.act == 1) v = fmaxf(v, 0.0f);
-          outv[i][j][e] = v + res[i][j][e];
-        }
+        for (int e = 0; e < 4; ++e)
+          if (off[i][j][e] >= 0)
+            __hip_atomic_store(pb + split * MN + off[i][j][e], acc[i][j][e], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    // Every partial store of this lane acknowledged at the agent-coherent
+    // level, then every wave's, before the tile counter sees this split.
+    wait_vmcnt<0>();
+    __shared__ int last_split;
+    __syncthreads();
+    int* const arrival = arrivals + ((int64_t)b * tiles_n + tn) * tiles_m + tm;
+    if (tid == 0)
+      last_split = __hip_atomic_fetch_add(arrival, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    __syncthreads();
+    if (!last_split) return;
+    if (tid == 0) __hip_atomic_store(arrival, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Sum in split order, four splits' loads in flight at a time; this
+    // split's own part comes from its registers.
+    floatx4 sum[2][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn * 32 + j * 16 + fr;
-        if (n >= g.N) continue;
-        const int nc = n + (int)((int64_t)b * g.c_bstride);
+      for (int j = 0; j < 2; ++j) sum[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < splits; s0 += 4) {
+      float t[4][2][2][4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
-          if (m >= g.M) continue;
-          if (ep.out) ep.out[(int64_t)m * ep.ldo + nc] = outv[i][j][e];
-          if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_bf16_bits(outv[i][j][e]);
-        }
+      for (int q = 0; q < 4; ++q) {
+        const int sp = s0 + q;
+        const bool other = sp < splits && sp != split;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              t[q][i][j][e] = (other && off[i][j][e] >= 0)
+                                  ? __hip_atomic_load(pb + sp * MN + off[i][j][e],
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : acc[i][j][e];
       }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (s0 + q < splits)
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) sum[i][j][e] += t[q][i][j][e];
     }
-  } else {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn * 32 + j * 16 + fr;
-        if (n >= g.N) continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
-          if (m >= g.M) continue;
-          partial[(((int64_t)b * splits + split) * g.M + m) * g.N + n] = acc[i][j][e];
-        }
-      }
-    }
+      for (int j = 0; j < 2; ++j) acc[i][j] = sum[i][j];
   }
-}
 
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, const float* partial,
-                                                            int splits) {
-  const int64_t total = (int64_t)g.batch * g.M * g.N;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int n = (int)(idx % g.N);
-    const int64_t bm = idx / g.N;
-    const int m = (int)(bm % g.M);
-    const int b = (int)(bm / g.M);
-    const float* p = partial + ((int64_t)b * splits * g.M + m) * g.N + n;
-    float v = 0.0f;
-    for (int s = 0; s < splits; ++s) v += p[(int64_t)s * g.M * g.N];
-    apply_store(g.ep, v, m, n + (int)((int64_t)b * g.c_bstride));
+  // All residual reads before any store: the residual may be the output
+  // itself (x += f(x)); element by element in place is exact, and issuing
+  // the reads first avoids a store-to-load ordering wait per element.
+  const GemmEpilogue& ep = g.ep;
+  float res[2][2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int n = n0 + wn * 32 + j * 16 + fr;
+        const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
+        res[i][j][e] = (ep.residual && n < g.N && m < g.M)
+                           ? ep.residual[(int64_t)m * ep.ldr + n + (int64_t)b * g.c_bstride]
+                           : 0.0f;
+      }
+  // Every value first, then every store (no register of a pending store
+  // is rewritten while stores are in flight).
+  float outv[2][2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = acc[i][j][e] + bias_v[j];
+        if (ep.round_lp) v = round_bf16(v);
+        if (ep.act == 1) v = fmaxf(v, 0.0f);
+        outv[i][j][e] = v + res[i][j][e];
+      }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn * 32 + j * 16 + fr;
+      if (n >= g.N) continue;
+      const int nc = n + (int)((int64_t)b * g.c_bstride);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
+        if (m >= g.M) continue;
+        if (ep.out) ep.out[(int64_t)m * ep.ldo + nc] = outv[i][j][e];
+        if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_bf16_bits(outv[i][j][e]);
+      }
+    }
   }
 }
 
@@ -390,29 +429,23 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
   }
   splits = std::max(1, std::min(splits, ktiles));
   while (splits > 1 && (int64_t)splits * g.batch * g.M * g.N > ws.partial_elems) --splits;
+  if (tiles > ws.arrival_elems || ws.arrivals == nullptr) splits = 1;
   const int64_t nwg = tiles * splits;
   HK_REQUIRE(nwg < (1LL << 31), "gemm: grid too large");
   if (g.type == GemmType::kBF16) {
     hipLaunchKernelGGL((gemm_kernel<GemmType::kBF16, Tr<GemmType::kBF16>::BK, kStages>),
-                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, splits, tiles_m,
-                       tiles_n);
+                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, ws.arrivals, splits,
+                       tiles_m, tiles_n);
   } else if (!narrow) {
     hipLaunchKernelGGL((gemm_kernel<GemmType::kF32, Tr<GemmType::kF32>::BK, kStages>),
-                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, splits, tiles_m,
-                       tiles_n);
+                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, ws.arrivals, splits,
+                       tiles_m, tiles_n);
   } else {
     hipLaunchKernelGGL((gemm_kernel<GemmType::kF32, Tr<GemmType::kF32>::BK_NARROW, kStages>),
-                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, splits, tiles_m,
-                       tiles_n);
+                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, ws.arrivals, splits,
+                       tiles_m, tiles_n);
   }
   HK_LAUNCH_CHECK();
-  if (splits > 1) {
-    const int64_t total = (int64_t)g.batch * g.M * g.N;
-    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, g, ws.partial,
-                       splits);
-    HK_LAUNCH_CHECK();
-  }
   return HK_OK;
 }
 
