@@ -37,6 +37,26 @@ __device__ __forceinline__ float logsigmoid(float x) {
 
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Short-latency forms for the step-serial recurrences, on the hardware
+// base-2 exponential / logarithm and reciprocal (v_exp_f32, v_log_f32,
+// v_rcp_f32, each about 1 ulp): e^x = 2^(x log2 e), log1p(y) = log2(1 + y)
+// ln 2. The rounding of x log2 e adds |x| * 2^-24 relative error to e^x
+// (under 1e-6 for |x| < 16); log1p loses relative accuracy for y < 2^-24
+// but keeps an absolute error under 2^-24, which is what logsigmoid needs.
+__device__ __forceinline__ float fast_exp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_logsigmoid(float x) {
+  return fminf(x, 0.0f) - __builtin_amdgcn_logf(1.0f + fast_exp(-fabsf(x))) * 0.693147180559945309f;
+}
+__device__ __forceinline__ float fast_sigmoid(float x) { return fast_rcp(1.0f + fast_exp(-x)); }
+// tanh z = sign(z) (1 - e) / (1 + e), e = e^{-2|z|} in (0, 1]: no overflow.
+__device__ __forceinline__ float fast_tanh(float z) {
+  const float e = fast_exp(-2.0f * fabsf(z));
+  return copysignf((1.0f - e) * fast_rcp(1.0f + e), z);
+}
+
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
 }

@@ -279,6 +279,12 @@ struct SlstmPersistArgs {
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
+// LDS ints of the run descriptors (run_off, slot_ids, act), kept even so
+// that what follows stays 8-byte aligned.
+__host__ __device__ __forceinline__ int persist_meta_ints(int n_runs, int n_rounds) {
+  return (2 * n_runs + 1 + n_rounds + 1) & ~1;
+}
+
 __device__ __forceinline__ unsigned long long xch_word(float v, unsigned int tag) {
   return (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32);
 }
@@ -337,6 +343,11 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
   float* hbuf = smem;                               // [16][PAD]
   float* gsum = hbuf + kPersistRuns * PAD;          // [16 runs][64 rows], k half 0
   float* xbuf = gsum + kPersistRuns * 64;           // [16 runs][64 rows], k half 1
+  // The run descriptors, copied to LDS once: every step reads them, and a
+  // global load there would put a memory latency ahead of each step's poll.
+  int* l_off = reinterpret_cast<int*>(xbuf + kPersistRuns * 64);  // [n_runs + 1]
+  int* l_slot = l_off + a.n_runs + 1;                             // [n_runs]
+  int* l_act = l_slot + a.n_runs;                                 // [n_rounds]
   __shared__ int s_abort;
   // The recurrence is latency-bound and shares its CUs with other streams'
   // kernels: its waves take instruction-issue priority over theirs.
@@ -381,14 +392,17 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
     bo = a.b_state[3 * H + ccol];
   }
   if (tid == 0) s_abort = 0;
+  for (int i = tid; i <= a.n_runs; i += NT) l_off[i] = a.run_off[i];
+  for (int i = tid; i < a.n_runs; i += NT) l_slot[i] = a.slot_ids[i];
+  for (int i = tid; i < a.n_rounds; i += NT) l_act[i] = a.act[i];
   lds_barrier();
 
   // Optional phase stamps of work-group 0 (thread 0), kept in LDS during the
   // recurrence so that taking them adds no memory waits, stored at the end.
   const bool tr = a.trace != nullptr && blockIdx.x == 0 && tid == 0;
-  uint64_t* ltr = reinterpret_cast<uint64_t*>(xbuf + kPersistRuns * 64);
+  uint64_t* ltr = reinterpret_cast<uint64_t*>(l_off + persist_meta_ints(a.n_runs, a.n_rounds));
   for (int t = 0; t < a.n_rounds; ++t) {
-    const int na = a.act[t];
+    const int na = l_act[t];
     if (tr) ltr[t * 8 + 0] = __builtin_amdgcn_s_memrealtime();
     for (int c0 = 0; c0 < na; c0 += kPersistRuns) {
       const int nj = min(kPersistRuns, na - c0);
@@ -399,9 +413,9 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
       int64_t psi = 0, prow = 0;
       if (cell) {
         const int run = c0 + jr;
-        const int row = a.run_off[run] + t;
+        const int row = l_off[run] + t;
         const float* gr = a.gin + (int64_t)row * 4 * H;
-        psi = (int64_t)a.slot_ids[run] * H + ccol;
+        psi = (int64_t)l_slot[run] * H + ccol;
         prow = row;
         pi = gr[ccol];
         pf = gr[H + ccol];
@@ -424,7 +438,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         for (int u = 0; u < kV; ++u) {
           const int i = min(u * NT + tid, nvec - 1);
           const int j = i / vph;
-          v[u] = reinterpret_cast<const float4*>(a.h_state + (int64_t)a.slot_ids[c0 + j] * H +
+          v[u] = reinterpret_cast<const float4*>(a.h_state + (int64_t)l_slot[c0 + j] * H +
                                                  head * hs)[i - j * vph];
         }
 #pragma unroll
@@ -445,7 +459,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         for (int u = 0; u < kS; ++u) {
           const int i = min(u * NT + tid, nel - 1);
           const int j = i / hs;
-          offs[u] = (uint32_t)(a.run_off[c0 + j] + t - 1) * (uint32_t)H + head * hs + (i - j * hs);
+          offs[u] = (uint32_t)(l_off[c0 + j] + t - 1) * (uint32_t)H + head * hs + (i - j * hs);
         }
         // Waves whose words all lie past the chunk poll the clamped last word.
         if (!poll_first<kS>(a.xch, offs, a.tag, a.err, v, (nel + NT - 1) / NT)) s_abort = 1;
@@ -516,14 +530,14 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         const float fp = pf + ((g0.y + g1.y) + bf);
         const float zp = pz + ((g0.z + g1.z) + bz);
         const float op = po + ((g0.w + g1.w) + bo);
-        const float lfm = pm + logsigmoid(fp);
+        const float lfm = pm + fast_logsigmoid(fp);
         const float mn = fmaxf(ip, lfm);
-        const float og = sigmoid(op);
-        const float ig = expf(ip - mn);
-        const float fg = expf(lfm - mn);
-        const float cn = fg * pc + ig * tanhf(zp);
+        const float og = fast_sigmoid(op);
+        const float ig = fast_exp(ip - mn);
+        const float fg = fast_exp(lfm - mn);
+        const float cn = fg * pc + ig * fast_tanh(zp);
         const float nn = fg * pn + ig;
-        const float h = og * cn / (nn + 1e-6f);
+        const float h = og * cn * fast_rcp(nn + 1e-6f);
         a.c_state[psi] = cn;
         a.n_state[psi] = nn;
         a.m_state[psi] = mn;
@@ -550,7 +564,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
     constexpr int kS = (hs + NT - 1) / NT;
     uint32_t offs[kS];
     float v[kS];
-    const uint32_t row = (uint32_t)a.run_off[a.n_runs - 1];
+    const uint32_t row = (uint32_t)l_off[a.n_runs - 1];
 #pragma unroll
     for (int u = 0; u < kS; ++u)
       offs[u] = row * (uint32_t)H + head * hs + min(u * NT + tid, hs - 1);
@@ -565,10 +579,10 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
     const int i = min(base + tid, total - 1);
     const int run = i >> 4;
     const int col = head * hs + u0 + (i & 15);
-    const uint32_t off = (uint32_t)(a.run_off[run + 1] - 1) * (uint32_t)H + col;
+    const uint32_t off = (uint32_t)(l_off[run + 1] - 1) * (uint32_t)H + col;
     float hv;
     if (!poll_words<1>(a.xch, &off, a.tag, a.err, &hv)) return;
-    if (base + tid < total) a.h_state[(int64_t)a.slot_ids[run] * H + col] = hv;
+    if (base + tid < total) a.h_state[(int64_t)l_slot[run] * H + col] = hv;
   }
 }
 
@@ -741,14 +755,21 @@ bool slstm_persist_supported(int hidden, int heads) {
 template <int HS>
 int launch_persist(const SlstmPersistArgs& a, size_t smem, hipStream_t s) {
   const dim3 grid(a.heads * (HS / 16)), block(kPersistThreads);
-  static int fits = -1;  // per process: one device type
-  if (fits < 0) {
-    int dev = 0, cus = 0, per_cu = 0;
+  // per process (one device type), for the last LDS size asked for
+  static int cus = -1;
+  static size_t fits_smem = 0;
+  static int64_t fits = -1;
+  if (cus < 0) {
+    int dev = 0;
     HK_CHECK_HIP(hipGetDevice(&dev));
     HK_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  if (fits < 0 || smem != fits_smem) {
+    int per_cu = 0;
     HK_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
         &per_cu, slstm_persist_kernel<HS>, kPersistThreads, smem));
     fits = (int64_t)cus * per_cu;
+    fits_smem = smem;
   }
   HK_REQUIRE((int64_t)grid.x <= fits, "slstm_persist: %u work-groups cannot be co-resident (%d)",
              grid.x, fits);
@@ -770,7 +791,10 @@ int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* 
   SlstmPersistArgs a{r.slot_ids, r.run_off, act_dev, n_rounds, r.n_runs, gin, hidden, heads,
                      w_state, b_state, h_state, c_state, n_state, m_state, y, xch, tag, err,
                      trace};
-  size_t smem = (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float);
+  size_t smem = (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float) +
+                (size_t)persist_meta_ints(r.n_runs, n_rounds) * sizeof(int);
+  HK_REQUIRE(smem <= 96 * 1024, "slstm_persist: %d runs over %d steps exceed the LDS descriptor copy",
+             r.n_runs, n_rounds);
   if (trace != nullptr) {
     HK_REQUIRE(n_rounds <= 512, "slstm_persist: tracing supports at most 512 steps");
     smem += (size_t)n_rounds * 8 * sizeof(uint64_t);
