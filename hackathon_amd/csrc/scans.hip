@@ -1,6 +1,9 @@
 // Per-run scan kernels: each work-group walks one symbol's run of requests
 // in order, carrying that symbol's small recurrent state in registers, so the
 // state is read once and written once per tick.
+#include <algorithm>
+#include <type_traits>
+
 #include "ops.h"
 
 namespace hk {
@@ -596,90 +599,165 @@ __global__ void slstm_final_kernel(const int* __restrict__ slot_ids,
     h_state[(int64_t)slot * hidden + c] = y[(int64_t)last * hidden + c];
 }
 
-// mLSTM gate / normaliser recurrence, one wave per (run, head): lane l holds
-// n[e*64 + l] for e < PER (hs <= 64*PER); steps in order, as the reference.
-// The step's q and k rows and gate pre-activations come from a ring of
-// kGateRing prefetched steps in registers (refilled unconditionally with
-// clamped rows, so the compiler's wait counts stay exact), hiding the load
-// latency that a run of many steps would otherwise pay at every step.
-constexpr int kGateRing = 8;
-template <int PER>
-__global__ __launch_bounds__(256) void mlstm_gates_kernel(
-    const int* __restrict__ slot_ids, const int* __restrict__ run_off, int n_runs,
-    const float* __restrict__ if_pre, int heads, const float* __restrict__ qkv, int inner,
-    const float* __restrict__ ks, float* __restrict__ n_state, float* __restrict__ m_state,
-    float* __restrict__ ig_out, float* __restrict__ fg_out, float* __restrict__ den_out) {
-  const int lane = threadIdx.x & 63;
-  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (pair >= n_runs * heads) return;  // whole wave
-  const int run = pair / heads;
-  const int head = pair - run * heads;
-  const int hs = inner / heads;  // at most 64 * PER; lanes past it hold zeros
+// mLSTM gate / normaliser recurrence (model/kernels.py:143-151), one
+// work-group of NWV waves per (run, head): thread i holds elements
+// [i*PER, i*PER + PER) of the head's normaliser n (threads past hs hold
+// zeros). Steps run in order in blocks of kGateBlock:
+//  - the stabiliser chain m_t = max(i_t, m_{t-1} + logsigmoid(f_t)) and the
+//    gates i', f' of the block's steps first (wave-uniform values);
+//  - then n_t = f'_t n_{t-1} + i'_t k_t and each thread's part of q_t . n_t
+//    for every step of the block;
+//  - then the block's dot products are summed together: a transposed
+//    butterfly leaves step j's wave sum in lane 8j after 10 shuffles (one
+//    wave sum per step would take 6 dependent shuffles each), and the waves'
+//    sums meet in LDS.
+// The rows of the next two blocks are prefetched into a register double
+// buffer; loads are unconditional (rows clamped to the run) so that the
+// compiler's wait counts stay exact.
+constexpr int kGateBlock = 8;
+template <int NWV, int PER>
+__global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
+    const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ if_pre,
+    int heads, const float* __restrict__ qkv, int inner, const float* __restrict__ ks,
+    float* __restrict__ n_state, float* __restrict__ m_state, float* __restrict__ ig_out,
+    float* __restrict__ fg_out, float* __restrict__ den_out) {
+  constexpr int B = kGateBlock;
+  using VecT = typename std::conditional<PER == 1, float,
+               typename std::conditional<PER == 2, float2, float4>::type>::type;
+  __shared__ float red[2][NWV][B];
+  const int run = blockIdx.x / heads;
+  const int head = blockIdx.x - run * heads;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hs = inner / heads;
   const int slot = slot_ids[run];
   const int r0 = run_off[run];
   const int len = run_off[run + 1] - r0;
   const int rl = r0 + len - 1;
-  float* nst = n_state + ((int64_t)slot * heads + head) * hs;
-  // element e*64 + lane of the head; past hs: clamped loads, zero values
-  int hidx[PER];
-  float ok[PER];
-#pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int h = e * 64 + lane;
-    hidx[e] = min(h, hs - 1);
-    ok[e] = h < hs ? 1.0f : 0.0f;
-  }
+  const int e0 = tid * PER;
+  const float okf = e0 < hs ? 1.0f : 0.0f;
+  const int ec = e0 < hs ? e0 : 0;  // clamped chunk (chunk 0 always exists)
+  float* nst = n_state + ((int64_t)slot * heads + head) * hs + ec;
+  auto get = [](const float* p, float* v) {
+    const VecT x = *reinterpret_cast<const VecT*>(p);
+    if constexpr (PER == 1) {
+      v[0] = x;
+    } else if constexpr (PER == 2) {
+      v[0] = x.x;
+      v[1] = x.y;
+    } else {
+      v[0] = x.x;
+      v[1] = x.y;
+      v[2] = x.z;
+      v[3] = x.w;
+    }
+  };
   float nv[PER];
+  get(nst, nv);
 #pragma unroll
-  for (int e = 0; e < PER; ++e) nv[e] = ok[e] * nst[hidx[e]];
+  for (int p = 0; p < PER; ++p) nv[p] *= okf;
   float m = m_state[(int64_t)slot * heads + head];
 
-  const float* qh = qkv + (int64_t)head * hs;
-  const float* kh = ks + (int64_t)head * hs;
-  float rq[kGateRing][PER], rk[kGateRing][PER], ri[kGateRing], rf[kGateRing];
-  auto fill = [&](int j, int row) {
+  const float* qh = qkv + (int64_t)head * hs + ec;
+  const float* kh = ks + (int64_t)head * hs + ec;
+  // gate pre-activations: lane j < 8 holds i of step j, lane 8 + j holds f
+  const int gj = lane & 7;
+  const float* gh = if_pre + head + ((lane & 8) ? heads : 0);
+  float rq[2][B][PER], rk[2][B][PER], rg[2];
+  auto fill = [&](float (&q)[B][PER], float (&k)[B][PER], float& g, int tb) {
 #pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      rq[j][e] = qh[(int64_t)row * 3 * inner + hidx[e]];
-      rk[j][e] = ok[e] * kh[(int64_t)row * inner + hidx[e]];
+    for (int j = 0; j < B; ++j) {
+      const int64_t row = min(r0 + tb + j, rl);
+      get(qh + row * 3 * inner, q[j]);
+      get(kh + row * inner, k[j]);
     }
-    ri[j] = if_pre[(int64_t)row * 2 * heads + head];
-    rf[j] = if_pre[(int64_t)row * 2 * heads + heads + head];
+    g = gh[(int64_t)min(r0 + tb + gj, rl) * 2 * heads];
   };
-#pragma unroll
-  for (int j = 0; j < kGateRing; ++j) fill(j, min(r0 + j, rl));
+  fill(rq[0], rk[0], rg[0], 0);
+  fill(rq[1], rk[1], rg[1], B);
 
-  for (int tb = 0; tb < len; tb += kGateRing) {
+  auto block = [&](const float (&q)[B][PER], const float (&k)[B][PER], float g, int tb, int par) {
+    float ig[B], fg[B], em[B];
 #pragma unroll
-    for (int j = 0; j < kGateRing; ++j) {
-      const int t = tb + j;
-      if (t < len) {
-        const float log_f = logsigmoid(rf[j]);
-        const float mn = fmaxf(ri[j], m + log_f);
-        const float ig = expf(ri[j] - mn);
-        const float fg = expf(log_f + m - mn);
-        float dot = 0.0f;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-          nv[e] = fg * nv[e] + ig * rk[j][e];
-          dot += rq[j][e] * nv[e];
-        }
-        dot = wave_sum(dot);
-        m = mn;
-        if (lane == 0) {
-          const int64_t row = r0 + t;
-          ig_out[row * heads + head] = ig;
-          fg_out[row * heads + head] = fg;
-          den_out[row * heads + head] = fmaxf(fabsf(dot), expf(-mn)) + 1e-6f;
-        }
-      }
-      fill(j, min(r0 + t + kGateRing, rl));
+    for (int j = 0; j < B; ++j) {
+      const float ri = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), j));
+      const float rf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), 8 + j));
+      const float lf = fast_logsigmoid(rf);
+      const float mn = fmaxf(ri, m + lf);
+      ig[j] = fast_exp(ri - mn);
+      fg[j] = fast_exp(lf + m - mn);
+      em[j] = fast_exp(-mn);
+      if (tb + j < len) m = mn;
     }
-  }
+    float pd[B];
 #pragma unroll
-  for (int e = 0; e < PER; ++e)
-    if (e * 64 + lane < hs) nst[e * 64 + lane] = nv[e];
-  if (lane == 0) m_state[(int64_t)slot * heads + head] = m;
+    for (int j = 0; j < B; ++j) {
+      if (tb + j < len) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) nv[p] = fg[j] * nv[p] + ig[j] * (okf * k[j][p]);
+      }
+      float d = 0.0f;
+#pragma unroll
+      for (int p = 0; p < PER; ++p) d += q[j][p] * nv[p];
+      pd[j] = d;
+    }
+    // transposed butterfly: after level b, lane bit (5 - b) selects which
+    // half of the remaining steps the lane keeps
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    float a4[4], a2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      a4[i] = (b5 ? pd[4 + i] : pd[i]) + __shfl_xor(b5 ? pd[i] : pd[4 + i], 32, 64);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      a2[i] = (b4 ? a4[2 + i] : a4[i]) + __shfl_xor(b4 ? a4[i] : a4[2 + i], 16, 64);
+    float a1 = (b3 ? a2[1] : a2[0]) + __shfl_xor(b3 ? a2[0] : a2[1], 8, 64);
+    a1 += __shfl_xor(a1, 4, 64);
+    a1 += __shfl_xor(a1, 2, 64);
+    a1 += __shfl_xor(a1, 1, 64);
+    // lane 8j holds step j's wave sum
+    const int myj = lane >> 3;
+    if constexpr (NWV > 1) {
+      if ((lane & 7) == 0) red[par][wave][myj] = a1;
+      lds_barrier();
+      a1 = 0.0f;
+#pragma unroll
+      for (int w2 = 0; w2 < NWV; ++w2) a1 += red[par][w2][myj];
+    }
+    if (wave == 0 && (lane & 7) == 0 && tb + myj < len) {
+      float sig = ig[0], sfg = fg[0], sem = em[0];
+#pragma unroll
+      for (int j = 1; j < B; ++j) {
+        sig = myj == j ? ig[j] : sig;
+        sfg = myj == j ? fg[j] : sfg;
+        sem = myj == j ? em[j] : sem;
+      }
+      const int64_t row = r0 + tb + myj;
+      ig_out[row * heads + head] = sig;
+      fg_out[row * heads + head] = sfg;
+      den_out[row * heads + head] = fmaxf(fabsf(a1), sem) + 1e-6f;
+    }
+  };
+
+  for (int tb = 0; tb < len; tb += 2 * B) {
+    block(rq[0], rk[0], rg[0], tb, 0);
+    fill(rq[0], rk[0], rg[0], tb + 2 * B);
+    block(rq[1], rk[1], rg[1], tb + B, 1);
+    fill(rq[1], rk[1], rg[1], tb + 3 * B);
+  }
+  if (e0 < hs) {
+    VecT x;
+    if constexpr (PER == 1) {
+      x = nv[0];
+    } else if constexpr (PER == 2) {
+      x = make_float2(nv[0], nv[1]);
+    } else {
+      x = make_float4(nv[0], nv[1], nv[2], nv[3]);
+    }
+    *reinterpret_cast<VecT*>(nst) = x;
+  }
+  if (tid == 0) m_state[(int64_t)slot * heads + head] = m;
 }
 
 }  // namespace
@@ -823,22 +901,29 @@ int mlstm_gates(const Runs& r, const float* if_pre, int heads, const float* qkv,
   const int hs = inner / heads;
   HK_REQUIRE(inner % heads == 0 && hs >= 1 && hs <= 1024,
              "mlstm_gates: head size %d unsupported (at most 1024)", hs);
-  const int pairs = r.n_runs * heads;
-  const dim3 grid((pairs + 3) / 4), block(256);
-  const int per = (hs + 63) / 64;
-#define HK_GATES(P)                                                                          \
-  hipLaunchKernelGGL(mlstm_gates_kernel<P>, grid, block, 0, s, r.slot_ids, r.run_off, r.n_runs, \
+  // NWV waves of 64 threads, PER consecutive elements per thread
+  const int nwv = std::min(4, (hs + 63) / 64);
+  const int per = hs <= 64 * nwv ? 1 : (hs <= 128 * nwv ? 2 : 4);
+  HK_REQUIRE(hs % per == 0 && inner % per == 0 &&
+                 (reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(ks) |
+                  reinterpret_cast<uintptr_t>(n_state)) % (4 * per) == 0,
+             "mlstm_gates: head size %d needs %d-float aligned rows", hs, per);
+  const dim3 grid(r.n_runs * heads), block(64 * nwv);
+#define HK_GATES(W, P)                                                                    \
+  hipLaunchKernelGGL((mlstm_gates_kernel<W, P>), grid, block, 0, s, r.slot_ids, r.run_off, \
                      if_pre, heads, qkv, inner, ks, n_state, m_state, ig, fg, den)
-  if (per <= 1) {
-    HK_GATES(1);
-  } else if (per <= 2) {
-    HK_GATES(2);
-  } else if (per <= 4) {
-    HK_GATES(4);
-  } else if (per <= 8) {
-    HK_GATES(8);
+  if (nwv == 1) {
+    HK_GATES(1, 1);
+  } else if (nwv == 2) {
+    HK_GATES(2, 1);
+  } else if (nwv == 3) {
+    HK_GATES(3, 1);
+  } else if (per == 1) {
+    HK_GATES(4, 1);
+  } else if (per == 2) {
+    HK_GATES(4, 2);
   } else {
-    HK_GATES(16);
+    HK_GATES(4, 4);
   }
 #undef HK_GATES
   HK_LAUNCH_CHECK();
