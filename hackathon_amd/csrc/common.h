@@ -116,6 +116,28 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Wave sums of NV values at once (NV a power of two, <= 64): each level of
+// the xor butterfly halves the values a lane keeps (lane bit d picks which
+// half), so NV sums take NV - 1 + 6 - log2(NV) shuffles instead of 6 * NV.
+// The result is the sum of value i = lane >> (6 - log2(NV)) over the wave:
+// lane i * 64 / NV (and every lane of its group) holds sum i.
+template <int NV>
+__device__ __forceinline__ float transposed_wave_sum(float (&v)[NV]) {
+  static_assert(NV >= 1 && NV <= 64 && (NV & (NV - 1)) == 0, "power of two up to 64");
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int n = NV, d = 32; n > 1; n >>= 1, d >>= 1) {
+    const bool hi = (lane & d) != 0;
+#pragma unroll
+    for (int i = 0; i < n / 2; ++i)
+      v[i] = (hi ? v[n / 2 + i] : v[i]) + __shfl_xor(hi ? v[i] : v[n / 2 + i], d, 64);
+  }
+  float r = v[0];
+#pragma unroll
+  for (int d = 32 / NV; d >= 1; d >>= 1) r += __shfl_xor(r, d, 64);
+  return r;
+}
+
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` must hold
 // blockDim.x / 64 floats of LDS. Every thread gets the total.
 __device__ __forceinline__ float block_sum(float v, float* red) {

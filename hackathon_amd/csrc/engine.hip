@@ -33,6 +33,7 @@ namespace {
 
 enum TowerType { kXLSTM = 0, kMamba2 = 1, kRetNet = 2, kHawk = 3 };
 constexpr int kTowers = 4;
+constexpr int kMaxIfSegments = 4;  // partial planes of the mLSTM gate pre-activations
 
 // ---- weight slots ----------------------------------------------------------
 // Block-level slots common to every tower type.
@@ -329,7 +330,7 @@ int build_workspace(Engine& e) {
         w.XMC = e.alloc_f(R * d.I);
         w.QKV = e.alloc_f(R * 3 * d.I);
         w.KS = e.alloc_f(R * d.I);
-        w.IF = e.alloc_f(R * 2 * d.nh);
+        w.IF = e.alloc_f(R * 2 * d.nh * kMaxIfSegments);
         w.IG = e.alloc_f(R * d.nh);
         w.FG = e.alloc_f(R * d.nh);
         w.DEN = e.alloc_f(R * d.nh);
@@ -510,6 +511,16 @@ int block_linear(Engine& e, TowerWS& w, const float* x, const float* x2, int x2_
 
 const Slot* S(Engine& e, int t, int l, int i) { return &e.slots[t][l + 1][i]; }
 
+// Column segments of the fused q/k/v + gate projection launch: about 256
+// four-column blocks (one per thread) per work-group, at most
+// kMaxIfSegments partial planes.
+int if_segments(int inner) {
+  const int nb = inner / 4;
+  int sg = std::min(kMaxIfSegments, std::max(1, nb / 256));
+  while (sg > 1 && nb % sg != 0) --sg;
+  return sg;
+}
+
 int timed_mat_scan(Engine& e, int kind, const MatScanDesc& m, hipStream_t s) {
   return timed(e, kind, s, [&] { return launch_mat_scan(m, s); });
 }
@@ -583,12 +594,25 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   HK_TRY(conv_scan(r, w.XMG, 2 * I, I, st[XS_L_CONV], le[XS_L_CONV], F32(e, kXLSTM, l, X_L_CONV_W),
                    F32(e, kXLSTM, l, X_L_CONV_B), 1, w.XMC, I, s));
   const float* wqkv = F32(e, kXLSTM, l, X_L_QKV_W);
-  HK_TRY(mlstm_qkv(w.XMC, w.XMG, 2 * I, wqkv, wqkv + (int64_t)I * 4, wqkv + (int64_t)2 * I * 4, n,
-                   I, 4, (float)std::sqrt((double)d.hs_m), w.QKV, w.KS, s));
-  HK_TRY(linear(e, w, Act{w.QKV, nullptr}, 3 * I,
-                {S(e, kXLSTM, l, X_L_IF_W), S(e, kXLSTM, l, X_L_IF_B)}, n, 2 * d.nh, 3 * I, 0,
-                nullptr, 0, w.IF, 2 * d.nh, nullptr, 0, s));
-  HK_TRY(mlstm_gates(r, w.IF, d.nh, w.QKV, I, w.KS, st[XS_L_N], st[XS_L_M], w.IG, w.FG, w.DEN, s));
+  const float k_div = (float)std::sqrt((double)d.hs_m);
+  const int n_if = 2 * d.nh;
+  const int segs = if_segments(I);
+  if (mlstm_qkv_if_supported(I, n_if, segs)) {
+    // q, k, v and the gate pre-activations in one launch (segment partials)
+    HK_TRY(mlstm_qkv_if(w.XMC, w.XMG, 2 * I, wqkv, wqkv + (int64_t)I * 4, wqkv + (int64_t)2 * I * 4,
+                        n, I, k_div, F32(e, kXLSTM, l, X_L_IF_W), F32(e, kXLSTM, l, X_L_IF_B), n_if,
+                        w.QKV, w.KS, w.IF, segs, s));
+    HK_TRY(mlstm_gates(r, w.IF, segs, (int64_t)n * n_if, d.nh, w.QKV, I, w.KS, st[XS_L_N],
+                       st[XS_L_M], w.IG, w.FG, w.DEN, s));
+  } else {
+    HK_TRY(mlstm_qkv(w.XMC, w.XMG, 2 * I, wqkv, wqkv + (int64_t)I * 4, wqkv + (int64_t)2 * I * 4,
+                     n, I, 4, k_div, w.QKV, w.KS, s));
+    HK_TRY(linear(e, w, Act{w.QKV, nullptr}, 3 * I,
+                  {S(e, kXLSTM, l, X_L_IF_W), S(e, kXLSTM, l, X_L_IF_B)}, n, n_if, 3 * I, 0,
+                  nullptr, 0, w.IF, n_if, nullptr, 0, s));
+    HK_TRY(mlstm_gates(r, w.IF, 1, 0, d.nh, w.QKV, I, w.KS, st[XS_L_N], st[XS_L_M], w.IG, w.FG,
+                       w.DEN, s));
+  }
   MatScanDesc m;
   m.state = st[XS_L_C];
   m.rows = d.hs_m;

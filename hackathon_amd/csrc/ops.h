@@ -71,11 +71,22 @@ int mlstm_post(const float* num, const float* den, int den_ld, const float* gn_w
 int output_proj(const float* x, const float* w, const float* b, int n_rows, int hidden,
                 float* preds, int pred_ld, int col, hipStream_t s);
 
-// mLSTM q/k/v BlockLinear with 4x4 blocks (model/xlstm.py:286-288, :315-317):
+// mLSTM q/k/v BlockLinear (model/xlstm.py:191-193, :220-222), blk x blk blocks:
 // qkv[:, 0:I] = q, [:, I:2I] = k, [:, 2I:3I] = v; ks = k / k_div.
 int mlstm_qkv(const float* x_conv, const float* x_m, int64_t ld_xm, const float* wq,
               const float* wk, const float* wv, int n_rows, int inner, int blk, float k_div,
               float* qkv, float* ks, hipStream_t s);
+
+// mlstm_qkv with blk 4 fused with the cell's input / forget gate projections
+// (model/xlstm.py:29-30, :52-54): w_if [n_out][3*inner] (igate rows, then
+// fgate rows), b_if [n_out]. The pre-activations land as `segs` partial
+// planes if_part [segs][n_rows][n_out], to be added in plane order (plane 0
+// holds the bias).
+bool mlstm_qkv_if_supported(int inner, int n_out, int segs);
+int mlstm_qkv_if(const float* x_conv, const float* x_m, int64_t ld_xm, const float* wq,
+                 const float* wk, const float* wv, int n_rows, int inner, float k_div,
+                 const float* w_if, const float* b_if, int n_out, float* qkv, float* ks,
+                 float* if_part, int segs, hipStream_t s);
 
 // bf16 copy of an fp32 matrix (weights at bind time).
 int to_bf16(const float* src, uint16_t* dst, int64_t n, hipStream_t s);
@@ -118,9 +129,11 @@ int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* 
 // After the last round: h_state[slot] = y[last row of the run].
 int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipStream_t s);
 
-// mLSTM gate / normaliser recurrence (model/xlstm.py:147-168, :236-238).
-int mlstm_gates(const Runs& r, const float* if_pre, int heads, const float* qkv, int inner,
-                const float* ks, float* n_state, float* m_state, float* ig, float* fg, float* den,
-                hipStream_t s);
+// mLSTM gate / normaliser recurrence (model/xlstm.py:61-74, :140-142). The
+// gate pre-activations if_pre [rows][2*heads] (i then f) are the sum of
+// n_parts planes part_stride floats apart, added in plane order.
+int mlstm_gates(const Runs& r, const float* if_pre, int n_parts, int64_t part_stride, int heads,
+                const float* qkv, int inner, const float* ks, float* n_state, float* m_state,
+                float* ig, float* fg, float* den, hipStream_t s);
 
 }  // namespace hk

@@ -362,6 +362,69 @@ __global__ void mlstm_qkv_kernel(const float* __restrict__ x_conv, const float* 
   }
 }
 
+// mLSTM q/k/v BlockLinear with 4x4 blocks (model/xlstm.py:191-193,
+// :220-222) fused with the input / forget gate projections of the cell,
+// [igate; fgate](cat(q, k, v)) (model/xlstm.py:29-30, :52-54), for one
+// (row, column segment) per work-group: each thread computes whole 4-column
+// blocks of q, k and v with 16-byte loads, stores them, and accumulates
+// their NOUT gate-row products; the work-group's NOUT sums (in a fixed
+// order) are segment seg's partial pre-activations, plane seg of if_part
+// [segs][n_rows][NOUT]; plane 0 also carries the bias.
+template <int NOUT>
+__global__ __launch_bounds__(256) void mlstm_qkv_if_kernel(
+    const float* __restrict__ x_conv, const float* __restrict__ x_m, int64_t ld_xm,
+    const float* __restrict__ wq, const float* __restrict__ wk, const float* __restrict__ wv,
+    int n_rows, int inner, float k_div, const float* __restrict__ w_if,
+    const float* __restrict__ b_if, float* __restrict__ qkv, float* __restrict__ ks,
+    float* __restrict__ if_part) {
+  __shared__ float red[4][NOUT];
+  const int seg = blockIdx.x;
+  const int row = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int per = (inner >> 2) / gridDim.x;  // 4-column blocks per segment
+  const float4* xc4 = reinterpret_cast<const float4*>(x_conv + (int64_t)row * inner);
+  const float4* xm4 = reinterpret_cast<const float4*>(x_m + (int64_t)row * ld_xm);
+  float4* q4o = reinterpret_cast<float4*>(qkv + (int64_t)row * 3 * inner);
+  float4* k4o = q4o + (inner >> 2);
+  float4* v4o = k4o + (inner >> 2);
+  float4* ks4 = reinterpret_cast<float4*>(ks + (int64_t)row * inner);
+  const int64_t wl = (int64_t)3 * inner;
+  auto dot4 = [](float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; };
+  float acc[NOUT];
+#pragma unroll
+  for (int n = 0; n < NOUT; ++n) acc[n] = 0.0f;
+  for (int nb = seg * per + tid; nb < (seg + 1) * per; nb += 256) {
+    const float4 xc = xc4[nb], xm = xm4[nb];
+    // W[nb][o][h]: block nb's 4x4 weights, row o = output column 4nb + o
+    const float4* bq = reinterpret_cast<const float4*>(wq) + (int64_t)nb * 4;
+    const float4* bk = reinterpret_cast<const float4*>(wk) + (int64_t)nb * 4;
+    const float4* bv = reinterpret_cast<const float4*>(wv) + (int64_t)nb * 4;
+    const float4 q = make_float4(dot4(xc, bq[0]), dot4(xc, bq[1]), dot4(xc, bq[2]), dot4(xc, bq[3]));
+    const float4 k = make_float4(dot4(xc, bk[0]), dot4(xc, bk[1]), dot4(xc, bk[2]), dot4(xc, bk[3]));
+    const float4 v = make_float4(dot4(xm, bv[0]), dot4(xm, bv[1]), dot4(xm, bv[2]), dot4(xm, bv[3]));
+    q4o[nb] = q;
+    k4o[nb] = k;
+    v4o[nb] = v;
+    ks4[nb] = make_float4(k.x / k_div, k.y / k_div, k.z / k_div, k.w / k_div);
+#pragma unroll
+    for (int n = 0; n < NOUT; ++n) {
+      const float4* wn = reinterpret_cast<const float4*>(w_if + n * wl);
+      acc[n] += dot4(q, wn[nb]) + dot4(k, wn[(inner >> 2) + nb]) + dot4(v, wn[(inner >> 1) + nb]);
+    }
+  }
+  // lane (64 / NOUT) * n of each wave holds the wave's sum n
+  const float ws = transposed_wave_sum<NOUT>(acc);
+  const int lane = tid & 63, wave = tid >> 6;
+  if (lane % (64 / NOUT) == 0) red[wave][lane / (64 / NOUT)] = ws;
+  lds_barrier();
+  if (tid < NOUT) {
+    float t = seg == 0 ? b_if[tid] : 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) t += red[w2][tid];
+    if_part[((int64_t)seg * n_rows + row) * NOUT + tid] = t;
+  }
+}
+
 __global__ void to_bf16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
                                int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -527,6 +590,45 @@ int mlstm_qkv(const float* x_conv, const float* x_m, int64_t ld_xm, const float*
                      x_conv, x_m, ld_xm, wq, wk, wv, n_rows, inner, blk, k_div, qkv, ks);
   HK_LAUNCH_CHECK();
   return HK_OK;
+}
+
+int mlstm_qkv_if(const float* x_conv, const float* x_m, int64_t ld_xm, const float* wq,
+                 const float* wk, const float* wv, int n_rows, int inner, float k_div,
+                 const float* w_if, const float* b_if, int n_out, float* qkv, float* ks,
+                 float* if_part, int segs, hipStream_t s) {
+  if (n_rows == 0) return HK_OK;
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  HK_REQUIRE(mlstm_qkv_if_supported(inner, n_out, segs) && ld_xm % 4 == 0 && al16(x_conv) &&
+                 al16(x_m) && al16(wq) && al16(wk) && al16(wv) && al16(w_if) && al16(qkv) &&
+                 al16(ks),
+             "mlstm_qkv_if: inner %d, %d gate rows, %d segments or alignment unsupported", inner,
+             n_out, segs);
+  const dim3 grid(segs, n_rows), block(256);
+  switch (n_out) {
+    case 4:
+      hipLaunchKernelGGL(mlstm_qkv_if_kernel<4>, grid, block, 0, s, x_conv, x_m, ld_xm, wq, wk, wv,
+                         n_rows, inner, k_div, w_if, b_if, qkv, ks, if_part);
+      break;
+    case 8:
+      hipLaunchKernelGGL(mlstm_qkv_if_kernel<8>, grid, block, 0, s, x_conv, x_m, ld_xm, wq, wk, wv,
+                         n_rows, inner, k_div, w_if, b_if, qkv, ks, if_part);
+      break;
+    case 16:
+      hipLaunchKernelGGL(mlstm_qkv_if_kernel<16>, grid, block, 0, s, x_conv, x_m, ld_xm, wq, wk,
+                         wv, n_rows, inner, k_div, w_if, b_if, qkv, ks, if_part);
+      break;
+    default:
+      hipLaunchKernelGGL(mlstm_qkv_if_kernel<32>, grid, block, 0, s, x_conv, x_m, ld_xm, wq, wk,
+                         wv, n_rows, inner, k_div, w_if, b_if, qkv, ks, if_part);
+      break;
+  }
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+bool mlstm_qkv_if_supported(int inner, int n_out, int segs) {
+  return (n_out == 4 || n_out == 8 || n_out == 16 || n_out == 32) && inner % 4 == 0 && segs >= 1 &&
+         (inner / 4) % segs == 0;
 }
 
 int to_bf16(const float* src, uint16_t* dst, int64_t n, hipStream_t s) {

@@ -599,12 +599,13 @@ __global__ void slstm_final_kernel(const int* __restrict__ slot_ids,
     h_state[(int64_t)slot * hidden + c] = y[(int64_t)last * hidden + c];
 }
 
-// mLSTM gate / normaliser recurrence (model/kernels.py:143-151), one
+// mLSTM gate / normaliser recurrence (model/xlstm.py:61-74, :140-142), one
 // work-group of NWV waves per (run, head): thread i holds elements
 // [i*PER, i*PER + PER) of the head's normaliser n (threads past hs hold
 // zeros). Steps run in order in blocks of kGateBlock:
 //  - the stabiliser chain m_t = max(i_t, m_{t-1} + logsigmoid(f_t)) and the
-//    gates i', f' of the block's steps first (wave-uniform values);
+//    gates i', f' of the block's steps first (wave-uniform values; the gate
+//    pre-activations may arrive as n_parts partial sums, added in order);
 //  - then n_t = f'_t n_{t-1} + i'_t k_t and each thread's part of q_t . n_t
 //    for every step of the block;
 //  - then the block's dot products are summed together: a transposed
@@ -618,7 +619,7 @@ constexpr int kGateBlock = 8;
 template <int NWV, int PER>
 __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
     const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ if_pre,
-    int heads, const float* __restrict__ qkv, int inner, const float* __restrict__ ks,
+    int n_parts, int64_t part_stride, int heads, const float* __restrict__ qkv, int inner, const float* __restrict__ ks,
     float* __restrict__ n_state, float* __restrict__ m_state, float* __restrict__ ig_out,
     float* __restrict__ fg_out, float* __restrict__ den_out) {
   constexpr int B = kGateBlock;
@@ -672,7 +673,9 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
       get(qh + row * 3 * inner, q[j]);
       get(kh + row * inner, k[j]);
     }
-    g = gh[(int64_t)min(r0 + tb + gj, rl) * 2 * heads];
+    const float* gp = gh + (int64_t)min(r0 + tb + gj, rl) * 2 * heads;
+    g = gp[0];
+    for (int p = 1; p < n_parts; ++p) g += gp[p * part_stride];
   };
   fill(rq[0], rk[0], rg[0], 0);
   fill(rq[1], rk[1], rg[1], B);
@@ -702,21 +705,8 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
       for (int p = 0; p < PER; ++p) d += q[j][p] * nv[p];
       pd[j] = d;
     }
-    // transposed butterfly: after level b, lane bit (5 - b) selects which
-    // half of the remaining steps the lane keeps
-    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
-    float a4[4], a2[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      a4[i] = (b5 ? pd[4 + i] : pd[i]) + __shfl_xor(b5 ? pd[i] : pd[4 + i], 32, 64);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      a2[i] = (b4 ? a4[2 + i] : a4[i]) + __shfl_xor(b4 ? a4[i] : a4[2 + i], 16, 64);
-    float a1 = (b3 ? a2[1] : a2[0]) + __shfl_xor(b3 ? a2[0] : a2[1], 8, 64);
-    a1 += __shfl_xor(a1, 4, 64);
-    a1 += __shfl_xor(a1, 2, 64);
-    a1 += __shfl_xor(a1, 1, 64);
     // lane 8j holds step j's wave sum
+    float a1 = transposed_wave_sum<B>(pd);
     const int myj = lane >> 3;
     if constexpr (NWV > 1) {
       if ((lane & 7) == 0) red[par][wave][myj] = a1;
@@ -894,10 +884,11 @@ int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipSt
   return HK_OK;
 }
 
-int mlstm_gates(const Runs& r, const float* if_pre, int heads, const float* qkv, int inner,
-                const float* ks, float* n_state, float* m_state, float* ig, float* fg, float* den,
-                hipStream_t s) {
+int mlstm_gates(const Runs& r, const float* if_pre, int n_parts, int64_t part_stride, int heads,
+                const float* qkv, int inner, const float* ks, float* n_state, float* m_state,
+                float* ig, float* fg, float* den, hipStream_t s) {
   if (r.n_runs == 0) return HK_OK;
+  HK_REQUIRE(n_parts >= 1 && n_parts <= 8, "mlstm_gates: 1 to 8 partial gate sums");
   const int hs = inner / heads;
   HK_REQUIRE(inner % heads == 0 && hs >= 1 && hs <= 1024,
              "mlstm_gates: head size %d unsupported (at most 1024)", hs);
@@ -911,7 +902,8 @@ int mlstm_gates(const Runs& r, const float* if_pre, int heads, const float* qkv,
   const dim3 grid(r.n_runs * heads), block(64 * nwv);
 #define HK_GATES(W, P)                                                                    \
   hipLaunchKernelGGL((mlstm_gates_kernel<W, P>), grid, block, 0, s, r.slot_ids, r.run_off, \
-                     if_pre, heads, qkv, inner, ks, n_state, m_state, ig, fg, den)
+                     if_pre, n_parts, part_stride, heads, qkv, inner, ks, n_state, m_state, ig, \
+                     fg, den)
   if (nwv == 1) {
     HK_GATES(1, 1);
   } else if (nwv == 2) {
