@@ -138,6 +138,14 @@ __device__ __forceinline__ float transposed_wave_sum(float (&v)[NV]) {
   return r;
 }
 
+// Element i of the sum of n planes `stride` floats apart, added in plane
+// order (split-row scan outputs).
+__device__ __forceinline__ float plane_sum(const float* p, int64_t i, int n, int64_t stride) {
+  float v = p[i];
+  for (int q = 1; q < n; ++q) v += p[i + q * stride];
+  return v;
+}
+
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` must hold
 // blockDim.x / 64 floats of LDS. Every thread gets the total.
 __device__ __forceinline__ float block_sum(float v, float* red) {

@@ -34,6 +34,11 @@ namespace {
 enum TowerType { kXLSTM = 0, kMamba2 = 1, kRetNet = 2, kHawk = 3 };
 constexpr int kTowers = 4;
 constexpr int kMaxIfSegments = 4;  // partial planes of the mLSTM gate pre-activations
+// Matrix-scan launches whose longest run has at least kRowSplitMinLen steps
+// are latency-bound on that run: their tile rows are split over up to
+// kMaxRowParts work-groups, and the scan's consumer adds the output planes.
+constexpr int kMaxRowParts = 4;
+constexpr int kRowSplitMinLen = 8;
 
 // ---- weight slots ----------------------------------------------------------
 // Block-level slots common to every tower type.
@@ -334,7 +339,7 @@ int build_workspace(Engine& e) {
         w.IG = e.alloc_f(R * d.nh);
         w.FG = e.alloc_f(R * d.nh);
         w.DEN = e.alloc_f(R * d.nh);
-        w.NUM = e.alloc_f(R * d.I);
+        w.NUM = e.alloc_f(R * d.I * kMaxRowParts);
         w.HS = e.alloc_act(R * d.I, false);
         w.X2 = e.alloc_f(R * d.H);
         if (!w.XN || !w.XCA || !w.GIN || !w.SY || !w.X1 || any_null(w.XN2, false, e.lowp) ||
@@ -350,7 +355,7 @@ int build_workspace(Engine& e) {
         w.DTS = e.alloc_f(R * d.nhm);
         w.DEC = e.alloc_f(R * d.nhm);
         w.MXC = e.alloc_f(R * C);
-        w.YS = e.alloc_f(R * d.Im);
+        w.YS = e.alloc_f(R * d.Im * kMaxRowParts);
         w.YN = e.alloc_act(R * d.Im, false);
         if (!w.PROJ || !w.DTR || !w.DTS || !w.DEC || !w.MXC || !w.YS ||
             any_null(w.YN, false, e.lowp))
@@ -362,7 +367,7 @@ int build_workspace(Engine& e) {
         w.QKVG = e.alloc_f(R * 4 * d.H);
         w.KR = e.alloc_f(R * d.H);
         w.QS = e.alloc_f(R * d.H);
-        w.O = e.alloc_f(R * d.H);
+        w.O = e.alloc_f(R * d.H * kMaxRowParts);
         w.YO = e.alloc_act(R * d.H, false);
         if (!w.QKVG || !w.KR || !w.QS || !w.O || any_null(w.YO, false, e.lowp)) return HK_ERR_HIP;
         max_n = std::max<int64_t>(max_n, 4 * d.H);
@@ -521,6 +526,13 @@ int if_segments(int inner) {
   return sg;
 }
 
+int row_parts(const Runs& r, int rows) {
+  if (r.max_len < kRowSplitMinLen) return 1;
+  int p = kMaxRowParts;
+  while (p > 1 && rows % (4 * p) != 0) p /= 2;
+  return p;
+}
+
 int timed_mat_scan(Engine& e, int kind, const MatScanDesc& m, hipStream_t s) {
   return timed(e, kind, s, [&] { return launch_mat_scan(m, s); });
 }
@@ -633,8 +645,10 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   m.out = w.NUM;
   m.out_row_stride = I;
   m.out_head_stride = d.hs_m;
+  m.row_parts = row_parts(r, d.hs_m);
+  m.out_part_stride = (int64_t)n * I;
   HK_TRY(timed_mat_scan(e, 0, m, s));
-  HK_TRY(mlstm_post(w.NUM, w.DEN, d.nh, F32(e, kXLSTM, l, X_L_GN_W), F32(e, kXLSTM, l, X_L_GN_B),
+  HK_TRY(mlstm_post(w.NUM, m.row_parts, m.out_part_stride, w.DEN, d.nh, F32(e, kXLSTM, l, X_L_GN_W), F32(e, kXLSTM, l, X_L_GN_B),
                     F32(e, kXLSTM, l, X_L_SKIP), w.XMC, w.XMG + I, 2 * I, n, I, d.nh, w.HS.f,
                     w.HS.l, s));
   HK_TRY(linear(e, w, w.HS, I, {S(e, kXLSTM, l, X_L_DOWN_W), nullptr}, n, H, I, 0, w.X1, H, w.X2,
@@ -682,8 +696,11 @@ int run_mamba2(Engine& e, int l, const Runs& r, hipStream_t s) {
   m.out = w.YS;
   m.out_row_stride = I;
   m.out_head_stride = d.hm;
+  // (not split: the 128-row tile leaves too little work per part, and this
+  // tower's stream is not the one that ends the tick)
+  m.out_part_stride = (int64_t)n * I;
   HK_TRY(timed_mat_scan(e, 1, m, s));
-  HK_TRY(mamba2_post(w.YS, w.MXC, C, w.PROJ + C, W, F32(e, kMamba2, l, M_D),
+  HK_TRY(mamba2_post(w.YS, m.row_parts, m.out_part_stride, w.MXC, C, w.PROJ + C, W, F32(e, kMamba2, l, M_D),
                      F32(e, kMamba2, l, M_NORM), n, I, d.hm, w.YN.f, w.YN.l, s));
   HK_TRY(linear(e, w, w.YN, I, {S(e, kMamba2, l, M_OUT_W), nullptr}, n, H, I, 0, w.X.f, H, w.X.f,
                 H, nullptr, 0, s));
@@ -723,8 +740,11 @@ int run_retnet(Engine& e, int l, const Runs& r, hipStream_t s) {
   m.out = w.O;
   m.out_row_stride = H;
   m.out_head_stride = d.hs_r;
+  m.row_parts = row_parts(r, d.hs_r);
+  m.out_part_stride = (int64_t)n * H;
   HK_TRY(timed_mat_scan(e, 2, m, s));
-  HK_TRY(retnet_post(w.O, w.QKVG + 3 * H, 4 * H, n, H, d.hs_r, w.YO.f, w.YO.l, s));
+  HK_TRY(retnet_post(w.O, m.row_parts, m.out_part_stride, w.QKVG + 3 * H, 4 * H, n, H, d.hs_r,
+                     w.YO.f, w.YO.l, s));
   HK_TRY(linear(e, w, w.YO, H, {S(e, kRetNet, l, R_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f,
                 H, nullptr, 0, s));
   return HK_OK;
@@ -1237,7 +1257,7 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   HK_CHECK_HIP(hipEventRecord(e.stage_done[k], s));
 
   hk::Group all;
-  all.r = hk::Runs{e.d_slots, e.d_off, n_runs, n_rows};
+  all.r = hk::Runs{e.d_slots, e.d_off, n_runs, n_rows, steps};
   all.act_dev = e.d_act;
   all.act.assign(h_act, h_act + steps);
   HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, s));
@@ -1249,10 +1269,10 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   HK_TRY(hk::run_tower(e, hk::kHawk, all, preds_dev, e.side[2]));
   if (split < n_runs) {
     hk::Group g1, g2;
-    g1.r = hk::Runs{e.d_slots, e.d_off, split, row_split};
+    g1.r = hk::Runs{e.d_slots, e.d_off, split, row_split, steps};
     g1.act_dev = e.d_act1;
     g1.act.assign(h_act1, h_act1 + steps);
-    g2.r = hk::Runs{e.d_slots + split, e.d_off2, n_runs - split, n_rows - row_split};
+    g2.r = hk::Runs{e.d_slots + split, e.d_off2, n_runs - split, n_rows - row_split, steps2};
     g2.act_dev = e.d_act2;
     g2.act.assign(h_act2, h_act2 + steps2);
     g2.row0 = row_split;

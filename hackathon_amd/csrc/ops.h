@@ -14,6 +14,7 @@ struct Runs {
   const int* run_off = nullptr;   // device [n_runs + 1]
   int n_runs = 0;
   int n_rows = 0;
+  int max_len = 0;                // steps of the longest run (host)
 };
 
 // ---- row kernels (rowops.hip) ---------------------------------------------
@@ -28,19 +29,22 @@ int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, u
                    hipStream_t s);
 
 // Mamba2 tail before out_proj (model/mamba2.py:158-164):
-// y = (ssm_out + d[head] * x) * silu(z); RMSNorm(eps 1e-5) * w.
-int mamba2_post(const float* ssm_out, const float* x, int64_t ldx, const float* z, int64_t ldz,
-                const float* d, const float* w, int n_rows, int inner, int head_size,
-                float* out, uint16_t* out_lp, hipStream_t s);
+// y = (ssm_out + d[head] * x) * silu(z); RMSNorm(eps 1e-5) * w. ssm_out is
+// the sum of n_parts planes part_stride floats apart (split-row scan).
+int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const float* x,
+                int64_t ldx, const float* z, int64_t ldz, const float* d, const float* w,
+                int n_rows, int inner, int head_size, float* out, uint16_t* out_lp,
+                hipStream_t s);
 
 // dt = softplus(dt_raw); decay = exp(a[head] * dt) (model/mamba2.py:92-97).
 int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float* dt,
               float* decay, hipStream_t s);
 
 // RetNet tail before out_proj (model/retnet.py:168-169): per-head RMSNorm
-// (eps 1e-6, no affine), times silu(g).
-int retnet_post(const float* o, const float* g, int64_t ldg, int n_rows, int hidden,
-                int head_size, float* out, uint16_t* out_lp, hipStream_t s);
+// (eps 1e-6, no affine), times silu(g). o is the sum of n_parts planes.
+int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g, int64_t ldg,
+                int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp,
+                hipStream_t s);
 
 // sLSTM block tail + mLSTM block norm (model/xlstm.py:422-424, :308):
 // x1 = GroupNorm(groups)(y) + skip; xn = LayerNorm(x1) * w_ln.
@@ -62,10 +66,11 @@ int layernorm_rows(const float* x, const float* w, const float* residual, int n_
 
 // mLSTM cell/block tail (model/xlstm.py:236-241, :321-322):
 // out = GroupNorm(num / den) ; h = (out + skip * x_conv) * silu(x_gate).
-int mlstm_post(const float* num, const float* den, int den_ld, const float* gn_w,
-               const float* gn_b, const float* skip_w, const float* x_conv, const float* x_gate,
-               int64_t ld_gate, int n_rows, int inner, int heads, float* out, uint16_t* out_lp,
-               hipStream_t s);
+// num is the sum of n_parts planes part_stride floats apart.
+int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* den, int den_ld,
+               const float* gn_w, const float* gn_b, const float* skip_w, const float* x_conv,
+               const float* x_gate, int64_t ld_gate, int n_rows, int inner, int heads,
+               float* out, uint16_t* out_lp, hipStream_t s);
 
 // preds[r, col] = x[r] . w + b (shared output_proj, model/inference_model.py:142).
 int output_proj(const float* x, const float* w, const float* b, int n_rows, int hidden,

@@ -4,6 +4,8 @@
 // formulas (mean of squares / biased variance over the normalised extent,
 // eps inside the square root); reductions run in a fixed order, so a row's
 // result does not depend on the batch it rides in.
+#include <algorithm>
+
 #include "ops.h"
 
 namespace hk {
@@ -172,30 +174,39 @@ __global__ void stage_features_kernel(const float* __restrict__ feat, int n_rows
   }
 }
 
+// Row values held in registers (inner <= 256 * kMambaPostMax).
+constexpr int kMambaPostMax = 32;
 __global__ __launch_bounds__(256) void mamba2_post_kernel(
-    const float* __restrict__ ssm_out, const float* __restrict__ x, int64_t ldx,
-    const float* __restrict__ z, int64_t ldz, const float* __restrict__ d,
-    const float* __restrict__ w, int inner, int head_size, float* __restrict__ out,
-    uint16_t* __restrict__ out_lp) {
+    const float* __restrict__ ssm_out, int n_parts, int64_t part_stride,
+    const float* __restrict__ x, int64_t ldx, const float* __restrict__ z, int64_t ldz,
+    const float* __restrict__ d, const float* __restrict__ w, int inner, int head_size,
+    float* __restrict__ out, uint16_t* __restrict__ out_lp) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
-  const float* so = ssm_out + row * inner;
   const float* xr = x + row * ldx;
   const float* zr = z + row * ldz;
+  float yv[kMambaPostMax];
   float ss = 0.0f;
-#pragma unroll 8
-  for (int c = threadIdx.x; c < inner; c += 256) {
-    const float y = (so[c] + d[c / head_size] * xr[c]) * silu(zr[c]);
-    ss += y * y;
+#pragma unroll
+  for (int u = 0; u < kMambaPostMax; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    yv[u] = 0.0f;
+    if (c < inner) {
+      const float so = plane_sum(ssm_out, row * inner + c, n_parts, part_stride);
+      yv[u] = (so + d[c / head_size] * xr[c]) * silu(zr[c]);
+      ss += yv[u] * yv[u];
+    }
   }
   ss = block_sum(ss, red);
   const float inv = 1.0f / sqrtf(ss / (float)inner + 1e-5f);
-#pragma unroll 8
-  for (int c = threadIdx.x; c < inner; c += 256) {
-    const float y = (so[c] + d[c / head_size] * xr[c]) * silu(zr[c]);
-    const float o = (y * inv) * w[c];
-    if (out) out[row * inner + c] = o;
-    if (out_lp) out_lp[row * inner + c] = f32_to_bf16_bits(o);
+#pragma unroll
+  for (int u = 0; u < kMambaPostMax; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    if (c < inner) {
+      const float o = (yv[u] * inv) * w[c];
+      if (out) out[row * inner + c] = o;
+      if (out_lp) out_lp[row * inner + c] = f32_to_bf16_bits(o);
+    }
   }
 }
 
@@ -212,28 +223,35 @@ __global__ void mamba2_dt_kernel(const float* __restrict__ dt_raw, const float* 
 }
 
 // One wave per head.
-__global__ void retnet_post_kernel(const float* __restrict__ o, const float* __restrict__ g,
-                                   int64_t ldg, int hidden, int head_size,
-                                   float* __restrict__ out, uint16_t* __restrict__ out_lp) {
+// A head's values held in registers (head_size <= 64 * kHeadPostMax).
+constexpr int kHeadPostMax = 16;
+__global__ void retnet_post_kernel(const float* __restrict__ o, int n_parts, int64_t part_stride,
+                                   const float* __restrict__ g, int64_t ldg, int hidden,
+                                   int head_size, float* __restrict__ out,
+                                   uint16_t* __restrict__ out_lp) {
   const int64_t row = blockIdx.x;
   const int head = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const float* orow = o + row * hidden + (int64_t)head * head_size;
+  const int64_t ob = row * hidden + (int64_t)head * head_size;
   const float* grow = g + row * ldg + (int64_t)head * head_size;
+  float ov[kHeadPostMax];
   float ss = 0.0f;
-#pragma unroll 8
-  for (int j = lane; j < head_size; j += 64) {
-    const float v = orow[j];
-    ss += v * v;
+#pragma unroll
+  for (int u = 0; u < kHeadPostMax; ++u) {
+    const int j = lane + 64 * u;
+    ov[u] = j < head_size ? plane_sum(o, ob + j, n_parts, part_stride) : 0.0f;
+    ss += ov[u] * ov[u];
   }
   ss = wave_sum(ss);
   const float inv = 1.0f / sqrtf(ss / (float)head_size + 1e-6f);
-#pragma unroll 8
-  for (int j = lane; j < head_size; j += 64) {
-    const float v = silu(grow[j]) * (orow[j] * inv);
-    const int64_t idx = row * hidden + (int64_t)head * head_size + j;
-    if (out) out[idx] = v;
-    if (out_lp) out_lp[idx] = f32_to_bf16_bits(v);
+#pragma unroll
+  for (int u = 0; u < kHeadPostMax; ++u) {
+    const int j = lane + 64 * u;
+    if (j < head_size) {
+      const float v = silu(grow[j]) * (ov[u] * inv);
+      if (out) out[ob + j] = v;
+      if (out_lp) out_lp[ob + j] = f32_to_bf16_bits(v);
+    }
   }
 }
 
@@ -286,9 +304,10 @@ __global__ void slstm_post_kernel(const float* __restrict__ y, const float* __re
 }
 
 // One wave per head (= GroupNorm group).
-__global__ void mlstm_post_kernel(const float* __restrict__ num, const float* __restrict__ den,
-                                  int den_ld, const float* __restrict__ gn_w,
-                                  const float* __restrict__ gn_b, const float* __restrict__ skip_w,
+__global__ void mlstm_post_kernel(const float* __restrict__ num, int n_parts, int64_t part_stride,
+                                  const float* __restrict__ den, int den_ld,
+                                  const float* __restrict__ gn_w, const float* __restrict__ gn_b,
+                                  const float* __restrict__ skip_w,
                                   const float* __restrict__ x_conv,
                                   const float* __restrict__ x_gate, int64_t ld_gate, int inner,
                                   int hs, float* __restrict__ out, uint16_t* __restrict__ out_lp) {
@@ -297,24 +316,33 @@ __global__ void mlstm_post_kernel(const float* __restrict__ num, const float* __
   const int lane = threadIdx.x & 63;
   const int64_t base = row * inner + (int64_t)head * hs;
   const float dn = den[row * den_ld + head];
+  float hv[kHeadPostMax];  // num / den of this lane's elements
   float s = 0.0f;
-#pragma unroll 8
-  for (int j = lane; j < hs; j += 64) s += num[base + j] / dn;
+#pragma unroll
+  for (int u = 0; u < kHeadPostMax; ++u) {
+    const int j = lane + 64 * u;
+    hv[u] = j < hs ? plane_sum(num, base + j, n_parts, part_stride) / dn : 0.0f;
+    s += hv[u];
+  }
   const float mean = wave_sum(s) / (float)hs;
   float v = 0.0f;
-#pragma unroll 8
-  for (int j = lane; j < hs; j += 64) {
-    const float dlt = num[base + j] / dn - mean;
+#pragma unroll
+  for (int u = 0; u < kHeadPostMax; ++u) {
+    const int j = lane + 64 * u;
+    const float dlt = j < hs ? hv[u] - mean : 0.0f;
     v += dlt * dlt;
   }
   const float rstd = 1.0f / sqrtf(wave_sum(v) / (float)hs + 1e-5f);
-#pragma unroll 8
-  for (int j = lane; j < hs; j += 64) {
-    const int c = head * hs + j;
-    const float gnv = ((num[base + j] / dn - mean) * rstd) * gn_w[c] + gn_b[c];
-    const float h = (gnv + skip_w[c] * x_conv[base + j]) * silu(x_gate[row * ld_gate + c]);
-    if (out) out[base + j] = h;
-    if (out_lp) out_lp[base + j] = f32_to_bf16_bits(h);
+#pragma unroll
+  for (int u = 0; u < kHeadPostMax; ++u) {
+    const int j = lane + 64 * u;
+    if (j < hs) {
+      const int c = head * hs + j;
+      const float gnv = ((hv[u] - mean) * rstd) * gn_w[c] + gn_b[c];
+      const float h = (gnv + skip_w[c] * x_conv[base + j]) * silu(x_gate[row * ld_gate + c]);
+      if (out) out[base + j] = h;
+      if (out_lp) out_lp[base + j] = f32_to_bf16_bits(h);
+    }
   }
 }
 
@@ -371,7 +399,7 @@ __global__ void mlstm_qkv_kernel(const float* __restrict__ x_conv, const float* 
 // order) are segment seg's partial pre-activations, plane seg of if_part
 // [segs][n_rows][NOUT]; plane 0 also carries the bias.
 template <int NOUT>
-__global__ __launch_bounds__(256) void mlstm_qkv_if_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void mlstm_qkv_if_kernel(
     const float* __restrict__ x_conv, const float* __restrict__ x_m, int64_t ld_xm,
     const float* __restrict__ wq, const float* __restrict__ wk, const float* __restrict__ wv,
     int n_rows, int inner, float k_div, const float* __restrict__ w_if,
@@ -394,11 +422,26 @@ __global__ __launch_bounds__(256) void mlstm_qkv_if_kernel(
 #pragma unroll
   for (int n = 0; n < NOUT; ++n) acc[n] = 0.0f;
   for (int nb = seg * per + tid; nb < (seg + 1) * per; nb += 256) {
+    // Every operand of the block is loaded before any is used (one L2 round
+    // trip per block, not one per gate row).
     const float4 xc = xc4[nb], xm = xm4[nb];
     // W[nb][o][h]: block nb's 4x4 weights, row o = output column 4nb + o
-    const float4* bq = reinterpret_cast<const float4*>(wq) + (int64_t)nb * 4;
-    const float4* bk = reinterpret_cast<const float4*>(wk) + (int64_t)nb * 4;
-    const float4* bv = reinterpret_cast<const float4*>(wv) + (int64_t)nb * 4;
+    float4 bq[4], bk[4], bv[4];
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+      bq[o] = reinterpret_cast<const float4*>(wq)[(int64_t)nb * 4 + o];
+      bk[o] = reinterpret_cast<const float4*>(wk)[(int64_t)nb * 4 + o];
+      bv[o] = reinterpret_cast<const float4*>(wv)[(int64_t)nb * 4 + o];
+    }
+    // the gate rows' 16-byte pieces of this block's q, k and v columns
+    float4 wi[NOUT][3];
+#pragma unroll
+    for (int n = 0; n < NOUT; ++n) {
+      const float4* wn = reinterpret_cast<const float4*>(w_if + n * wl);
+      wi[n][0] = wn[nb];
+      wi[n][1] = wn[(inner >> 2) + nb];
+      wi[n][2] = wn[(inner >> 1) + nb];
+    }
     const float4 q = make_float4(dot4(xc, bq[0]), dot4(xc, bq[1]), dot4(xc, bq[2]), dot4(xc, bq[3]));
     const float4 k = make_float4(dot4(xc, bk[0]), dot4(xc, bk[1]), dot4(xc, bk[2]), dot4(xc, bk[3]));
     const float4 v = make_float4(dot4(xm, bv[0]), dot4(xm, bv[1]), dot4(xm, bv[2]), dot4(xm, bv[3]));
@@ -407,10 +450,8 @@ __global__ __launch_bounds__(256) void mlstm_qkv_if_kernel(
     v4o[nb] = v;
     ks4[nb] = make_float4(k.x / k_div, k.y / k_div, k.z / k_div, k.w / k_div);
 #pragma unroll
-    for (int n = 0; n < NOUT; ++n) {
-      const float4* wn = reinterpret_cast<const float4*>(w_if + n * wl);
-      acc[n] += dot4(q, wn[nb]) + dot4(k, wn[(inner >> 2) + nb]) + dot4(v, wn[(inner >> 1) + nb]);
-    }
+    for (int n = 0; n < NOUT; ++n)
+      acc[n] += dot4(q, wi[n][0]) + dot4(k, wi[n][1]) + dot4(v, wi[n][2]);
   }
   // lane (64 / NOUT) * n of each wave holds the wave's sum n
   const float ws = transposed_wave_sum<NOUT>(acc);
@@ -504,12 +545,15 @@ int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, u
   return HK_OK;
 }
 
-int mamba2_post(const float* ssm_out, const float* x, int64_t ldx, const float* z, int64_t ldz,
-                const float* d, const float* w, int n_rows, int inner, int head_size,
-                float* out, uint16_t* out_lp, hipStream_t s) {
+int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const float* x,
+                int64_t ldx, const float* z, int64_t ldz, const float* d, const float* w,
+                int n_rows, int inner, int head_size, float* out, uint16_t* out_lp,
+                hipStream_t s) {
   if (n_rows == 0) return HK_OK;
-  hipLaunchKernelGGL(mamba2_post_kernel, dim3(n_rows), dim3(256), 0, s, ssm_out, x, ldx, z, ldz,
-                     d, w, inner, head_size, out, out_lp);
+  HK_REQUIRE(inner <= 256 * kMambaPostMax && n_parts >= 1,
+             "mamba2_post: inner %d above %d or no planes", inner, 256 * kMambaPostMax);
+  hipLaunchKernelGGL(mamba2_post_kernel, dim3(n_rows), dim3(256), 0, s, ssm_out, n_parts,
+                     part_stride, x, ldx, z, ldz, d, w, inner, head_size, out, out_lp);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
@@ -523,14 +567,16 @@ int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float*
   return HK_OK;
 }
 
-int retnet_post(const float* o, const float* g, int64_t ldg, int n_rows, int hidden,
-                int head_size, float* out, uint16_t* out_lp, hipStream_t s) {
+int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g, int64_t ldg,
+                int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp,
+                hipStream_t s) {
   if (n_rows == 0) return HK_OK;
   const int heads = hidden / head_size;
-  HK_REQUIRE(heads * head_size == hidden && heads <= 16, "retnet_post: %d heads unsupported",
-             heads);
-  hipLaunchKernelGGL(retnet_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, o, g, ldg, hidden,
-                     head_size, out, out_lp);
+  HK_REQUIRE(heads * head_size == hidden && heads <= 16 && head_size <= 64 * kHeadPostMax &&
+                 n_parts >= 1,
+             "retnet_post: %d heads of %d unsupported", heads, head_size);
+  hipLaunchKernelGGL(retnet_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, o, n_parts,
+                     part_stride, g, ldg, hidden, head_size, out, out_lp);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
@@ -559,16 +605,17 @@ int layernorm_rows(const float* x, const float* w, const float* residual, int n_
   return HK_OK;
 }
 
-int mlstm_post(const float* num, const float* den, int den_ld, const float* gn_w,
-               const float* gn_b, const float* skip_w, const float* x_conv, const float* x_gate,
-               int64_t ld_gate, int n_rows, int inner, int heads, float* out, uint16_t* out_lp,
-               hipStream_t s) {
+int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* den, int den_ld,
+               const float* gn_w, const float* gn_b, const float* skip_w, const float* x_conv,
+               const float* x_gate, int64_t ld_gate, int n_rows, int inner, int heads,
+               float* out, uint16_t* out_lp, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
-  HK_REQUIRE(heads >= 1 && heads <= 16 && inner % heads == 0, "mlstm_post: %d heads unsupported",
-             heads);
-  hipLaunchKernelGGL(mlstm_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, num, den, den_ld,
-                     gn_w, gn_b, skip_w, x_conv, x_gate, ld_gate, inner, inner / heads, out,
-                     out_lp);
+  HK_REQUIRE(heads >= 1 && heads <= 16 && inner % heads == 0 &&
+                 inner / heads <= 64 * kHeadPostMax && n_parts >= 1,
+             "mlstm_post: %d heads of %d unsupported", heads, inner / std::max(heads, 1));
+  hipLaunchKernelGGL(mlstm_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, num, n_parts,
+                     part_stride, den, den_ld, gn_w, gn_b, skip_w, x_conv, x_gate, ld_gate, inner,
+                     inner / heads, out, out_lp);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }

@@ -37,6 +37,15 @@ struct MatScanDesc {
   Operand alpha, scale, beta, gamma, w;
   float* out = nullptr;
   int64_t out_row_stride = 0, out_head_stride = 0;
+  // Row split: with row_parts > 1 (rows a multiple of 4 * row_parts) each
+  // (run, head, column tile) is advanced by row_parts work-groups, part p
+  // owning rows [p * rows / row_parts, (p + 1) * rows / row_parts); part p
+  // writes its share of out_t (the sum over its rows) to out + p *
+  // out_part_stride, and the caller adds the planes in part order. The
+  // update of a state row never reads another row, so only the output sum
+  // is split; a long run then has row_parts times the parallelism per step.
+  int row_parts = 1;
+  int64_t out_part_stride = 0;
 };
 
 int launch_mat_scan(const MatScanDesc& d, hipStream_t stream);

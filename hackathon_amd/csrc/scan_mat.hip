@@ -38,7 +38,10 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
   // Column tile varies fastest in dispatch order: the work-groups of one
   // (run, head) tile stream adjacent segments of the same rows together.
   const int run = blockIdx.z;
-  const int head = blockIdx.y;
+  const int part = blockIdx.y % d.row_parts;
+  const int head = blockIdx.y / d.row_parts;
+  const int prows = d.rows / d.row_parts;  // this part's tile rows
+  const int row_off = part * prows;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -58,7 +61,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
     r0 = d.run_off[run];
     len = d.run_off[run + 1] - r0;
   }
-  float* out_base = d.out + (int64_t)head * d.out_head_stride;
+  float* out_base = d.out + (int64_t)head * d.out_head_stride + (int64_t)part * d.out_part_stride;
   if (len == 0) {
     // Idle row (reference API): state untouched, output defined as zero.
     if (wave == 0) {
@@ -69,11 +72,11 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
     return;
   }
 
-  // Rows past d.rows hold zero in LDS and in the tile, so they contribute
-  // nothing and need no branch in the inner loop.
+  // Rows past the part's rows hold zero in LDS and in the tile, so they
+  // contribute nothing and need no branch in the inner loop.
   for (int i = tid; i < kSteps * kRows; i += NT) {
     const int r = i % kRows;
-    if (r >= d.rows) {
+    if (r >= prows) {
       sb[i / kRows][r] = 0.0f;
       sw[i / kRows][r] = 0.0f;
     }
@@ -82,11 +85,12 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
   // Uniform tile base (scalar registers) + 32-bit per-lane offsets: a tile
   // spans well under 2^32 elements, and this keeps 64-bit address math out
   // of the unrolled row loops.
-  float* tbase = d.state + (int64_t)slot * d.slot_stride + (int64_t)head * d.head_stride;
+  float* tbase = d.state + (int64_t)slot * d.slot_stride + (int64_t)head * d.head_stride +
+                 (int64_t)row_off * d.row_stride;
   const int rbase = wave * RPW;
   const uint32_t rstride = (uint32_t)d.row_stride;
   const uint32_t off0 = (uint32_t)colv * (uint32_t)d.col_stride + (uint32_t)rbase * rstride;
-  const int rlim = d.rows - rbase;  // rows of this wave's slice that exist
+  const int rlim = prows - rbase;  // rows of this wave's slice that exist
   float s[RPW][VW];
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
@@ -103,15 +107,15 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
     }
   }
 
-  const float* beta_h = d.beta.ptr + (int64_t)head * d.beta.head_stride;
-  const float* w_h = d.w.ptr + (int64_t)head * d.w.head_stride;
+  const float* beta_h = d.beta.ptr + (int64_t)head * d.beta.head_stride + row_off;
+  const float* w_h = d.w.ptr + (int64_t)head * d.w.head_stride + row_off;
   for (int t0 = 0; t0 < len; t0 += kSteps) {
     const int ns = min(kSteps, len - t0);
     const int64_t row0 = r0 + t0;
     // ---- stage ns steps of row vectors, all loads in flight at once
     if constexpr (VEC) {
       constexpr int V = (kSteps * kRows / 4 + NT - 1) / NT;
-      const int vpr = d.rows >> 2;  // float4 per step
+      const int vpr = prows >> 2;  // float4 per step
       const int nv = ns * vpr;
       float4 vb[V], vw[V];
 #pragma unroll
@@ -144,9 +148,9 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
         }
       }
     } else {
-      for (int i = tid; i < ns * d.rows; i += NT) {
-        const int st = i / d.rows;
-        const int k = i - st * d.rows;
+      for (int i = tid; i < ns * prows; i += NT) {
+        const int st = i / prows;
+        const int k = i - st * prows;
         const int64_t row = row0 + st;
         const float sc = d.scale.ptr ? d.scale.ptr[row * d.scale.row_stride +
                                                    head * d.scale.head_stride]
@@ -229,41 +233,45 @@ int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
   HK_REQUIRE(d.rows > 0 && d.cols > 0 && d.heads > 0, "mat_scan: empty tile %dx%d heads %d",
              d.rows, d.cols, d.heads);
   HK_REQUIRE(d.per_row || (d.slot_ids && d.run_off), "mat_scan: need run descriptors");
-  HK_REQUIRE(d.heads <= 65535, "mat_scan: too many heads");
+  HK_REQUIRE(d.row_parts >= 1 && (d.row_parts == 1 || d.rows % (4 * d.row_parts) == 0),
+             "mat_scan: %d rows do not split into %d parts of a multiple of 4", d.rows,
+             d.row_parts);
+  HK_REQUIRE((int64_t)d.heads * d.row_parts <= 65535, "mat_scan: too many heads");
+  const int prows = d.rows / d.row_parts;
   HK_REQUIRE((int64_t)d.rows * d.row_stride + (int64_t)d.cols * d.col_stride < (1LL << 32),
              "mat_scan: tile too large for 32-bit offsets");
   if (d.n_runs == 0) return HK_OK;
   HK_REQUIRE(d.n_runs <= 65535, "mat_scan: at most 65535 runs per launch");
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  const bool vec = d.rows % 4 == 0 && al16(d.beta.ptr) && al16(d.w.ptr) &&
+  const bool vec = prows % 4 == 0 && al16(d.beta.ptr) && al16(d.w.ptr) &&
                    d.beta.row_stride % 4 == 0 && d.beta.head_stride % 4 == 0 &&
                    d.w.row_stride % 4 == 0 && d.w.head_stride % 4 == 0;
   // 256-row tiles with whole 128-column tiles, unit column stride and 8-byte
   // aligned rows: 8 waves x float2 columns. 512-row tiles: 8 waves x 64 rows
   // (wider tiles there exceed the register file of an 8-wave work-group).
-  const bool wide = d.rows > 128 && d.cols % 128 == 0 && d.col_stride == 1 &&
+  const bool wide = prows > 128 && d.cols % 128 == 0 && d.col_stride == 1 &&
                     d.row_stride % 2 == 0 && d.head_stride % 2 == 0 && d.slot_stride % 2 == 0 &&
                     (reinterpret_cast<uintptr_t>(d.state) & 7) == 0;
 #define HK_SCAN_LAUNCH(R, NW, VW)                                                          \
   {                                                                                        \
-    dim3 grid((d.cols + 64 * VW - 1) / (64 * VW), d.heads, d.n_runs);                      \
+    dim3 grid((d.cols + 64 * VW - 1) / (64 * VW), d.heads * d.row_parts, d.n_runs);        \
     if (vec)                                                                               \
       hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, true>), grid, dim3(64 * NW), 0, stream, d); \
     else                                                                                   \
       hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, false>), grid, dim3(64 * NW), 0, stream, d); \
   }
-  if (d.rows <= 32) {
+  if (prows <= 32) {
     HK_SCAN_LAUNCH(8, 4, 1)
-  } else if (d.rows <= 64) {
+  } else if (prows <= 64) {
     HK_SCAN_LAUNCH(16, 4, 1)
-  } else if (d.rows <= 128) {
+  } else if (prows <= 128) {
     HK_SCAN_LAUNCH(32, 4, 1)
-  } else if (d.rows <= 256) {
+  } else if (prows <= 256) {
     if (wide) HK_SCAN_LAUNCH(32, 8, 2) else HK_SCAN_LAUNCH(64, 4, 1)
-  } else if (d.rows <= 512) {
+  } else if (prows <= 512) {
     HK_SCAN_LAUNCH(64, 8, 1)
   } else {
-    HK_REQUIRE(false, "mat_scan: %d rows exceeds the 512-row tile", d.rows);
+    HK_REQUIRE(false, "mat_scan: %d rows per part exceed the 512-row tile", prows);
   }
 #undef HK_SCAN_LAUNCH
   HK_LAUNCH_CHECK();
