@@ -38,7 +38,7 @@ constexpr int kMaxIfSegments = 4;  // partial planes of the mLSTM gate pre-activ
 // are latency-bound on that run: their tile rows are split over up to
 // kMaxRowParts work-groups, and the scan's consumer adds the output planes.
 constexpr int kMaxRowParts = 4;
-constexpr int kRowSplitMinLen = 8;
+constexpr int kRowSplitMinLen = 16;
 
 // ---- weight slots ----------------------------------------------------------
 // Block-level slots common to every tower type.
