@@ -23,7 +23,9 @@ constexpr int kSteps = 8;  // steps whose row vectors are staged per LDS block
 // The 512-row tile (8 waves x 64 rows) is held to 128 VGPRs (4 waves per
 // SIMD) so that two work-groups share a CU: one streams its state tile in or
 // out while the other computes.
-template <int RPW, int NW, int VW, bool VEC>
+// SPLIT: the launch splits tile rows (row_parts > 1); without it the
+// row-part arithmetic folds away.
+template <int RPW, int NW, int VW, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_scan_kernel(
     MatScanDesc d) {
   constexpr int kRows = NW * RPW;
@@ -38,9 +40,10 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
   // Column tile varies fastest in dispatch order: the work-groups of one
   // (run, head) tile stream adjacent segments of the same rows together.
   const int run = blockIdx.z;
-  const int part = blockIdx.y % d.row_parts;
-  const int head = blockIdx.y / d.row_parts;
-  const int prows = d.rows / d.row_parts;  // this part's tile rows
+  const int parts = SPLIT ? d.row_parts : 1;
+  const int part = SPLIT ? (int)blockIdx.y % parts : 0;
+  const int head = SPLIT ? (int)blockIdx.y / parts : (int)blockIdx.y;
+  const int prows = d.rows / parts;  // this part's tile rows
   const int row_off = part * prows;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -252,13 +255,20 @@ int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
   const bool wide = prows > 128 && d.cols % 128 == 0 && d.col_stride == 1 &&
                     d.row_stride % 2 == 0 && d.head_stride % 2 == 0 && d.slot_stride % 2 == 0 &&
                     (reinterpret_cast<uintptr_t>(d.state) & 7) == 0;
-#define HK_SCAN_LAUNCH(R, NW, VW)                                                          \
-  {                                                                                        \
-    dim3 grid((d.cols + 64 * VW - 1) / (64 * VW), d.heads * d.row_parts, d.n_runs);        \
-    if (vec)                                                                               \
-      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, true>), grid, dim3(64 * NW), 0, stream, d); \
-    else                                                                                   \
-      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, false>), grid, dim3(64 * NW), 0, stream, d); \
+#define HK_SCAN_LAUNCH_S(R, NW, VW, SP)                                                     \
+  {                                                                                          \
+    dim3 grid((d.cols + 64 * VW - 1) / (64 * VW), d.heads * d.row_parts, d.n_runs);          \
+    if (vec)                                                                                 \
+      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, true, SP>), grid, dim3(64 * NW), 0, stream, \
+                         d);                                                                 \
+    else                                                                                     \
+      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, false, SP>), grid, dim3(64 * NW), 0,      \
+                         stream, d);                                                         \
+  }
+#define HK_SCAN_LAUNCH(R, NW, VW)                              \
+  {                                                            \
+    if (d.row_parts > 1) HK_SCAN_LAUNCH_S(R, NW, VW, true)     \
+    else HK_SCAN_LAUNCH_S(R, NW, VW, false)                    \
   }
   if (prows <= 32) {
     HK_SCAN_LAUNCH(8, 4, 1)
@@ -274,6 +284,7 @@ int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
     HK_REQUIRE(false, "mat_scan: %d rows per part exceed the 512-row tile", prows);
   }
 #undef HK_SCAN_LAUNCH
+#undef HK_SCAN_LAUNCH_S
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
