@@ -276,6 +276,7 @@ struct Engine {
     for (auto& v : sl_ev)
       for (auto& ev : v)
         if (ev) (void)hipEventDestroy(ev);
+
     for (auto& v : prof_ev)
       for (auto& pr : v) {
         (void)hipEventDestroy(pr.first);
@@ -423,6 +424,7 @@ int build_workspace(Engine& e) {
     v.assign(d.D, nullptr);
     for (auto& ev : v) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   }
+
   return HK_OK;
 }
 
@@ -824,30 +826,43 @@ int tower_tail(Engine& e, int t, TowerWS& w, const Group& g, float* preds, hipSt
                      preds + (int64_t)g.row0 * kTowers, kTowers, t, s);
 }
 
-int run_tower(Engine& e, int t, const Group& g, float* preds, hipStream_t s) {
-  TowerWS& w = e.ws[t];
-  HK_TRY(tower_head(e, t, w, g, s));
-  for (int l = 0; l < e.d.D; ++l) HK_TRY(tower_layer(e, t, w, g, l, e.d_xch, SlOrder{}, s));
-  return tower_tail(e, t, w, g, preds, s);
-}
-
-// The xLSTM tower over two run groups on two streams, enqueued layer by
-// layer so that each persistent sLSTM launch waits on the other group's
-// previous one (g2 layer l after g1 layer l-1, g1 layer l after g2 layer l).
-int run_xlstm_split(Engine& e, const Group& g1, hipStream_t s1, const Group& g2, hipStream_t s2,
-                    float* preds) {
+// Every tower of the tick, enqueued layer by layer: the xLSTM on the caller's
+// stream s (run group g1) and, when split, side[0] (group g2); Mamba2 on
+// side[1]; RetNet and Hawk on side[2].
+// - The two xLSTM groups' persistent sLSTM launches alternate (g2 layer l
+//   after g1 layer l-1, g1 layer l after g2 layer l), so two persistent
+//   launches never compete for co-residency.
+// (Pacing the side towers' layers to the xLSTM's, so that their HBM traffic
+// spreads over the whole tick, measured no faster: the sLSTM chain then
+// meets the same traffic later.)
+int run_towers(Engine& e, const Group& all, const Group& g1, const Group* g2, hipStream_t s,
+                     float* preds) {
   TowerWS& w1 = e.ws[kXLSTM];
   TowerWS& w2 = e.ws_x2;
-  HK_TRY(tower_head(e, kXLSTM, w1, g1, s1));
-  HK_TRY(tower_head(e, kXLSTM, w2, g2, s2));
+  HK_TRY(tower_head(e, kMamba2, e.ws[kMamba2], all, e.side[1]));
+  HK_TRY(tower_head(e, kRetNet, e.ws[kRetNet], all, e.side[2]));
+  HK_TRY(tower_head(e, kHawk, e.ws[kHawk], all, e.side[2]));
+  HK_TRY(tower_head(e, kXLSTM, w1, g1, s));
+  if (g2) HK_TRY(tower_head(e, kXLSTM, w2, *g2, e.side[0]));
   for (int l = 0; l < e.d.D; ++l) {
-    SlOrder o2{l > 0 ? e.sl_ev[0][l - 1] : nullptr, e.sl_ev[1][l]};
-    HK_TRY(tower_layer(e, kXLSTM, w2, g2, l, e.d_xch2, o2, s2));
-    SlOrder o1{e.sl_ev[1][l], e.sl_ev[0][l]};
-    HK_TRY(tower_layer(e, kXLSTM, w1, g1, l, e.d_xch, o1, s1));
+    if (g2) {
+      SlOrder o2{l > 0 ? e.sl_ev[0][l - 1] : nullptr, e.sl_ev[1][l]};
+      HK_TRY(tower_layer(e, kXLSTM, w2, *g2, l, e.d_xch2, o2, e.side[0]));
+      SlOrder o1{e.sl_ev[1][l], e.sl_ev[0][l]};
+      HK_TRY(tower_layer(e, kXLSTM, w1, g1, l, e.d_xch, o1, s));
+    } else {
+      HK_TRY(tower_layer(e, kXLSTM, w1, g1, l, e.d_xch, SlOrder{}, s));
+    }
+    HK_TRY(tower_layer(e, kMamba2, e.ws[kMamba2], all, l, nullptr, SlOrder{}, e.side[1]));
+    HK_TRY(tower_layer(e, kRetNet, e.ws[kRetNet], all, l, nullptr, SlOrder{}, e.side[2]));
+    HK_TRY(tower_layer(e, kHawk, e.ws[kHawk], all, l, nullptr, SlOrder{}, e.side[2]));
   }
-  HK_TRY(tower_tail(e, kXLSTM, w1, g1, preds, s1));
-  return tower_tail(e, kXLSTM, w2, g2, preds, s2);
+  HK_TRY(tower_tail(e, kMamba2, e.ws[kMamba2], all, preds, e.side[1]));
+  HK_TRY(tower_tail(e, kRetNet, e.ws[kRetNet], all, preds, e.side[2]));
+  HK_TRY(tower_tail(e, kHawk, e.ws[kHawk], all, preds, e.side[2]));
+  HK_TRY(tower_tail(e, kXLSTM, w1, g1, preds, s));
+  if (g2) HK_TRY(tower_tail(e, kXLSTM, w2, *g2, preds, e.side[0]));
+  return HK_OK;
 }
 
 // Where to split the length-sorted runs into two xLSTM groups (returns
@@ -1263,10 +1278,6 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, s));
   HK_CHECK_HIP(hipEventRecord(e.fork_ev, s));
   for (int i = 0; i < Engine::kSide; ++i) HK_CHECK_HIP(hipStreamWaitEvent(e.side[i], e.fork_ev, 0));
-  // Mamba2 on side[1]; RetNet then Hawk on side[2].
-  HK_TRY(hk::run_tower(e, hk::kMamba2, all, preds_dev, e.side[1]));
-  HK_TRY(hk::run_tower(e, hk::kRetNet, all, preds_dev, e.side[2]));
-  HK_TRY(hk::run_tower(e, hk::kHawk, all, preds_dev, e.side[2]));
   if (split < n_runs) {
     hk::Group g1, g2;
     g1.r = hk::Runs{e.d_slots, e.d_off, split, row_split, steps};
@@ -1276,9 +1287,9 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
     g2.act_dev = e.d_act2;
     g2.act.assign(h_act2, h_act2 + steps2);
     g2.row0 = row_split;
-    HK_TRY(hk::run_xlstm_split(e, g1, s, g2, e.side[0], preds_dev));
+    HK_TRY(hk::run_towers(e, all, g1, &g2, s, preds_dev));
   } else {
-    HK_TRY(hk::run_tower(e, hk::kXLSTM, all, preds_dev, s));
+    HK_TRY(hk::run_towers(e, all, all, nullptr, s, preds_dev));
   }
   for (int i = 0; i < Engine::kSide; ++i) {
     HK_CHECK_HIP(hipEventRecord(e.join_ev[i], e.side[i]));
