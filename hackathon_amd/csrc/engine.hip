@@ -38,6 +38,9 @@ constexpr int kMaxIfSegments = 4;  // partial planes of the mLSTM gate pre-activ
 // are latency-bound on that run: their tile rows are split over up to
 // kMaxRowParts work-groups, and the scan's consumer adds the output planes.
 constexpr int kMaxRowParts = 4;
+// Pending rank-1 updates a matrix-state tile may carry before its write-back
+// (one staging block of the scan).
+constexpr int kLogCap = 8;
 constexpr int kRowSplitMinLen = 16;
 
 // ---- weight slots ----------------------------------------------------------
@@ -225,6 +228,14 @@ struct Engine {
   // state[tower][layer][leaf] -> device base, per-slot elements
   std::vector<std::vector<std::vector<float*>>> state;
   std::vector<std::vector<int64_t>> leaf_elems;
+  // Write-back logs of the matrix-state leaves, [tower][layer] (null for
+  // Hawk): see MatScanDesc.
+  struct MatLog {
+    float* hdr = nullptr;
+    float* b = nullptr;
+    float* g = nullptr;
+  };
+  std::vector<std::vector<MatLog>> mlog;
   TowerWS ws[kTowers];
   TowerWS ws_x2;             // xLSTM workspace of the second run group
   Act FE;
@@ -528,6 +539,42 @@ int if_segments(int inner) {
   return sg;
 }
 
+// The matrix-state leaf of tower t (-1: none).
+int matrix_leaf(int t) {
+  return t == kXLSTM ? XS_L_C : t == kMamba2 ? MS_SSM : t == kRetNet ? RS_S : -1;
+}
+
+// Layout and write-back log of tower t's matrix state at layer l (the scan
+// operands are the caller's).
+MatScanDesc mat_state_desc(const Engine& e, int t, int l) {
+  const Dims& d = e.d;
+  const int leaf = matrix_leaf(t);
+  MatScanDesc m;
+  m.state = e.state[t][l][leaf];
+  m.slot_stride = e.leaf_elems[t][leaf];
+  if (t == kXLSTM) {
+    m.rows = m.cols = d.hs_m;
+    m.heads = d.nh;
+  } else if (t == kMamba2) {
+    // SSM state stored [head][c][h]: tile rows are the contracted bc axis.
+    m.rows = d.bc;
+    m.cols = d.hm;
+    m.heads = d.nhm;
+  } else {
+    m.rows = m.cols = d.hs_r;
+    m.heads = d.nh;
+  }
+  m.row_stride = m.cols;
+  m.col_stride = 1;
+  m.head_stride = (int64_t)m.rows * m.cols;
+  const Engine::MatLog& lg = e.mlog[t][l];
+  m.log_hdr = lg.hdr;
+  m.log_b = lg.b;
+  m.log_g = lg.g;
+  m.log_cap = lg.hdr ? kLogCap : 0;
+  return m;
+}
+
 int row_parts(const Runs& r, int rows) {
   if (r.max_len < kRowSplitMinLen) return 1;
   int p = kMaxRowParts;
@@ -627,15 +674,7 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
     HK_TRY(mlstm_gates(r, w.IF, 1, 0, d.nh, w.QKV, I, w.KS, st[XS_L_N], st[XS_L_M], w.IG, w.FG,
                        w.DEN, s));
   }
-  MatScanDesc m;
-  m.state = st[XS_L_C];
-  m.rows = d.hs_m;
-  m.cols = d.hs_m;
-  m.heads = d.nh;
-  m.row_stride = d.hs_m;
-  m.col_stride = 1;
-  m.head_stride = (int64_t)d.hs_m * d.hs_m;
-  m.slot_stride = le[XS_L_C];
+  MatScanDesc m = mat_state_desc(e, kXLSTM, l);
   m.slot_ids = r.slot_ids;
   m.run_off = r.run_off;
   m.n_runs = r.n_runs;
@@ -650,6 +689,7 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   m.row_parts = row_parts(r, d.hs_m);
   m.out_part_stride = (int64_t)n * I;
   HK_TRY(timed_mat_scan(e, 0, m, s));
+  HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(mlstm_post(w.NUM, m.row_parts, m.out_part_stride, w.DEN, d.nh, F32(e, kXLSTM, l, X_L_GN_W), F32(e, kXLSTM, l, X_L_GN_B),
                     F32(e, kXLSTM, l, X_L_SKIP), w.XMC, w.XMG + I, 2 * I, n, I, d.nh, w.HS.f,
                     w.HS.l, s));
@@ -677,16 +717,7 @@ int run_mamba2(Engine& e, int l, const Runs& r, hipStream_t s) {
   HK_TRY(mamba2_dt(w.DTR, F32(e, kMamba2, l, M_A), n, d.nhm, w.DTS, w.DEC, s));
   HK_TRY(conv_scan(r, w.PROJ, W, C, st[MS_CONV], le[MS_CONV], F32(e, kMamba2, l, M_CONV_W),
                    F32(e, kMamba2, l, M_CONV_B), 1, w.MXC, C, s));
-  // SSM state stored [head][c][h]: tile rows are the contracted bc axis.
-  MatScanDesc m;
-  m.state = st[MS_SSM];
-  m.rows = d.bc;
-  m.cols = d.hm;
-  m.heads = d.nhm;
-  m.row_stride = d.hm;
-  m.col_stride = 1;
-  m.head_stride = (int64_t)d.bc * d.hm;
-  m.slot_stride = le[MS_SSM];
+  MatScanDesc m = mat_state_desc(e, kMamba2, l);
   m.slot_ids = r.slot_ids;
   m.run_off = r.run_off;
   m.n_runs = r.n_runs;
@@ -702,6 +733,7 @@ int run_mamba2(Engine& e, int l, const Runs& r, hipStream_t s) {
   // tower's stream is not the one that ends the tick)
   m.out_part_stride = (int64_t)n * I;
   HK_TRY(timed_mat_scan(e, 1, m, s));
+  HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(mamba2_post(w.YS, m.row_parts, m.out_part_stride, w.MXC, C, w.PROJ + C, W, F32(e, kMamba2, l, M_D),
                      F32(e, kMamba2, l, M_NORM), n, I, d.hm, w.YN.f, w.YN.l, s));
   HK_TRY(linear(e, w, w.YN, I, {S(e, kMamba2, l, M_OUT_W), nullptr}, n, H, I, 0, w.X.f, H, w.X.f,
@@ -723,15 +755,7 @@ int run_retnet(Engine& e, int l, const Runs& r, hipStream_t s) {
   HK_TRY(retnet_prep(r, w.QKVG, 4 * H, H, d.nh, scaling, F32(e, kRetNet, l, R_ANGLE),
                      F32(e, kRetNet, l, R_DECAY), reinterpret_cast<int*>(st[RS_OFF]),
                      st[RS_SCALE], w.KR, w.QS, s));
-  MatScanDesc m;
-  m.state = st[RS_S];
-  m.rows = d.hs_r;
-  m.cols = d.hs_r;
-  m.heads = d.nh;
-  m.row_stride = d.hs_r;
-  m.col_stride = 1;
-  m.head_stride = (int64_t)d.hs_r * d.hs_r;
-  m.slot_stride = le[RS_S];
+  MatScanDesc m = mat_state_desc(e, kRetNet, l);
   m.slot_ids = r.slot_ids;
   m.run_off = r.run_off;
   m.n_runs = r.n_runs;
@@ -745,6 +769,7 @@ int run_retnet(Engine& e, int l, const Runs& r, hipStream_t s) {
   m.row_parts = row_parts(r, d.hs_r);
   m.out_part_stride = (int64_t)n * H;
   HK_TRY(timed_mat_scan(e, 2, m, s));
+  HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(retnet_post(w.O, m.row_parts, m.out_part_stride, w.QKVG + 3 * H, 4 * H, n, H, d.hs_r,
                      w.YO.f, w.YO.l, s));
   HK_TRY(linear(e, w, w.YO, H, {S(e, kRetNet, l, R_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f,
@@ -996,6 +1021,26 @@ int hk_engine_create(const int* cfg, int n_cfg, void** out) {
       }
     }
   }
+  // write-back logs of the matrix states, empty
+  e->mlog.assign(hk::kTowers, std::vector<Engine::MatLog>(d.D));
+  for (int t = 0; t < hk::kTowers; ++t) {
+    if (hk::matrix_leaf(t) < 0) continue;
+    for (int l = 0; l < d.D; ++l) {
+      hk::MatScanDesc m = hk::mat_state_desc(*e, t, l);  // layout (no log yet)
+      const int64_t per_head = (int64_t)e->capacity * m.heads;
+      Engine::MatLog& lg = e->mlog[t][l];
+      lg.hdr = e->alloc_f(per_head * hk::kLogHdr);
+      lg.b = e->alloc_f(per_head * hk::kLogCap * m.rows);
+      lg.g = e->alloc_f(per_head * hk::kLogCap * m.cols);
+      if (!lg.hdr || !lg.b || !lg.g) {
+        hk::set_error("hk_engine_create: out of device memory for the write-back logs");
+        return HK_ERR_HIP;
+      }
+      m = hk::mat_state_desc(*e, t, l);
+      HK_TRY(hk::mat_log_clear(m, nullptr, 0, e->capacity, nullptr));
+    }
+  }
+  HK_CHECK_HIP(hipDeviceSynchronize());
   int st = hk::build_workspace(*e);
   if (st != HK_OK) {
     hk::set_error("hk_engine_create: out of device memory for the workspace (%d rows)",
@@ -1080,10 +1125,17 @@ int hk_engine_state_copy(void* h, int tower, int layer, int leaf, int slot0, int
   const int64_t per = e.leaf_elems[tower][leaf];
   float* base = e.state[tower][layer][leaf] + (int64_t)slot0 * per;
   const size_t bytes = (size_t)nslots * per * 4;
-  if (to_engine)
-    HK_CHECK_HIP(hipMemcpyAsync(base, buf, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
-  else
-    HK_CHECK_HIP(hipMemcpyAsync(buf, base, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  hipStream_t s = (hipStream_t)stream;
+  // A matrix-state leaf with pending write-back updates is materialised
+  // before it is read, and its log emptied once it is overwritten.
+  const bool logged = leaf == hk::matrix_leaf(tower) && nslots > 0;
+  if (to_engine) {
+    HK_CHECK_HIP(hipMemcpyAsync(base, buf, bytes, hipMemcpyDeviceToDevice, s));
+    if (logged) HK_TRY(hk::mat_log_clear(hk::mat_state_desc(e, tower, layer), nullptr, slot0, nslots, s));
+  } else {
+    if (logged) HK_TRY(hk::mat_log_flush(hk::mat_state_desc(e, tower, layer), slot0, nslots, s));
+    HK_CHECK_HIP(hipMemcpyAsync(buf, base, bytes, hipMemcpyDeviceToDevice, s));
+  }
   return HK_OK;
 }
 
@@ -1099,13 +1151,16 @@ int hk_engine_reset_slots(void* h, const int* slots_host, int n, void* stream) {
         const float v = (t == hk::kXLSTM && leaf == hk::XS_S_M) ? -INFINITY : 0.0f;
         const int64_t per = e.leaf_elems[t][leaf];
         float* base = e.state[t][l][leaf];
+        const bool logged = (int)leaf == hk::matrix_leaf(t);
         if (n < 0) {
           HK_TRY(hk::fill_f32(base, per * e.capacity, v, s));
+          if (logged) HK_TRY(hk::mat_log_clear(hk::mat_state_desc(e, t, l), nullptr, 0, e.capacity, s));
         } else {
           for (int i = 0; i < n; ++i) {
             const int slot = slots_host[i];
             HK_REQUIRE(slot >= 0 && slot < e.capacity, "reset: slot %d out of range", slot);
             HK_TRY(hk::fill_f32(base + (int64_t)slot * per, per, v, s));
+            if (logged) HK_TRY(hk::mat_log_clear(hk::mat_state_desc(e, t, l), nullptr, slot, 1, s));
           }
         }
       }

@@ -46,8 +46,33 @@ struct MatScanDesc {
   // is split; a long run then has row_parts times the parallelism per step.
   int row_parts = 1;
   int64_t out_part_stride = 0;
+  // Deferred write-back (log_cap > 0). A slot's tile is
+  //   S = F * B + sum_{j < n} a_j b_j g_j^T
+  // with B the tile at `state` and n <= log_cap pending rank-1 updates
+  // (b_j: scale * beta of a past step, g_j: its gamma, a_j: the product of
+  // the alphas applied since). A run of len steps with n + len <= log_cap
+  // leaves B untouched and appends its steps to the log; any other run
+  // writes the materialised tile back and empties the log. The scan only
+  // reads the log header; launch_mat_log_commit (after the scan, on the same
+  // stream) updates it. State reads stay one tile per run, state writes
+  // drop to one tile per log_cap steps of short runs.
+  float* log_hdr = nullptr;  // [slot][head][kLogHdr]: n, F, a_0 .. a_{cap-1}
+  float* log_b = nullptr;    // [slot][head][cap][rows]
+  float* log_g = nullptr;    // [slot][head][cap][cols]
+  int log_cap = 0;
 };
 
+constexpr int kLogHdr = 16;  // floats per (slot, head) log header
+constexpr int kLogCapMax = 8;
+
 int launch_mat_scan(const MatScanDesc& d, hipStream_t stream);
+// The log header update of a scan launch (deferred write-back); run after it.
+int launch_mat_log_commit(const MatScanDesc& d, hipStream_t stream);
+// Materialises slots [slot0, slot0 + n) into B and empties their logs.
+int mat_log_flush(const MatScanDesc& d, int slot0, int n, hipStream_t stream);
+// Empties the logs of n slots after their B was set directly: slots_dev[i]
+// (a device list) or, with slots_dev null, slot0 + i.
+int mat_log_clear(const MatScanDesc& d, const int* slots_dev, int slot0, int n,
+                  hipStream_t stream);
 
 }  // namespace hk

@@ -110,6 +110,50 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
     }
   }
 
+  // ---- deferred write-back: materialise the tile from B and the log
+  // (s = F s, then s = fma(b_j, a_j g_j, s) in entry order, as mat_log_flush
+// does)
+  int log_n = 0;
+  bool defer = false;
+  if (d.log_cap > 0) {
+    const float* lh = d.log_hdr + ((int64_t)slot * d.heads + head) * kLogHdr;
+    log_n = (int)lh[0];
+    defer = log_n + len <= d.log_cap;
+    if (log_n > 0) {
+      const float F = lh[1];
+      const int64_t le = ((int64_t)slot * d.heads + head) * d.log_cap;
+      const float* lb = d.log_b + le * d.rows + row_off;
+      const float* lg = d.log_g + le * d.cols + col0;
+      for (int i = tid; i < log_n * prows; i += NT) {
+        const int j = i / prows;
+        sb[j][i - j * prows] = lb[(int64_t)j * d.rows + (i - j * prows)];
+      }
+      for (int i = tid; i < log_n * CW; i += NT) {
+        const int j = i / CW;
+        const int c = i - j * CW;
+        sg[j][c] = col0 + c < d.cols ? lg[(int64_t)j * d.cols + c] : 0.0f;
+      }
+      lds_barrier();
+      for (int j = 0; j < log_n; ++j) {
+        const float a = lh[2 + j];
+        const float f = j == 0 ? F : 1.0f;
+        float gj[VW];
+#pragma unroll
+        for (int v = 0; v < VW; ++v) gj[v] = a * sg[j][lane * VW + v];
+#pragma unroll
+        for (int i = 0; i < RPW; i += 4) {
+          const float4 bv = *reinterpret_cast<const float4*>(&sb[j][rbase + i]);
+          const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int v = 0; v < VW; ++v) s[i + k][v] = fmaf(bb[k], gj[v], f * s[i + k][v]);
+        }
+      }
+      lds_barrier();  // the step staging below rewrites sb / sg
+    }
+  }
+
   const float* beta_h = d.beta.ptr + (int64_t)head * d.beta.head_stride + row_off;
   const float* w_h = d.w.ptr + (int64_t)head * d.w.head_stride + row_off;
   for (int t0 = 0; t0 < len; t0 += kSteps) {
@@ -214,6 +258,29 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
     lds_barrier();  // the next block's staging overwrites sb/sw/sg/sa
   }
 
+  if (defer) {
+    // B stays; the run's steps (len <= log_cap <= kSteps: all in the one
+    // staging block, still in LDS) become log entries log_n .. log_n+len-1.
+    // Column tile 0 writes each part's rows of b; part 0 each tile's g.
+    const int64_t le = ((int64_t)slot * d.heads + head) * d.log_cap + log_n;
+    if (blockIdx.x == 0) {
+      float* lb = d.log_b + le * d.rows + row_off;
+      for (int i = tid; i < len * prows; i += NT) {
+        const int t = i / prows;
+        lb[(int64_t)t * d.rows + (i - t * prows)] = sb[t][i - t * prows];
+      }
+    }
+    if (part == 0) {
+      float* lg = d.log_g + le * d.cols + col0;
+      for (int i = tid; i < len * CW; i += NT) {
+        const int t = i / CW;
+        const int c = i - t * CW;
+        if (col0 + c < d.cols) lg[(int64_t)t * d.cols + c] = sg[t][c];
+      }
+    }
+    return;
+  }
+
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const uint32_t o = off0 + (uint32_t)i * rstride;
@@ -228,7 +295,106 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
   }
 }
 
+// Log header update after a scan launch, one thread per (run, head): a run
+// that was deferred (n + len <= cap) appends len entries, entry t weighted
+// by the product of the run's later alphas, and scales the older entries
+// and F by the product of all of them; any other run left B materialised,
+// so its log empties (n = 0, F = 1).
+__global__ void mat_log_commit_kernel(MatScanDesc d) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= d.n_runs * d.heads) return;
+  const int run = i / d.heads;
+  const int head = i - run * d.heads;
+  const int slot = d.slot_ids[run];
+  const int r0 = d.run_off[run];
+  const int len = d.run_off[run + 1] - r0;
+  float* h = d.log_hdr + ((int64_t)slot * d.heads + head) * kLogHdr;
+  const int n = (int)h[0];
+  if (n + len <= d.log_cap) {
+    float p = 1.0f;  // product of the alphas after step t
+    for (int t = len - 1; t >= 0; --t) {
+      h[2 + n + t] = p;
+      p *= d.alpha.ptr[(int64_t)(r0 + t) * d.alpha.row_stride + (int64_t)head * d.alpha.head_stride];
+    }
+    for (int j = 0; j < n; ++j) h[2 + j] *= p;
+    h[1] *= p;
+    h[0] = (float)(n + len);
+  } else {
+    h[0] = 0.0f;
+    h[1] = 1.0f;
+  }
+}
+
+// B <- F B + sum_j b_j (a_j g_j) for slots slot0 + blockIdx.z, one row per
+// work-group (the same operation order as the scan's materialisation).
+__global__ void mat_log_flush_kernel(MatScanDesc d, int slot0) {
+  const int row = blockIdx.x;
+  const int head = blockIdx.y;
+  const int slot = slot0 + blockIdx.z;
+  const float* lh = d.log_hdr + ((int64_t)slot * d.heads + head) * kLogHdr;
+  const int n = (int)lh[0];
+  if (n == 0) return;
+  const float F = lh[1];
+  const int64_t le = ((int64_t)slot * d.heads + head) * d.log_cap;
+  float* b = d.state + (int64_t)slot * d.slot_stride + (int64_t)head * d.head_stride +
+             (int64_t)row * d.row_stride;
+  for (int c = threadIdx.x; c < d.cols; c += blockDim.x) {
+    float v = b[(int64_t)c * d.col_stride] * F;
+    for (int j = 0; j < n; ++j) {
+      const float gj = lh[2 + j] * d.log_g[(le + j) * d.cols + c];
+      v = fmaf(d.log_b[(le + j) * d.rows + row], gj, v);
+    }
+    b[(int64_t)c * d.col_stride] = v;
+  }
+}
+
+// Empties the logs of slots slots[i] (or slot0 + i when slots is null).
+__global__ void mat_log_clear_kernel(float* hdr, int heads, const int* slots, int slot0, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * heads) return;
+  const int k = i / heads;
+  const int slot = slots ? slots[k] : slot0 + k;
+  float* h = hdr + ((int64_t)slot * heads + (i - k * heads)) * kLogHdr;
+  h[0] = 0.0f;
+  h[1] = 1.0f;
+}
+
 }  // namespace
+
+int launch_mat_log_commit(const MatScanDesc& d, hipStream_t stream) {
+  if (d.log_cap == 0 || d.n_runs == 0) return HK_OK;
+  HK_REQUIRE(!d.per_row && d.slot_ids && d.run_off && d.log_hdr, "mat_log_commit: need runs");
+  const int total = d.n_runs * d.heads;
+  hipLaunchKernelGGL(mat_log_commit_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, d);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int mat_log_flush(const MatScanDesc& d, int slot0, int n, hipStream_t stream) {
+  if (d.log_cap == 0 || n == 0) return HK_OK;
+  HK_REQUIRE(d.state && d.log_hdr && d.log_b && d.log_g && n > 0 && n <= 65535 &&
+                 d.heads <= 65535,
+             "mat_log_flush: bad arguments");
+  hipLaunchKernelGGL(mat_log_flush_kernel, dim3(d.rows, d.heads, n), dim3(256), 0, stream, d,
+                     slot0);
+  HK_LAUNCH_CHECK();
+  const int total = n * d.heads;
+  hipLaunchKernelGGL(mat_log_clear_kernel, dim3((total + 255) / 256), dim3(256), 0, stream,
+                     d.log_hdr, d.heads, nullptr, slot0, n);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int mat_log_clear(const MatScanDesc& d, const int* slots_dev, int slot0, int n,
+                  hipStream_t stream) {
+  if (d.log_cap == 0 || n == 0) return HK_OK;
+  HK_REQUIRE(n > 0 && d.log_hdr, "mat_log_clear: bad arguments");
+  const int total = n * d.heads;
+  hipLaunchKernelGGL(mat_log_clear_kernel, dim3((total + 255) / 256), dim3(256), 0, stream,
+                     d.log_hdr, d.heads, slots_dev, slot0, n);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
 
 int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
   HK_REQUIRE(d.state && d.out && d.alpha.ptr && d.beta.ptr && d.gamma.ptr && d.w.ptr,
@@ -240,6 +406,9 @@ int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
              "mat_scan: %d rows do not split into %d parts of a multiple of 4", d.rows,
              d.row_parts);
   HK_REQUIRE((int64_t)d.heads * d.row_parts <= 65535, "mat_scan: too many heads");
+  HK_REQUIRE(d.log_cap == 0 || (d.log_cap <= kLogCapMax && d.log_cap <= kLogHdr - 2 &&
+                                !d.per_row && d.log_hdr && d.log_b && d.log_g),
+             "mat_scan: bad write-back log");
   const int prows = d.rows / d.row_parts;
   HK_REQUIRE((int64_t)d.rows * d.row_stride + (int64_t)d.cols * d.col_stride < (1LL << 32),
              "mat_scan: tile too large for 32-bit offsets");
