@@ -48,6 +48,32 @@ def zipf_ticks(n_ticks: int, n_symbols: int, batch: int, s: float, seed: int):
     return ticks
 
 
+LOG_CAP = 8  # pending rank-1 updates a matrix-state tile may carry (engine kLogCap)
+
+
+def matrix_scan_bytes(ticks, first, depth, tile_bytes, entry_bytes, row_bytes):
+    """Algorithmic bytes of one matrix-state scan (all its layers) over ticks
+    first.. of `ticks`. Each run reads its symbol's tile once; a run that fits
+    the slot's pending-update log (n + len <= LOG_CAP) appends len entries
+    instead of writing the tile, any other run writes the tile and empties the
+    log; the n pending entries are read either way. The log evolves the same
+    way in every layer (it depends only on the slot's run lengths), so the
+    replay is exact. Plus row_bytes per request row."""
+    n_log = {}
+    total = 0.0
+    for i, (syms, counts) in enumerate(ticks):
+        for s, c in zip(syms.tolist(), counts.tolist()):
+            n = n_log.get(s, 0)
+            defer = n + c <= LOG_CAP
+            if i >= first:
+                total += tile_bytes + n * entry_bytes
+                total += c * entry_bytes if defer else tile_bytes
+            n_log[s] = n + c if defer else 0
+        if i >= first:
+            total += int(counts.sum()) * row_bytes
+    return depth * total
+
+
 COUNTERS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         "mat_scan_mlstm_1024sym_hbm_counters.txt")
 
@@ -198,19 +224,21 @@ def main() -> int:
     total_s = t1 - t0
     reqs = K * args.batch
 
-    # Algorithmic bytes of the mLSTM scan per launch (one per block per tick):
-    # the state of every distinct symbol read and written once, plus per row
-    # q, k/sqrt(d), v and the output (4 x inner fp32) and the two gates.
+    # Algorithmic bytes of the matrix scans over the timed ticks (one launch
+    # per block and run group per tick for the mLSTM): state tiles, pending
+    # log entries (a row and a column vector per head) and per request row the
+    # step vectors and the output (mLSTM: q, k/sqrt(d), v, output = 4 x inner
+    # fp32, and the two gates).
     nh, hs, inner = cfg.num_heads, cfg.mlstm_head, cfg.inner
     bc, hm, nhm, hr = cfg.mamba_bc_size, cfg.mamba_head_size, cfg.mamba_heads, cfg.retnet_head
     H = cfg.hidden_size
-    mbytes = sbytes = rbytes = 0.0
-    for j in range(K):
-        r = packed[W + j]
-        D, n = len(r.slot_ids), r.n_rows
-        mbytes += cfg.tower_depth * (2.0 * D * nh * hs * hs * 4 + n * (4 * inner + 2 * nh) * 4)
-        sbytes += cfg.tower_depth * (2.0 * D * nhm * bc * hm * 4 + n * (2 * bc + inner + inner + 2 * nhm) * 4)
-        rbytes += cfg.tower_depth * (2.0 * D * nh * hr * hr * 4 + n * 4 * H * 4)
+    D_ = cfg.tower_depth
+    mbytes = matrix_scan_bytes(ticks, W, D_, nh * hs * hs * 4.0, nh * 2 * hs * 4.0,
+                               (4 * inner + 2 * nh) * 4.0)
+    sbytes = matrix_scan_bytes(ticks, W, D_, nhm * bc * hm * 4.0, nhm * (bc + hm) * 4.0,
+                               (2 * bc + inner + inner + 2 * nhm) * 4.0)
+    rbytes = matrix_scan_bytes(ticks, W, D_, nh * hr * hr * 4.0, nh * 2 * hr * 4.0,
+                               4 * H * 4.0)
     per_launch_bytes = mbytes / max(n_launch, 1)
     achieved = mbytes / (scan_ms / 1000.0) / 1e9 if scan_ms > 0 else 0.0
     kernels = {"mlstm_scan": {"launches": n_launch, "avg_us": 1000.0 * scan_ms / max(n_launch, 1),
