@@ -9,6 +9,7 @@
 namespace hk {
 namespace {
 
+constexpr int kConvChunk = 16;
 // grid (runs, ceil(C/256)); thread per channel.
 __global__ __launch_bounds__(256) void conv_scan_kernel(
     const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ in,
@@ -21,22 +22,40 @@ __global__ __launch_bounds__(256) void conv_scan_kernel(
   const int slot = slot_ids[run];
   const int r0 = run_off[run];
   const int r1 = run_off[run + 1];
+  if (r1 <= r0) return;
   float* st = state + (int64_t)slot * slot_stride;
   float s0 = st[c], s1 = st[channels + c], s2 = st[2 * channels + c];
   const float w0 = w[c], w1 = w[channels + c], w2 = w[2 * channels + c], w3 = w[3 * channels + c];
   const float b = bias[c];
-  // unrolled so that several rows' loads are in flight together
-#pragma unroll 8
-  for (int r = r0; r < r1; ++r) {
-    const float x = in[(int64_t)r * ld_in + c];
-    float v = b + w0 * s0;
-    v += w1 * s1;
-    v += w2 * s2;
-    v += w3 * x;
-    out[(int64_t)r * ldo + c] = act_silu ? silu(v) : v;
-    s0 = s1;
-    s1 = s2;
-    s2 = x;
+  // The run's inputs stream through two register buffers of kConvChunk
+  // rows: the next chunk's loads are in flight while this one is computed
+  // (rows past the run read its last row, unused).
+  float xa[kConvChunk], xb[kConvChunk];
+  auto load = [&](float (&x)[kConvChunk], int rb) {
+#pragma unroll
+    for (int k = 0; k < kConvChunk; ++k) x[k] = in[(int64_t)min(rb + k, r1 - 1) * ld_in + c];
+  };
+  auto step = [&](const float (&x)[kConvChunk], int rb) {
+#pragma unroll
+    for (int k = 0; k < kConvChunk; ++k) {
+      if (rb + k < r1) {
+        float v = b + w0 * s0;
+        v += w1 * s1;
+        v += w2 * s2;
+        v += w3 * x[k];
+        out[(int64_t)(rb + k) * ldo + c] = act_silu ? silu(v) : v;
+        s0 = s1;
+        s1 = s2;
+        s2 = x[k];
+      }
+    }
+  };
+  load(xa, r0);
+  for (int rb = r0; rb < r1; rb += 2 * kConvChunk) {
+    load(xb, rb + kConvChunk);
+    step(xa, rb);
+    load(xa, rb + 2 * kConvChunk);
+    step(xb, rb + kConvChunk);
   }
   st[c] = s0;
   st[channels + c] = s1;
