@@ -144,9 +144,288 @@ def cpu_baseline(params, cfg, symbols, counts, feats, budget_s: float):
     }
 
 
+def _stream_handle(torch, dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def bench_cell_step(args) -> int:
+    """C2 (Mamba2 step, B=256, 8 heads x headdim 64, d_state 64, 128 steps from
+    a zero state) or C3 (mLSTM step, B=1024, 4 heads x 64 x 64, 256 steps from
+    zero): the kernel API's C entry point (hk_mamba2_step / hk_mlstm_step)
+    called back to back on device-resident per-step inputs, timed with HIP
+    events on the stream; plus one point with a state past the 256 MB
+    Infinity Cache (B=2048 / B=4096). Inputs follow the configs' generators
+    (seed 0): C2 x ~ N(0,1), b, c ~ N(0,1/64), dt = softplus(N(0,1)),
+    decay = exp(A dt) with A = -exp(U(0, ln 16)); C3 q, k, v ~ N(0,1/64),
+    gate pre-activations N(0,1) through the stabilised exp / sigmoid gates."""
+    import torch
+
+    from hackathon_amd import _lib
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    c2 = args.workload == "c2"
+    lib = _lib.lib()
+
+    def run(B, steps):
+        if c2:
+            heads, sh, sc = 8, 64, 64
+            state = torch.zeros(B, heads, sh, sc, device=dev)
+            x = torch.randn(steps, B, heads, sh, device=dev, generator=g)
+            b = torch.randn(steps, B, sc, device=dev, generator=g) / 8
+            c = torch.randn(steps, B, sc, device=dev, generator=g) / 8
+            dt = torch.nn.functional.softplus(torch.randn(steps, B, heads, device=dev, generator=g))
+            A = -torch.exp(torch.rand(heads, device=dev, generator=g) * float(np.log(16.0)))
+            decay = torch.exp(A * dt)
+            out = torch.empty(steps, B, heads, sh, device=dev)
+            ins = (x, b, c, dt, decay)
+            fn = lib.hk_mamba2_step
+            # state r+w, x, b, c, dt, decay, y
+            step_bytes = 4.0 * (2 * B * heads * sh * sc + B * heads * sh + 2 * B * sc +
+                                2 * B * heads + B * heads * sh)
+            flops = 5.0 * B * heads * sh * sc
+        else:
+            heads, sh, sk = 4, 64, 64
+            state = torch.zeros(B, heads, sh, sk, device=dev)
+            q = torch.randn(steps, B, heads, sh, device=dev, generator=g) / 8
+            k = torch.randn(steps, B, heads, sh, device=dev, generator=g) / 8
+            v = torch.randn(steps, B, heads, sk, device=dev, generator=g) / 8
+            ip = torch.randn(steps, B, heads, device=dev, generator=g)
+            fp = torch.randn(steps, B, heads, device=dev, generator=g)
+            ig = torch.empty_like(ip)
+            fg = torch.empty_like(fp)
+            m = torch.zeros(B, heads, device=dev)
+            for t in range(steps):  # the reference's stabilised gates (model/xlstm.py:61-65)
+                lf = torch.nn.functional.logsigmoid(fp[t])
+                mn = torch.maximum(ip[t], m + lf)
+                ig[t] = torch.exp(ip[t] - mn)
+                fg[t] = torch.exp(lf + m - mn)
+                m = mn
+            out = torch.empty(steps, B, heads, sk, device=dev)
+            ins = (q, k, v, ig, fg)
+            fn = lib.hk_mlstm_step
+            # cell r+w, q, k, v, i, f, out
+            step_bytes = 4.0 * (2 * B * heads * sh * sk + 2 * B * heads * sh + B * heads * sk +
+                                2 * B * heads + B * heads * sk)
+            flops = 4.0 * B * heads * sh * sk
+        dims = (B, heads, state.shape[2], state.shape[3])
+        stream = _stream_handle(torch, dev)
+        calls = [tuple(t[i].data_ptr() for t in ins) for i in range(steps)]
+        outs = [out[i].data_ptr() for i in range(steps)]
+
+        def go(n):
+            for i in range(n):
+                st = fn(state.data_ptr(), *calls[i], None, outs[i], *dims, stream)
+                if st != 0:
+                    raise RuntimeError(_lib.lib().hk_last_error().decode())
+
+        go(min(8, steps))  # warm-up on the same inputs, then restart from zero
+        state.zero_()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        go(steps)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / steps
+        assert torch.isfinite(out).all() and torch.isfinite(state).all()
+        return {"batch": B, "us_per_step": us, "algorithmic_bytes_per_step": step_bytes,
+                "achieved_GBs": step_bytes / us / 1e3, "flops_per_step": flops,
+                "state_MB": 4.0 * state.numel() / 1e6}
+
+    steps = 128 if c2 else 256
+    main_b = 256 if c2 else 1024
+    big_b = 2048 if c2 else 4096
+    pts = [run(main_b, steps), run(big_b, steps)]
+    head = pts[0]
+    name = ("C2 Mamba2 step (8 heads x 64 x d_state 64)" if c2 else
+            "C3 mLSTM cell step (4 heads x 64 x 64)")
+    line = {
+        "metric": f"{name}: us per step at B={main_b}",
+        "value": head["us_per_step"],
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 8,
+        "higher_is_better": False,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": name, "batch": main_b,
+                   "entry_point": "hk_mamba2_step" if c2 else "hk_mlstm_step"},
+        "roofline": {
+            "kernel": "mat_scan_kernel (per-row mode, the kernel API)",
+            "bound": "hbm",
+            "achieved": head["achieved_GBs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": head["achieved_GBs"] / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_step": head["algorithmic_bytes_per_step"],
+            "note": (f"state {head['state_MB']:.1f} MB fits the 256 MB Infinity Cache; "
+                     f"the B={big_b} point ({pts[1]['state_MB']:.0f} MB) does not"),
+        },
+        "points": pts,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_c5(args) -> int:
+    """C5 (stress) at reduced width, 8192 resident symbols: H=512, P=1024,
+    depth 12, 8 heads (14.8 MB of state per symbol; default dims need 153.5
+    MB and 8192 of them do not fit 288 GB). Per tick B ~ U{1..512} requests
+    with symbol ids ~ U{0..8191} (seed 3), features N(0,1) (seed 1), bf16
+    CastLinear weights, fp32 state, init-spec weights (seed 0)."""
+    import torch
+
+    from hackathon_amd import spec, weights
+    from hackathon_amd.engine import Engine, pack_runs
+
+    dev = torch.device("cuda:0")
+    cfg = spec.ModelConfig(hidden_size=512, proj_size=1024, tower_depth=12, num_heads=8,
+                           num_features=79)
+    S, BMAX = 8192, 512
+    K, W = args.steps, args.warmup
+    params = weights.generate(cfg, 0)
+    eng = Engine(cfg, capacity=S, max_rows=BMAX, max_runs=BMAX, linear_dtype="bf16", device=dev)
+    eng.load_weights(params)
+    rng = np.random.default_rng(3)
+    frng = np.random.default_rng(1)
+    packed, feats = [], []
+    for _ in range(W + K):
+        B = int(rng.integers(1, BMAX + 1))
+        ids = rng.integers(0, S, size=B)
+        uniq, first, counts = np.unique(ids, return_index=True, return_counts=True)
+        order = np.argsort(first, kind="stable")
+        runs, _ = pack_runs(uniq[order].astype(np.int32), counts[order].astype(np.int64))
+        packed.append(runs)
+        feats.append(torch.from_numpy(frng.standard_normal((B, cfg.num_features),
+                                                           dtype=np.float32)).to(dev))
+    preds = torch.empty(BMAX, 4, dtype=torch.float32, device=dev)
+    for i in range(W):
+        eng.tick(packed[i], feats[i], preds[: packed[i].n_rows])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(K)]
+    t0 = time.perf_counter()
+    for j in range(K):
+        r = packed[W + j]
+        ev[j][0].record(stream)
+        eng.tick(r, feats[W + j], preds[: r.n_rows])
+        ev[j][1].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    eng.check()
+    assert torch.isfinite(preds).all()
+    lat = np.array([a.elapsed_time(b) * 1000.0 for a, b in ev])
+    reqs = sum(packed[W + j].n_rows for j in range(K))
+    line = {
+        "metric": "C5 stress: requests/sec at 8192 symbols, B~U(1..512); p50/p99 tick latency (us)",
+        "value": reqs / (t1 - t0),
+        "unit": "requests/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": 1000.0 * (t1 - t0) / K,
+        "higher_is_better": True,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "C5 stress, reduced width (H=512, P=1024, depth 12, 8 heads, "
+                               "14.8 MB of state per symbol)",
+                   "symbols": S, "batch": "U(1..512)"},
+        "p50_us": float(np.percentile(lat, 50)),
+        "p99_us": float(np.percentile(lat, 99)),
+        "mean_requests_per_tick": reqs / K,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_c1(args) -> int:
+    """C1 at default dims in fp32 (the reference's CPU-runnable case): 4
+    symbols x 256 single-request steps, every symbol active each step. GPU
+    engine (fp32 weights) timed per step with HIP events; the oracle (the
+    reference algorithm on the host's cores) runs the first steps in the same
+    process within --cpu-budget seconds, and its predictions are compared
+    with the GPU's on those steps."""
+    import torch
+
+    from hackathon_amd import spec, weights
+    from hackathon_amd.engine import Engine
+
+    dev = torch.device("cuda:0")
+    cfg = spec.DEFAULT
+    B, steps = 4, 256
+    params = weights.generate(cfg, 0)
+    eng = Engine(cfg, capacity=B, max_rows=16, linear_dtype="fp32", device=dev)
+    eng.load_weights(params)
+    rng = np.random.default_rng(1)
+    x_host = np.clip(rng.standard_normal((steps, B, cfg.num_features), dtype=np.float32), -5, 5)
+    x = torch.from_numpy(x_host).to(dev)
+    preds = []
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for t in range(steps):
+        preds.append(eng.forward_masked(x[t], None))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gpu_ms = e0.elapsed_time(e1) / steps
+    gpu = torch.stack(preds).cpu().double()
+    eng.close()
+    del eng
+    torch.cuda.empty_cache()
+
+    from oracle import model as om  # the CPU baseline and parity check only
+
+    threads = max(1, min(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+                         os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    P = om.Params(params)
+    st = om.init_state(cfg, B)
+    worst = 0.0
+    done = 0
+    t0 = time.perf_counter()
+    with torch.inference_mode():
+        for t in range(steps):
+            o, st = om.forward(P, cfg, torch.from_numpy(x_host[t]), st)
+            d = (gpu[t] - o.double()).abs() / (o.double().abs() + 2.0)
+            worst = max(worst, float(d.max()))
+            done += 1
+            if time.perf_counter() - t0 > args.cpu_budget:
+                break
+    cpu_ms = 1000.0 * (time.perf_counter() - t0) / done
+    line = {
+        "metric": "C1 default dims fp32: ms per step, 4 symbols x 256 single-request steps",
+        "value": gpu_ms,
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 0,
+        "higher_is_better": False,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "C1: default dims, fp32 weights and state, 4 symbols",
+                   "batch": B},
+        "cpu_baseline": {"value": cpu_ms, "unit": "ms per step", "cores": threads,
+                         "kind": "port",
+                         "sample": f"steps 0..{done - 1} of the same inputs, fp32 oracle"},
+        "parity": {"steps_compared": done,
+                   "max_abs_diff_over_abs_plus_2": worst,
+                   "note": "|gpu - oracle| / (|oracle| + 2) over the 4 predictions per row"},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", choices=("c4", "c1", "c2", "c3", "c5"), default="c4",
+                    help="c4 (default): the headline ensemble tick; c1, c2, c3, c5: the other "
+                         "configurations (one JSON line each)")
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--symbols", type=int, default=1024)
@@ -163,6 +442,13 @@ def main() -> int:
               "traffic per tick, and this build runs on a single MI355X; use --gpus 1.",
               file=sys.stderr)
         return 2
+
+    if args.workload in ("c2", "c3"):
+        return bench_cell_step(args)
+    if args.workload == "c5":
+        return bench_c5(args)
+    if args.workload == "c1":
+        return bench_c1(args)
 
     import torch
 

@@ -21,6 +21,74 @@ void set_error(const char* fmt, ...) {
   g_last_error = buf;
 }
 
+namespace {
+
+// Mamba2 step in the reference's state layout [B][heads][h][c], where c (the
+// axis y contracts over) is contiguous: one work-group per (row, head), lane
+// = column c (CPL columns per lane, so a state row is one coalesced wave
+// access), each wave 16 rows h at a time; the 16 row sums over c come out
+// of one transposed butterfly (lane 4i holds row i). Idle rows: state
+// untouched, output zero.
+template <int CPL>
+__global__ __launch_bounds__(256) void mamba2_row_step_kernel(
+    float* __restrict__ ssm, const float* __restrict__ x, const float* __restrict__ b,
+    const float* __restrict__ c, const float* __restrict__ dt, const float* __restrict__ decay,
+    const uint8_t* __restrict__ mask, float* __restrict__ y, int heads, int size_h, int size_c) {
+  const int head = blockIdx.x;
+  const int row = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t rh = (int64_t)row * heads + head;
+  float* yo = y + rh * size_h;
+  if (mask != nullptr && mask[row] == 0) {
+    for (int h = threadIdx.x; h < size_h; h += blockDim.x) yo[h] = 0.0f;
+    return;
+  }
+  const float a = decay[rh];
+  const float sdt = dt[rh];
+  float coef[CPL], cw[CPL];
+  bool cok[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int ci = lane + 64 * j;
+    cok[j] = ci < size_c;
+    coef[j] = cok[j] ? sdt * b[(int64_t)row * size_c + ci] : 0.0f;  // (dt * b), then * x
+    cw[j] = cok[j] ? c[(int64_t)row * size_c + ci] : 0.0f;
+  }
+  float* st = ssm + rh * size_h * size_c;
+  const float* xr = x + rh * size_h;
+  for (int h0 = wave * 16; h0 < size_h; h0 += 64) {
+    float sv[16][CPL], xv[16], p[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const bool hok = h0 + i < size_h;
+      xv[i] = hok ? xr[h0 + i] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        sv[i][j] = (hok && cok[j]) ? st[(int64_t)(h0 + i) * size_c + lane + 64 * j] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        sv[i][j] = a * sv[i][j] + coef[j] * xv[i];
+        acc += cw[j] * sv[i][j];
+      }
+      p[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (h0 + i < size_h && cok[j]) st[(int64_t)(h0 + i) * size_c + lane + 64 * j] = sv[i][j];
+    const float sum = transposed_wave_sum<16>(p);
+    if ((lane & 3) == 0 && h0 + (lane >> 2) < size_h) yo[h0 + (lane >> 2)] = sum;
+  }
+}
+
+}  // namespace
+
 }  // namespace hk
 
 extern "C" {
@@ -90,8 +158,26 @@ int hk_mamba2_step(float* ssm, const float* x, const float* b, const float* c, c
                    int size_h, int size_c, void* stream) {
   HK_REQUIRE(batch >= 0 && heads > 0 && size_h > 0 && size_c > 0,
              "hk_mamba2_step: bad shape B=%d n=%d h=%d c=%d", batch, heads, size_h, size_c);
-  // The reference layout keeps c (the contracted axis) contiguous: tile rows
-  // are c with stride 1, tile columns are h with stride size_c.
+  if (batch == 0) return HK_OK;
+  if (size_c <= 256 && batch <= 65535 && heads <= 65535) {
+    const dim3 grid(heads, batch), block(256);
+    hipStream_t s = (hipStream_t)stream;
+#define HK_M2(C)                                                                              \
+  hipLaunchKernelGGL(hk::mamba2_row_step_kernel<C>, grid, block, 0, s, ssm, x, b, c, dt, decay, \
+                     mask, y, heads, size_h, size_c)
+    if (size_c <= 64) {
+      HK_M2(1);
+    } else if (size_c <= 128) {
+      HK_M2(2);
+    } else {
+      HK_M2(4);
+    }
+#undef HK_M2
+    HK_LAUNCH_CHECK();
+    return HK_OK;
+  }
+  // Wider states: the matrix scan with tile rows = c (stride 1) and tile
+  // columns = h (stride size_c).
   hk::MatScanDesc d;
   d.state = ssm;
   d.rows = size_c;
