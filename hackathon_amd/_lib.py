@@ -42,6 +42,11 @@ _SIGNATURES = {
     "hk_mlstm_step": (c_int, [c_void_p] * 8 + [c_int] * 4 + [c_void_p]),
     "hk_retnet_step": (c_int, [c_void_p] * 7 + [c_int] * 4 + [c_void_p]),
     "hk_mamba2_step": (c_int, [c_void_p] * 8 + [c_int] * 4 + [c_void_p]),
+    "hk_conv1d_step": (c_int, [c_void_p] * 6 + [c_int] * 3 + [c_void_p]),
+    "hk_block_linear": (c_int, [c_void_p] * 4 + [c_int] * 3 + [c_void_p]),
+    "hk_rglru_step": (c_int, [c_void_p] * 5 + [c_float] + [c_void_p] * 2 + [c_int] * 2
+                      + [c_void_p]),
+    "hk_slstm_step": (c_int, [c_void_p] * 9 + [c_int] * 2 + [c_void_p]),
 }
 
 _lib = None

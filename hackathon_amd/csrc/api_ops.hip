@@ -6,6 +6,7 @@
 #include <string>
 
 #include "common.h"
+#include "gemm.h"
 #include "scan_mat.h"
 
 namespace hk {
@@ -86,6 +87,112 @@ __global__ __launch_bounds__(256) void mamba2_row_step_kernel(
     if ((lane & 3) == 0 && h0 + (lane >> 2) < size_h) yo[h0 + (lane >> 2)] = sum;
   }
 }
+
+// Depthwise causal conv step in the reference's layout: state [B][C][K-1]
+// (oldest tap first), weight [C][K]. One thread per (row, channel); the
+// window is [state, x] and the taps are added in window order after the
+// bias, as the engine's run kernel does.
+constexpr int kConvMaxTaps = 8;
+
+__global__ __launch_bounds__(256) void conv1d_step_kernel(
+    float* __restrict__ state, const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ bias, const uint8_t* __restrict__ mask, float* __restrict__ out,
+    int64_t n, int channels, int taps) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t row = i / channels;
+  const int ch = (int)(i - row * channels);
+  if (mask != nullptr && mask[row] == 0) {
+    out[i] = 0.0f;
+    return;
+  }
+  float win[kConvMaxTaps];
+  float* st = state + i * (taps - 1);
+  for (int j = 0; j < taps - 1; ++j) win[j] = st[j];
+  win[taps - 1] = x[i];
+  const float* wr = w + (int64_t)ch * taps;
+  float v = (bias ? bias[ch] : 0.0f) + wr[0] * win[0];
+  for (int j = 1; j < taps; ++j) v += wr[j] * win[j];
+  out[i] = v;
+  for (int j = 0; j < taps - 1; ++j) st[j] = win[j + 1];
+}
+
+// RG-LRU elementwise step on the gate pre-activations: h' = h a^(c r) +
+// sqrt(1 - a^(2 c r)) (i x), i = sigmoid(gi), r = sigmoid(gr), the same
+// operations in the same order as the engine's run kernel.
+__global__ __launch_bounds__(256) void rglru_step_kernel(
+    float* __restrict__ h, const float* __restrict__ x, const float* __restrict__ gi,
+    const float* __restrict__ gr, const float* __restrict__ a, float c_exp,
+    const uint8_t* __restrict__ mask, float* __restrict__ out, int64_t n, int width) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t row = i / width;
+  const int ch = (int)(i - row * width);
+  if (mask != nullptr && mask[row] == 0) {
+    if (out) out[i] = 0.0f;
+    return;
+  }
+  const float it = sigmoid(gi[i]);
+  const float rt = sigmoid(gr[i]);
+  const float at = powf(a[ch], c_exp * rt);
+  const float mult = sqrtf(1.0f - at * at);
+  const float hn = (h[i] * at) + (mult * (it * x[i]));
+  h[i] = hn;
+  if (out) out[i] = hn;
+}
+
+// sLSTM cell step on the four gate pre-activations (stabilised exponential
+// gates; the same operations as the engine's round kernel).
+__global__ __launch_bounds__(256) void slstm_step_kernel(
+    float* __restrict__ c_state, float* __restrict__ n_state, float* __restrict__ m_state,
+    const float* __restrict__ ip, const float* __restrict__ fp, const float* __restrict__ zp,
+    const float* __restrict__ op, const uint8_t* __restrict__ mask, float* __restrict__ y,
+    int64_t n, int width) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  if (mask != nullptr && mask[i / width] == 0) {
+    y[i] = 0.0f;
+    return;
+  }
+  const float lfm = m_state[i] + logsigmoid(fp[i]);
+  const float mn = fmaxf(ip[i], lfm);
+  const float og = sigmoid(op[i]);
+  const float ig = expf(ip[i] - mn);
+  const float fg = expf(lfm - mn);
+  const float cn = fg * c_state[i] + ig * tanhf(zp[i]);
+  const float nn = fg * n_state[i] + ig;
+  c_state[i] = cn;
+  n_state[i] = nn;
+  m_state[i] = mn;
+  y[i] = og * cn / (nn + 1e-6f);
+}
+
+// BlockLinear with blocks too small or unaligned for the matrix-core GEMM:
+// one thread per output, the dot product over the block in input order.
+__global__ __launch_bounds__(256) void block_linear_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
+    float* __restrict__ out, int64_t n, int blocks, int bs) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int width = blocks * bs;
+  const int64_t row = i / width;
+  const int col = (int)(i - row * width);
+  const int blk = col / bs;
+  const float* xr = x + row * width + (int64_t)blk * bs;
+  const float* wr = w + (int64_t)col * bs;  // W[blk][o][:], col = blk*bs + o
+  float acc = 0.0f;
+  for (int h = 0; h < bs; ++h) acc = fmaf(xr[h], wr[h], acc);
+  out[i] = bias ? acc + bias[col] : acc;
+}
+
+int elementwise_grid(int64_t n, unsigned* blocks) {
+  const int64_t b = (n + 255) / 256;
+  HK_REQUIRE(b < (1LL << 31), "too many elements (%lld)", (long long)n);
+  *blocks = (unsigned)b;
+  return HK_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
@@ -199,6 +306,96 @@ int hk_mamba2_step(float* ssm, const float* x, const float* b, const float* c, c
   d.out_row_stride = (int64_t)heads * size_h;
   d.out_head_stride = size_h;
   return hk::launch_mat_scan(d, (hipStream_t)stream);
+}
+
+int hk_conv1d_step(float* state, const float* x, const float* weight, const float* bias,
+                   const uint8_t* mask, float* out, int batch, int channels, int kernel_size,
+                   void* stream) {
+  HK_REQUIRE(batch >= 0 && channels > 0 && kernel_size >= 1 &&
+                 kernel_size <= hk::kConvMaxTaps,
+             "hk_conv1d_step: bad shape B=%d C=%d K=%d (K in 1..%d)", batch, channels,
+             kernel_size, hk::kConvMaxTaps);
+  HK_REQUIRE(state || kernel_size == 1, "hk_conv1d_step: null state");
+  HK_REQUIRE(x && weight && out, "hk_conv1d_step: null operand");
+  const int64_t n = (int64_t)batch * channels;
+  if (n == 0) return HK_OK;
+  unsigned blocks;
+  const int st = hk::elementwise_grid(n, &blocks);
+  if (st != HK_OK) return st;
+  hipLaunchKernelGGL(hk::conv1d_step_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     state, x, weight, bias, mask, out, n, channels, kernel_size);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int hk_block_linear(const float* x, const float* weight, const float* bias, float* out, int batch,
+                    int blocks, int block_size, void* stream) {
+  HK_REQUIRE(batch >= 0 && blocks > 0 && block_size > 0,
+             "hk_block_linear: bad shape B=%d blocks=%d size=%d", batch, blocks, block_size);
+  HK_REQUIRE(x && weight && out, "hk_block_linear: null operand");
+  if (batch == 0) return HK_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (block_size % 16 == 0 && hk::aligned16(x) && hk::aligned16(weight) && hk::aligned16(out)) {
+    // Matrix cores: the blocks are the batches of one fp32 GEMM launch.
+    hk::GemmArgs g;
+    g.type = hk::GemmType::kF32;
+    g.A = x;
+    g.lda = (int64_t)blocks * block_size;
+    g.W = weight;
+    g.ldw = block_size;
+    g.M = batch;
+    g.N = block_size;
+    g.K = block_size;
+    g.batch = blocks;
+    g.a_bstride = block_size;
+    g.w_bstride = (int64_t)block_size * block_size;
+    g.c_bstride = block_size;
+    g.ep.bias = bias;
+    g.ep.out = out;
+    g.ep.ldo = (int64_t)blocks * block_size;
+    return hk::gemm(g, hk::GemmWorkspace{}, s);
+  }
+  const int64_t n = (int64_t)batch * blocks * block_size;
+  unsigned nb;
+  const int st = hk::elementwise_grid(n, &nb);
+  if (st != HK_OK) return st;
+  hipLaunchKernelGGL(hk::block_linear_kernel, dim3(nb), dim3(256), 0, s, x, weight, bias, out, n,
+                     blocks, block_size);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int hk_rglru_step(float* h, const float* x, const float* gate_i, const float* gate_r,
+                  const float* a, float c, const uint8_t* mask, float* out, int batch, int width,
+                  void* stream) {
+  HK_REQUIRE(batch >= 0 && width > 0, "hk_rglru_step: bad shape B=%d H=%d", batch, width);
+  HK_REQUIRE(h && x && gate_i && gate_r && a, "hk_rglru_step: null operand");
+  const int64_t n = (int64_t)batch * width;
+  if (n == 0) return HK_OK;
+  unsigned blocks;
+  const int st = hk::elementwise_grid(n, &blocks);
+  if (st != HK_OK) return st;
+  hipLaunchKernelGGL(hk::rglru_step_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, h, x,
+                     gate_i, gate_r, a, c, mask, out, n, width);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int hk_slstm_step(float* c_state, float* n_state, float* m_state, const float* i_pre,
+                  const float* f_pre, const float* z_pre, const float* o_pre,
+                  const uint8_t* mask, float* y, int batch, int width, void* stream) {
+  HK_REQUIRE(batch >= 0 && width > 0, "hk_slstm_step: bad shape B=%d H=%d", batch, width);
+  HK_REQUIRE(c_state && n_state && m_state && i_pre && f_pre && z_pre && o_pre && y,
+             "hk_slstm_step: null operand");
+  const int64_t n = (int64_t)batch * width;
+  if (n == 0) return HK_OK;
+  unsigned blocks;
+  const int st = hk::elementwise_grid(n, &blocks);
+  if (st != HK_OK) return st;
+  hipLaunchKernelGGL(hk::slstm_step_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     c_state, n_state, m_state, i_pre, f_pre, z_pre, o_pre, mask, y, n, width);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
 }
 
 }  // extern "C"

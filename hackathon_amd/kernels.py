@@ -1,7 +1,11 @@
 """Fused recurrent state steps on gfx950, behind the reference's kernel API.
 
 Drop-in for `model/kernels.py:346-401` (`mlstm_step`, `retnet_step`,
-`mamba2_step`) with the same contract (`model/kernels.py:28-34`):
+`mamba2_step`) with the same contract (`model/kernels.py:28-34`), plus the
+towers' other per-step operators under the same contract: the causal conv
+(`model/modules.py:45-49`), BlockLinear (`model/modules.py:71-79`), the
+RG-LRU step (`model/hawk.py:31-37`) and the sLSTM cell
+(`model/xlstm.py:247-274`):
 
 - the state is updated IN PLACE; rows whose mask is False end bit-identical,
   rows whose mask is True hold the new value;
@@ -116,4 +120,112 @@ def mamba2_step(ssm, x, b, c, dt, decay, mask):
         _lib.current_stream(dev),
     )
     _lib.check(st, "hk_mamba2_step")
+    return y
+
+
+def _dense(t: torch.Tensor, shape: tuple, name: str, device) -> None:
+    # In-place operands: fp32, contiguous, on the GPU (model/kernels.py:116-121).
+    assert t.dtype == torch.float32, f"{name} must be fp32, got {t.dtype}"
+    assert t.is_contiguous(), f"{name} must be contiguous, it is written in place"
+    assert tuple(t.shape) == shape, f"{name} must be {shape}, got {tuple(t.shape)}"
+    if t.device.type != "cuda":
+        raise _lib.HipLibraryError(f"{name} is on {t.device}; the HIP kernels need a GPU tensor")
+    assert t.device == device, f"{name} must be on {device}, it is on {t.device}"
+
+
+def causal_conv1d_step(state, x, weight, bias, mask=None):
+    """CausalConv1d.forward (model/modules.py:45-49) as a masked in-place step.
+
+    state [B, C, K-1] is advanced in place on active rows; weight is the
+    conv's [C, 1, K] (or [C, K]); bias [C] or None. Returns out [B, C], zero
+    on idle rows.
+    """
+    assert state.dim() == 3, f"state must be 3-D, got {tuple(state.shape)}"
+    batch, channels, hist = (int(s) for s in state.shape)
+    _dense(state, (batch, channels, hist), "state", state.device)
+    dev = state.device
+    taps = hist + 1
+    if weight.dim() == 3:
+        assert weight.shape[1] == 1, f"weight must be [C, 1, K], got {tuple(weight.shape)}"
+        weight = weight.reshape(weight.shape[0], weight.shape[2])
+    weight = _small(weight, (channels, taps), "weight", dev)
+    bias = None if bias is None else _small(bias, (channels,), "bias", dev)
+    x = _small(x, (batch, channels), "x", dev)
+    m = _mask_u8(mask, batch, dev)
+    out = torch.empty((batch, channels), dtype=torch.float32, device=dev)
+    st = _lib.lib().hk_conv1d_step(
+        state.data_ptr(), x.data_ptr(), weight.data_ptr(), _lib.ptr(bias), _lib.ptr(m),
+        out.data_ptr(), batch, channels, taps, _lib.current_stream(dev),
+    )
+    _lib.check(st, "hk_conv1d_step")
+    return out
+
+
+def block_linear(x, weight, bias=None):
+    """BlockLinear.forward (model/modules.py:71-79): weight [blocks, bs, bs]
+    as (blocks, out, in), x [B, blocks*bs]; returns a fresh [B, blocks*bs]."""
+    assert weight.dim() == 3 and weight.shape[1] == weight.shape[2], (
+        f"weight must be [blocks, bs, bs], got {tuple(weight.shape)}")
+    blocks, bs = int(weight.shape[0]), int(weight.shape[1])
+    dev = weight.device
+    if dev.type != "cuda":
+        raise _lib.HipLibraryError(f"weight is on {dev}; the HIP kernels need a GPU tensor")
+    assert x.dim() == 2, f"x must be 2-D, got {tuple(x.shape)}"
+    batch = int(x.shape[0])
+    x = _small(x, (batch, blocks * bs), "x", dev)
+    weight = _small(weight, (blocks, bs, bs), "weight", dev)
+    bias = None if bias is None else _small(bias, (blocks * bs,), "bias", dev)
+    out = torch.empty((batch, blocks * bs), dtype=torch.float32, device=dev)
+    st = _lib.lib().hk_block_linear(
+        x.data_ptr(), weight.data_ptr(), _lib.ptr(bias), out.data_ptr(), batch, blocks, bs,
+        _lib.current_stream(dev),
+    )
+    _lib.check(st, "hk_block_linear")
+    return out
+
+
+def rglru_step(state, x, gate_i, gate_r, a, c=8.0, mask=None):
+    """RGLRU.forward after its BlockLinears (model/hawk.py:31-37): gate_i =
+    input_gate(x), gate_r = recurrence_gate(x). state [B, H] is advanced in
+    place on active rows; returns the new state rows, zero on idle rows."""
+    assert state.dim() == 2, f"state must be 2-D, got {tuple(state.shape)}"
+    batch, width = (int(s) for s in state.shape)
+    dev = state.device
+    _dense(state, (batch, width), "state", dev)
+    x = _small(x, (batch, width), "x", dev)
+    gate_i = _small(gate_i, (batch, width), "gate_i", dev)
+    gate_r = _small(gate_r, (batch, width), "gate_r", dev)
+    a = _small(a, (width,), "a", dev)
+    m = _mask_u8(mask, batch, dev)
+    out = torch.empty((batch, width), dtype=torch.float32, device=dev)
+    st = _lib.lib().hk_rglru_step(
+        state.data_ptr(), x.data_ptr(), gate_i.data_ptr(), gate_r.data_ptr(), a.data_ptr(),
+        float(c), _lib.ptr(m), out.data_ptr(), batch, width, _lib.current_stream(dev),
+    )
+    _lib.check(st, "hk_rglru_step")
+    return out
+
+
+def slstm_step(state, i, f, z, o, mask=None):
+    """SLSTMCell.forward (model/xlstm.py:247-274) on gate pre-activations.
+
+    state = (cell, norm, max) [B, H] each, advanced in place on active rows
+    (max starts at -inf). Returns y [B, H], zero on idle rows.
+    """
+    c_st, n_st, m_st = state
+    assert c_st.dim() == 2, f"cell state must be 2-D, got {tuple(c_st.shape)}"
+    batch, width = (int(s) for s in c_st.shape)
+    dev = c_st.device
+    for t, name in ((c_st, "cell_state"), (n_st, "norm_state"), (m_st, "max_state")):
+        _dense(t, (batch, width), name, dev)
+    i, f, z, o = (_small(t, (batch, width), name, dev)
+                  for t, name in ((i, "i"), (f, "f"), (z, "z"), (o, "o")))
+    m = _mask_u8(mask, batch, dev)
+    y = torch.empty((batch, width), dtype=torch.float32, device=dev)
+    st = _lib.lib().hk_slstm_step(
+        c_st.data_ptr(), n_st.data_ptr(), m_st.data_ptr(), i.data_ptr(), f.data_ptr(),
+        z.data_ptr(), o.data_ptr(), _lib.ptr(m), y.data_ptr(), batch, width,
+        _lib.current_stream(dev),
+    )
+    _lib.check(st, "hk_slstm_step")
     return y

@@ -59,6 +59,49 @@ int hk_mamba2_step(float* ssm, const float* x, const float* b, const float* c, c
                    const float* decay, const uint8_t* mask, float* y, int batch, int heads,
                    int size_h, int size_c, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * The other per-step operators of the towers, same contract as above (state
+ * in place on active rows, idle rows bit-identical, zero outputs on idle
+ * rows, mask NULL = all rows). The reference computes these with torch
+ * modules and blends small state leaves with where(mask, new, old)
+ * (example_model.py:907-949); on active rows the results are those modules'.
+ * ------------------------------------------------------------------------- */
+
+/* CausalConv1d.forward (model/modules.py:23-49): window = [state[b,c,0..K-2],
+ * x[b,c]]; out[b,c] = bias[c] + sum_j weight[c,j] * window[j] (bias NULL =
+ * none); state[b,c,:] <- window[1..K-1]. state [B,C,K-1], weight [C,K] (the
+ * conv's [C,1,K]), 1 <= K <= 8. Mamba2's x/b/c convs (model/mamba2.py:84-86),
+ * the xLSTM blocks' and Hawk's conv all go through this one operator. */
+int hk_conv1d_step(float* state, const float* x, const float* weight, const float* bias,
+                   const uint8_t* mask, float* out, int batch, int channels, int kernel_size,
+                   void* stream);
+
+/* BlockLinear.forward (model/modules.py:71-79): out[b, n*bs + k] =
+ * sum_h x[b, n*bs + h] * weight[n,k,h] (+ bias[n*bs + k]); x, out
+ * [B, blocks*bs], weight [blocks, bs, bs] (blocks, out, in). No state, no
+ * mask. Block sizes that are multiples of 16 with 16-byte aligned operands
+ * run on the fp32 matrix cores. */
+int hk_block_linear(const float* x, const float* weight, const float* bias, float* out, int batch,
+                    int blocks, int block_size, void* stream);
+
+/* RGLRU.forward after its two BlockLinears (model/hawk.py:31-37):
+ * i = sigmoid(gate_i), r = sigmoid(gate_r), a_t = a ** (c * r),
+ * h <- h * a_t + sqrt(1 - a_t^2) * (i * x); out (NULL = none) = new h on
+ * active rows. h, x, gate_i, gate_r, out [B,H]; a [H]; the reference's c is 8. */
+int hk_rglru_step(float* h, const float* x, const float* gate_i, const float* gate_r,
+                  const float* a, float c, const uint8_t* mask, float* out, int batch, int width,
+                  void* stream);
+
+/* SLSTMCell.forward (model/xlstm.py:247-274) on the gate pre-activations
+ * (input BlockLinear + state BlockLinear + bias, model/xlstm.py:319-322):
+ * m' = max(i, m + logsigmoid(f)), i' = exp(i - m'), f' = exp(m + logsigmoid(f)
+ * - m'), c' = f' c + i' tanh(z), n' = f' n + i', y = sigmoid(o) c' / (n' +
+ * 1e-6). c, n, m [B,H] updated in place (m starts at -inf, model/xlstm.py:280);
+ * y [B,H]. */
+int hk_slstm_step(float* c_state, float* n_state, float* m_state, const float* i_pre,
+                  const float* f_pre, const float* z_pre, const float* o_pre,
+                  const uint8_t* mask, float* y, int batch, int width, void* stream);
+
 
 /* ---------------------------------------------------------------------------
  * Deterministic parameter initialisation (host, no GPU).

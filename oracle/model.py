@@ -89,6 +89,30 @@ def block_linear(x, w, b=None):
     return out if b is None else out + b
 
 
+def rglru(x, h, gi, gr, a, c=8.0):
+    """RGLRU.forward after its two BlockLinears (model/hawk.py:31-37):
+    gi = input_gate(x), gr = recurrence_gate(x); returns the new state."""
+    i_t = torch.sigmoid(gi)
+    r_t = torch.sigmoid(gr)
+    a_t = a ** (c * r_t)
+    mult = torch.sqrt(1 - a_t ** 2)
+    return (h * a_t) + (mult * (i_t * x))
+
+
+def slstm_cell(gi, gf, gz, go, c, n, m):
+    """SLSTMCell.forward (model/xlstm.py:258-274) on gate pre-activations;
+    returns y and the new (c, n, m)."""
+    lfm = m + F.logsigmoid(gf)
+    m_new = torch.maximum(gi, lfm)
+    o_gate = torch.sigmoid(go)
+    i_gate = torch.exp(gi - m_new)
+    f_gate = torch.exp(lfm - m_new)
+    c_new = f_gate * c + i_gate * torch.tanh(gz)
+    n_new = f_gate * n + i_gate
+    y = o_gate * c_new / (n_new + 1e-6)
+    return y, (c_new, n_new, m_new)
+
+
 # ---- layers ----------------------------------------------------------------------
 
 
@@ -151,11 +175,8 @@ def hawk(P: Params, pre, cfg, x, state):
     gate = F.gelu(P.linear(x, pre + "gate_proj", bias=False))
     x = P.linear(x, pre + "recurrent_proj", bias=False)
     x, conv_state = causal_conv(x, conv_state, P[pre + "conv.conv.weight"], P[pre + "conv.conv.bias"])
-    i_t = torch.sigmoid(block_linear(x, P[pre + "rglru.input_gate.weight"]))
-    r_t = torch.sigmoid(block_linear(x, P[pre + "rglru.recurrence_gate.weight"]))
-    a_t = P[pre + "rglru.a"] ** (8.0 * r_t)
-    mult = torch.sqrt(1 - a_t ** 2)
-    h_new = (h * a_t) + (mult * (i_t * x))
+    h_new = rglru(x, h, block_linear(x, P[pre + "rglru.input_gate.weight"]),
+                  block_linear(x, P[pre + "rglru.recurrence_gate.weight"]), P[pre + "rglru.a"])
     return P.linear(gate * h_new, pre + "out_proj", bias=False), [conv_state, h_new]
 
 
@@ -169,14 +190,7 @@ def slstm_block(P: Params, pre, cfg, x, state):
     gf = block_linear(xca, P[pre + "fgate_input.weight"]) + block_linear(h, P[pre + "fgate_state.weight"], P[pre + "fgate_state.bias"])
     gz = block_linear(xn, P[pre + "zgate_input.weight"]) + block_linear(h, P[pre + "zgate_state.weight"], P[pre + "zgate_state.bias"])
     go = block_linear(xn, P[pre + "ogate_input.weight"]) + block_linear(h, P[pre + "ogate_state.weight"], P[pre + "ogate_state.bias"])
-    lfm = m + F.logsigmoid(gf)
-    m_new = torch.maximum(gi, lfm)
-    o_gate = torch.sigmoid(go)
-    i_gate = torch.exp(gi - m_new)
-    f_gate = torch.exp(lfm - m_new)
-    c_new = f_gate * c + i_gate * torch.tanh(gz)
-    n_new = f_gate * n + i_gate
-    y = o_gate * c_new / (n_new + 1e-6)
+    y, (c_new, n_new, m_new) = slstm_cell(gi, gf, gz, go, c, n, m)
     out = group_norm(y, cfg.slstm_heads, P[pre + "group_norm.weight"], P[pre + "group_norm.bias"])
     return out + skip, (conv_state, y, (c_new, n_new, m_new))
 

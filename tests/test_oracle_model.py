@@ -101,3 +101,40 @@ def test_block_linear_is_block_diagonal_linear():
     x = torch.randn(B, nb * bs, generator=g)
     dense = torch.block_diag(*W)  # (out, in) blocks
     torch.testing.assert_close(om.block_linear(x, W), F.linear(x, dense))
+
+
+def test_rglru_special_cases():
+    # model/hawk.py:31-37. Recurrence gate saturated shut (r = 0): a_t = 1,
+    # the state carries over and the input is dropped; saturated open (r = 1)
+    # with the input gate shut (i = 0): plain decay h * a^c.
+    h = torch.randn(3, 5, dtype=torch.float64)
+    x = torch.randn(3, 5, dtype=torch.float64)
+    a = torch.rand(5, dtype=torch.float64) * 0.8 + 0.1
+    big = torch.full((3, 5), 1e4, dtype=torch.float64)
+    assert torch.equal(om.rglru(x, h, big, -big, a), h)
+    torch.testing.assert_close(om.rglru(x, h, -big, big, a), h * a ** 8, rtol=1e-12, atol=0)
+    # both gates open: h' = a^8 h + sqrt(1 - a^16) x
+    want = a ** 8 * h + torch.sqrt(1 - a ** 16) * x
+    torch.testing.assert_close(om.rglru(x, h, big, big, a), want, rtol=1e-12, atol=1e-12)
+
+
+def test_slstm_cell_first_step_and_scale_invariance():
+    # model/xlstm.py:258-274 from the initial state (c = n = 0, m = -inf):
+    # m' = i, i' = 1, f' = 0, c' = tanh z, n' = 1, y = sigmoid(o) tanh(z) / (1 + 1e-6).
+    g = torch.Generator().manual_seed(3)
+    i, f, z, o = (torch.randn(4, 6, generator=g, dtype=torch.float64) for _ in range(4))
+    zero = torch.zeros(4, 6, dtype=torch.float64)
+    y, (c, n, m) = om.slstm_cell(i, f, z, o, zero, zero, torch.full_like(zero, float("-inf")))
+    assert torch.equal(m, i) and torch.equal(n, torch.ones_like(n))
+    torch.testing.assert_close(c, torch.tanh(z), rtol=1e-15, atol=0)
+    torch.testing.assert_close(y, torch.sigmoid(o) * torch.tanh(z) / (1 + 1e-6), rtol=1e-15, atol=0)
+    # The stabiliser is a representation: (c, n, m) and (c e^-d, n e^-d, m + d)
+    # stand for the same unstabilised state c e^m, so one step on the same
+    # gates gives the same ratio c'/n'.
+    c0 = torch.randn(4, 6, generator=g, dtype=torch.float64)
+    n0 = torch.rand(4, 6, generator=g, dtype=torch.float64) + 0.5
+    m0 = torch.randn(4, 6, generator=g, dtype=torch.float64)
+    _, (c1, n1, _) = om.slstm_cell(i, f, z, o, c0, n0, m0)
+    _, (c2, n2, _) = om.slstm_cell(i, f, z, o, c0 * torch.exp(torch.tensor(-2.0, dtype=torch.float64)),
+                                   n0 * torch.exp(torch.tensor(-2.0, dtype=torch.float64)), m0 + 2.0)
+    torch.testing.assert_close(c1 / n1, c2 / n2, rtol=1e-12, atol=1e-12)
