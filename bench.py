@@ -490,7 +490,9 @@ def main() -> int:
 
     stream = torch.cuda.current_stream(dev)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
-    eng.profile(True)
+    # Only the roofline's kernel is event-bracketed in the timed region: the
+    # hooks cost host and queue time per bracketed launch.
+    eng.profile(("mlstm",))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for j in range(K):
@@ -501,6 +503,15 @@ def main() -> int:
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     n_launch, scan_ms = eng.profile_read("mlstm")
+    eng.profile(False)
+    eng.check()
+    # Diagnostic pass after the timed region: every launch kind bracketed,
+    # over the first ticks of the timed sequence again.
+    n_diag = min(K, 40)
+    eng.profile(True)
+    for j in range(n_diag):
+        eng.tick(packed[W + j], feats[W + j], preds[W + j])
+    torch.cuda.synchronize()
     other = {k: eng.profile_read(k) for k in ("mamba2", "retnet", "slstm", "gemm")}
     eng.profile(False)
     eng.check()
@@ -529,14 +540,19 @@ def main() -> int:
     achieved = mbytes / (scan_ms / 1000.0) / 1e9 if scan_ms > 0 else 0.0
     kernels = {"mlstm_scan": {"launches": n_launch, "avg_us": 1000.0 * scan_ms / max(n_launch, 1),
                               "GB/s": achieved}}
+    # (The diagnostic pass replays timed ticks, so a launch's algorithmic
+    # bytes are taken as the timed region's per-launch average.)
     for name, b in (("mamba2", sbytes), ("retnet", rbytes)):
         n_l, ms = other[name]
+        per = b / (K * D_)
         kernels[f"{name}_scan"] = {"launches": n_l, "avg_us": 1000.0 * ms / max(n_l, 1),
-                                   "GB/s": b / (ms / 1000.0) / 1e9 if ms > 0 else 0.0}
+                                   "GB/s": per * n_l / (ms / 1000.0) / 1e9 if ms > 0 else 0.0}
     for name in ("slstm", "gemm"):
         n_l, ms = other[name]
         kernels[name] = {"launches": n_l, "avg_us": 1000.0 * ms / max(n_l, 1),
-                         "ms_per_step": ms / K}
+                         "ms_per_step": ms / max(n_diag, 1)}
+    kernels["note"] = (f"mlstm_scan: the timed ticks; the others: a diagnostic pass of {n_diag} "
+                       "ticks after them with every launch kind event-bracketed")
 
     traffic, traffic_ratio = counter_traffic()
     line = {

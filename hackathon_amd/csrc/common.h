@@ -129,8 +129,14 @@ __device__ __forceinline__ float transposed_wave_sum(float (&v)[NV]) {
   for (int n = NV, d = 32; n > 1; n >>= 1, d >>= 1) {
     const bool hi = (lane & d) != 0;
 #pragma unroll
-    for (int i = 0; i < n / 2; ++i)
-      v[i] = (hi ? v[n / 2 + i] : v[i]) + __shfl_xor(hi ? v[i] : v[n / 2 + i], d, 64);
+    for (int i = 0; i < n / 2; ++i) {
+      // selects on values (not on element addresses, which the compiler may
+      // turn into indexed private-memory accesses)
+      const float lo_v = v[i], hi_v = v[n / 2 + i];
+      const float keep = hi ? hi_v : lo_v;
+      const float send = hi ? lo_v : hi_v;
+      v[i] = keep + __shfl_xor(send, d, 64);
+    }
   }
   float r = v[0];
 #pragma unroll

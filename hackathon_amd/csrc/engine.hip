@@ -274,7 +274,7 @@ struct Engine {
   std::vector<char> seen;
   // Optional per-launch timing of the matrix-state scans (kind 0 mLSTM,
   // 1 Mamba2, 2 RetNet): event pairs recorded on the launch stream.
-  bool prof = false;
+  int prof = 0;  // bit k: time launches of kind k
   std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[5];
   size_t prof_used[5] = {0, 0, 0, 0, 0};
 
@@ -439,11 +439,12 @@ int build_workspace(Engine& e) {
   return HK_OK;
 }
 
-// Runs `fn` bracketed by timing events of `kind` when profiling is on
-// (0 mLSTM scan, 1 Mamba2 scan, 2 RetNet scan, 3 sLSTM recurrence, 4 GEMM).
+// Runs `fn` bracketed by timing events of `kind` when profiling of that kind
+// is on (0 mLSTM scan, 1 Mamba2 scan, 2 RetNet scan, 3 sLSTM recurrence,
+// 4 GEMM).
 template <typename Fn>
 int timed(Engine& e, int kind, hipStream_t s, Fn&& fn) {
-  if (!e.prof) return fn();
+  if (!(e.prof & (1 << kind))) return fn();
   auto& v = e.prof_ev[kind];
   if (e.prof_used[kind] == v.size()) {
     std::pair<hipEvent_t, hipEvent_t> pr;
@@ -1218,12 +1219,13 @@ int hk_engine_check(void* h) {
 }
 
 // Per-launch timing (kind 0 mLSTM scan, 1 Mamba2 scan, 2 RetNet scan,
-// 3 sLSTM recurrence, 4 GEMM). enable != 0 starts recording (and clears
-// earlier records).
-int hk_engine_profile(void* h, int enable) {
+// 3 sLSTM recurrence, 4 GEMM): bit k of `kinds` records kind k; 0 stops.
+// Clears earlier records.
+int hk_engine_profile(void* h, int kinds) {
   HK_REQUIRE(h, "hk_engine_profile: null handle");
+  HK_REQUIRE(kinds >= 0 && kinds < 32, "hk_engine_profile: bad kind mask %d", kinds);
   Engine& e = *static_cast<Engine*>(h);
-  e.prof = enable != 0;
+  e.prof = kinds;
   for (auto& u : e.prof_used) u = 0;
   return HK_OK;
 }

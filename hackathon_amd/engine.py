@@ -334,9 +334,17 @@ class Engine:
         _lib.check(_lib.lib().hk_engine_check(self._h), "hk_engine_check")
 
     # -- measurement ---------------------------------------------------------------
-    def profile(self, enable: bool):
-        """Start (or stop) timing every matrix-state scan launch."""
-        _lib.check(_lib.lib().hk_engine_profile(self._h, 1 if enable else 0), "hk_engine_profile")
+    def profile(self, kinds=True):
+        """Time the launches of the given kinds (names of SCAN_KINDS; True =
+        all, False or () = stop); clears earlier records."""
+        if kinds is True:
+            kinds = tuple(SCAN_KINDS)
+        elif kinds is False:
+            kinds = ()
+        mask = 0
+        for k in kinds:
+            mask |= 1 << SCAN_KINDS[k]
+        _lib.check(_lib.lib().hk_engine_profile(self._h, mask), "hk_engine_profile")
 
     def profile_read(self, kind: str) -> tuple[int, float]:
         """(launch count, summed ms) of the recorded launches of `kind`."""

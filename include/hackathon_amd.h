@@ -178,10 +178,11 @@ int hk_engine_tick(void* handle, const int* slot_ids_host, const int* run_off_ho
 int hk_engine_check(void* handle);
 
 /* Measurement hook (no reference counterpart; the reference times with CUDA
- * events and torch.profiler, profile_step.py:337-397): when enabled, every
- * launch of kind 0 mLSTM scan, 1 Mamba2 scan, 2 RetNet scan, 3 sLSTM
- * recurrence, 4 projection GEMM is bracketed by HIP events on its stream. */
-int hk_engine_profile(void* handle, int enable);
+ * events and torch.profiler, profile_step.py:337-397): with bit k of `kinds`
+ * set, every launch of kind k (0 mLSTM scan, 1 Mamba2 scan, 2 RetNet scan,
+ * 3 sLSTM recurrence, 4 projection GEMM) is bracketed by HIP events on its
+ * stream; 0 stops. Clears earlier records. */
+int hk_engine_profile(void* handle, int kinds);
 
 /* Waits for the recorded launches of `kind`, returns their count and summed
  * duration in ms, and clears the records. */
