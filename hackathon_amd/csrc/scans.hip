@@ -62,47 +62,52 @@ __global__ __launch_bounds__(256) void conv_scan_kernel(
   st[2 * channels + c] = s2;
 }
 
-// grid (runs, ceil(hidden/256)); thread per channel. The scale recurrence
-// s' = s*gamma + 1 is per head and is recomputed by every thread of the head.
+// grid (rows, ceil(hidden/256)); thread per (row, channel): every row is
+// independent once its run is known (binary search over the run offsets,
+// uniform per work-group). The scale recurrence s' = s*gamma + 1 is stepped
+// from the slot's stored scale through the row's position in its run, the
+// same operations in the same order as a sequential pass.
 __global__ __launch_bounds__(256) void retnet_prep_kernel(
-    const int* __restrict__ slot_ids, const int* __restrict__ run_off,
+    const int* __restrict__ slot_ids, const int* __restrict__ run_off, int n_runs,
     const float* __restrict__ qkvg, int64_t ld, int hidden, int head_size, float k_scaling,
     const float* __restrict__ angle, const float* __restrict__ decay,
     const int* __restrict__ offsets, const float* __restrict__ scales, float* __restrict__ k_rope,
     float* __restrict__ q_scaled) {
-  const int run = blockIdx.x;
+  const int r = blockIdx.x;
   const int c = blockIdx.y * 256 + threadIdx.x;
+  int lo = 0, hi = n_runs - 1;  // the run holding row r: run_off[lo] <= r < run_off[lo + 1]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (run_off[mid] <= r) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+    }
+  }
   if (c >= hidden) return;
   const int heads = hidden / head_size;
   const int head = c / head_size;
   const int j = c % head_size;
   const int partner = (j & 1) ? c - 1 : c + 1;
   const float sign = (j & 1) ? 1.0f : -1.0f;  // rotate_every_two: (-x1, x0)
-  const int slot = slot_ids[run];
-  const int r0 = run_off[run];
-  const int r1 = run_off[run + 1];
-  const int off0 = offsets[slot];
-  float sc = scales[(int64_t)slot * heads + head];
+  const int slot = slot_ids[lo];
+  const int t = r - run_off[lo];
   const float gam = decay[head];
-  const float ang = angle[j];
-  // unrolled so that several rows' loads are in flight together
-#pragma unroll 8
-  for (int r = r0; r < r1; ++r) {
-    const float* row = qkvg + (int64_t)r * ld;
-    const float theta = (float)(off0 + (r - r0)) * ang;
-    const float sn = sinf(theta);
-    const float cs = cosf(theta);
-    const float q = row[c];
-    const float qp = sign * row[partner];
-    const float k = row[hidden + c] * k_scaling;
-    const float kp = sign * (row[hidden + partner] * k_scaling);
-    const float qr = q * cs + qp * sn;
-    const float kr = k * cs + kp * sn;
-    sc = sc * gam + 1.0f;
-    const float sf = 1.0f / sqrtf(sc);
-    k_rope[(int64_t)r * hidden + c] = kr;
-    q_scaled[(int64_t)r * hidden + c] = qr * sf;
-  }
+  float sc = scales[(int64_t)slot * heads + head];
+  for (int i = 0; i <= t; ++i) sc = sc * gam + 1.0f;
+  const float* row = qkvg + (int64_t)r * ld;
+  const float theta = (float)(offsets[slot] + t) * angle[j];
+  const float sn = sinf(theta);
+  const float cs = cosf(theta);
+  const float q = row[c];
+  const float qp = sign * row[partner];
+  const float k = row[hidden + c] * k_scaling;
+  const float kp = sign * (row[hidden + partner] * k_scaling);
+  const float qr = q * cs + qp * sn;
+  const float kr = k * cs + kp * sn;
+  const float sf = 1.0f / sqrtf(sc);
+  k_rope[(int64_t)r * hidden + c] = kr;
+  q_scaled[(int64_t)r * hidden + c] = qr * sf;
 }
 
 // After retnet_prep: offsets += run length; scales advanced through the run
@@ -124,7 +129,12 @@ __global__ void retnet_advance_kernel(const int* __restrict__ slot_ids,
   if (head == 0) offsets[slot] += len;
 }
 
-// grid (runs, ceil(hidden/256)); thread per channel.
+// grid (runs, ceil(hidden/256)); thread per channel. Only h' = h*a_t + u_t
+// is sequential: a run's rows go through in chunks of kRgChunk, the next
+// chunk's loads in flight while this one is computed, and within a chunk the
+// gates (a_t, u_t and the output gate) of all rows are formed before the
+// recurrence runs over them.
+constexpr int kRgChunk = 16;
 __global__ __launch_bounds__(256) void rglru_scan_kernel(
     const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ x,
     const float* __restrict__ gi, const float* __restrict__ gr, int64_t ldg,
@@ -137,20 +147,53 @@ __global__ __launch_bounds__(256) void rglru_scan_kernel(
   const int slot = slot_ids[run];
   const int r0 = run_off[run];
   const int r1 = run_off[run + 1];
+  if (r1 <= r0) return;
   float h = h_state[(int64_t)slot * hidden + c];
   const float base = a[c];
-  // unrolled so that several rows' loads are in flight together
-#pragma unroll 8
-  for (int r = r0; r < r1; ++r) {
-    const int64_t ri = (int64_t)r;
-    const float it = sigmoid(gi[ri * ldg + c]);
-    const float rt = sigmoid(gr[ri * ldg + c]);
-    const float at = powf(base, c_exp * rt);
-    const float mult = sqrtf(1.0f - at * at);
-    h = (h * at) + (mult * (it * x[ri * hidden + c]));
-    const float o = gelu_erf(gate[ri * ld_gate + c]) * h;
-    if (out) out[ri * hidden + c] = o;
-    if (out_lp) out_lp[ri * hidden + c] = f32_to_bf16_bits(o);
+  struct Rows {
+    float i[kRgChunk], r[kRgChunk], x[kRgChunk], g[kRgChunk];
+  };
+  // rows past the run read its last row (unused)
+  auto load = [&](Rows& v, int rb) {
+#pragma unroll
+    for (int k = 0; k < kRgChunk; ++k) {
+      const int64_t ri = (int64_t)min(rb + k, r1 - 1);
+      v.i[k] = gi[ri * ldg + c];
+      v.r[k] = gr[ri * ldg + c];
+      v.x[k] = x[ri * hidden + c];
+      v.g[k] = gate[ri * ld_gate + c];
+    }
+  };
+  auto step = [&](const Rows& v, int rb) {
+    float at[kRgChunk], ut[kRgChunk], og[kRgChunk];
+#pragma unroll
+    for (int k = 0; k < kRgChunk; ++k) {
+      const float it = sigmoid(v.i[k]);
+      const float rt = sigmoid(v.r[k]);
+      at[k] = powf(base, c_exp * rt);
+      const float mult = sqrtf(1.0f - at[k] * at[k]);
+      ut[k] = mult * (it * v.x[k]);
+      og[k] = gelu_erf(v.g[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kRgChunk; ++k) {
+      if (rb + k < r1) {
+        h = (h * at[k]) + ut[k];
+        const float o = og[k] * h;
+        const int64_t ri = (int64_t)(rb + k);
+        if (out) out[ri * hidden + c] = o;
+        if (out_lp) out_lp[ri * hidden + c] = f32_to_bf16_bits(o);
+      }
+    }
+  };
+  Rows va, vb;
+  load(va, r0);
+  for (int rb = r0; rb < r1; rb += 2 * kRgChunk) {
+    if (rb + kRgChunk < r1) load(vb, rb + kRgChunk);
+    step(va, rb);
+    if (rb + kRgChunk >= r1) break;
+    if (rb + 2 * kRgChunk < r1) load(va, rb + 2 * kRgChunk);
+    step(vb, rb + kRgChunk);
   }
   h_state[(int64_t)slot * hidden + c] = h;
 }
@@ -787,10 +830,11 @@ int retnet_prep(const Runs& r, const float* qkvg, int64_t ld, int hidden, int he
                 float* scales, float* k_rope, float* q_scaled, hipStream_t s) {
   if (r.n_runs == 0) return HK_OK;
   HK_REQUIRE(hidden % heads == 0 && (hidden / heads) % 2 == 0, "retnet_prep: bad head size");
-  dim3 grid(r.n_runs, (hidden + 255) / 256);
-  hipLaunchKernelGGL(retnet_prep_kernel, grid, dim3(256), 0, s, r.slot_ids, r.run_off, qkvg, ld,
-                     hidden, hidden / heads, k_scaling, angle, decay, offsets, scales, k_rope,
-                     q_scaled);
+  HK_REQUIRE(r.n_rows > 0, "retnet_prep: bad row count %d", r.n_rows);
+  dim3 grid(r.n_rows, (hidden + 255) / 256);
+  hipLaunchKernelGGL(retnet_prep_kernel, grid, dim3(256), 0, s, r.slot_ids, r.run_off, r.n_runs,
+                     qkvg, ld, hidden, hidden / heads, k_scaling, angle, decay, offsets, scales,
+                     k_rope, q_scaled);
   HK_LAUNCH_CHECK();
   const int n = r.n_runs * heads;
   hipLaunchKernelGGL(retnet_advance_kernel, dim3((n + 255) / 256), dim3(256), 0, s, r.slot_ids,
