@@ -398,33 +398,36 @@ __global__ void mlstm_qkv_kernel(const float* __restrict__ x_conv, const float* 
 // their NOUT gate-row products; the work-group's NOUT sums (in a fixed
 // order) are segment seg's partial pre-activations, plane seg of if_part
 // [segs][n_rows][NOUT]; plane 0 also carries the bias.
-template <int NOUT>
+template <int NOUT, int R>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void mlstm_qkv_if_kernel(
     const float* __restrict__ x_conv, const float* __restrict__ x_m, int64_t ld_xm,
     const float* __restrict__ wq, const float* __restrict__ wk, const float* __restrict__ wv,
     int n_rows, int inner, float k_div, const float* __restrict__ w_if,
     const float* __restrict__ b_if, float* __restrict__ qkv, float* __restrict__ ks,
     float* __restrict__ if_part) {
-  __shared__ float red[4][NOUT];
+  static_assert(R * NOUT <= 64, "one butterfly for all sums");
+  __shared__ float red[4][R * NOUT];
   const int seg = blockIdx.x;
-  const int row = blockIdx.y;
+  const int rbase = blockIdx.y * R;  // rows rbase .. rbase + R - 1 (past n_rows: the last row)
   const int tid = threadIdx.x;
   const int per = (inner >> 2) / gridDim.x;  // 4-column blocks per segment
-  const float4* xc4 = reinterpret_cast<const float4*>(x_conv + (int64_t)row * inner);
-  const float4* xm4 = reinterpret_cast<const float4*>(x_m + (int64_t)row * ld_xm);
-  float4* q4o = reinterpret_cast<float4*>(qkv + (int64_t)row * 3 * inner);
-  float4* k4o = q4o + (inner >> 2);
-  float4* v4o = k4o + (inner >> 2);
-  float4* ks4 = reinterpret_cast<float4*>(ks + (int64_t)row * inner);
   const int64_t wl = (int64_t)3 * inner;
-  auto dot4 = [](float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; };
-  float acc[NOUT];
+  int rows[R];
 #pragma unroll
-  for (int n = 0; n < NOUT; ++n) acc[n] = 0.0f;
+  for (int r = 0; r < R; ++r) rows[r] = min(rbase + r, n_rows - 1);
+  auto dot4 = [](float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; };
+  float acc[R * NOUT];
+#pragma unroll
+  for (int i = 0; i < R * NOUT; ++i) acc[i] = 0.0f;
   for (int nb = seg * per + tid; nb < (seg + 1) * per; nb += 256) {
-    // Every operand of the block is loaded before any is used (one L2 round
-    // trip per block, not one per gate row).
-    const float4 xc = xc4[nb], xm = xm4[nb];
+    // The block's weights are loaded once for all R rows; every operand is
+    // loaded before any is used (one L2 round trip per block).
+    float4 xc[R], xm[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      xc[r] = reinterpret_cast<const float4*>(x_conv + (int64_t)rows[r] * inner)[nb];
+      xm[r] = reinterpret_cast<const float4*>(x_m + (int64_t)rows[r] * ld_xm)[nb];
+    }
     // W[nb][o][h]: block nb's 4x4 weights, row o = output column 4nb + o
     float4 bq[4], bk[4], bv[4];
 #pragma unroll
@@ -433,36 +436,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       bk[o] = reinterpret_cast<const float4*>(wk)[(int64_t)nb * 4 + o];
       bv[o] = reinterpret_cast<const float4*>(wv)[(int64_t)nb * 4 + o];
     }
+    float4 q[R], k[R], v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      q[r] = make_float4(dot4(xc[r], bq[0]), dot4(xc[r], bq[1]), dot4(xc[r], bq[2]), dot4(xc[r], bq[3]));
+      k[r] = make_float4(dot4(xc[r], bk[0]), dot4(xc[r], bk[1]), dot4(xc[r], bk[2]), dot4(xc[r], bk[3]));
+      v[r] = make_float4(dot4(xm[r], bv[0]), dot4(xm[r], bv[1]), dot4(xm[r], bv[2]), dot4(xm[r], bv[3]));
+      if (rbase + r < n_rows) {
+        float4* q4o = reinterpret_cast<float4*>(qkv + (int64_t)rows[r] * 3 * inner);
+        q4o[nb] = q[r];
+        q4o[(inner >> 2) + nb] = k[r];
+        q4o[(inner >> 1) + nb] = v[r];
+        reinterpret_cast<float4*>(ks + (int64_t)rows[r] * inner)[nb] =
+            make_float4(k[r].x / k_div, k[r].y / k_div, k[r].z / k_div, k[r].w / k_div);
+      }
+    }
     // the gate rows' 16-byte pieces of this block's q, k and v columns
-    float4 wi[NOUT][3];
 #pragma unroll
     for (int n = 0; n < NOUT; ++n) {
       const float4* wn = reinterpret_cast<const float4*>(w_if + n * wl);
-      wi[n][0] = wn[nb];
-      wi[n][1] = wn[(inner >> 2) + nb];
-      wi[n][2] = wn[(inner >> 1) + nb];
+      const float4 w0 = wn[nb], w1 = wn[(inner >> 2) + nb], w2 = wn[(inner >> 1) + nb];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        acc[r * NOUT + n] += dot4(q[r], w0) + dot4(k[r], w1) + dot4(v[r], w2);
     }
-    const float4 q = make_float4(dot4(xc, bq[0]), dot4(xc, bq[1]), dot4(xc, bq[2]), dot4(xc, bq[3]));
-    const float4 k = make_float4(dot4(xc, bk[0]), dot4(xc, bk[1]), dot4(xc, bk[2]), dot4(xc, bk[3]));
-    const float4 v = make_float4(dot4(xm, bv[0]), dot4(xm, bv[1]), dot4(xm, bv[2]), dot4(xm, bv[3]));
-    q4o[nb] = q;
-    k4o[nb] = k;
-    v4o[nb] = v;
-    ks4[nb] = make_float4(k.x / k_div, k.y / k_div, k.z / k_div, k.w / k_div);
-#pragma unroll
-    for (int n = 0; n < NOUT; ++n)
-      acc[n] += dot4(q, wi[n][0]) + dot4(k, wi[n][1]) + dot4(v, wi[n][2]);
   }
-  // lane (64 / NOUT) * n of each wave holds the wave's sum n
-  const float ws = transposed_wave_sum<NOUT>(acc);
+  // lane (64 / (R*NOUT)) * i of each wave holds the wave's sum i = r*NOUT + n
+  constexpr int NV = R * NOUT;
+  const float ws = transposed_wave_sum<NV>(acc);
   const int lane = tid & 63, wave = tid >> 6;
-  if (lane % (64 / NOUT) == 0) red[wave][lane / (64 / NOUT)] = ws;
+  if (lane % (64 / NV) == 0) red[wave][lane / (64 / NV)] = ws;
   lds_barrier();
-  if (tid < NOUT) {
-    float t = seg == 0 ? b_if[tid] : 0.0f;
+  if (tid < NV) {
+    const int r = tid / NOUT, n = tid % NOUT;
+    if (rbase + r < n_rows) {
+      float t = seg == 0 ? b_if[n] : 0.0f;
 #pragma unroll
-    for (int w2 = 0; w2 < 4; ++w2) t += red[w2][tid];
-    if_part[((int64_t)seg * n_rows + row) * NOUT + tid] = t;
+      for (int w2 = 0; w2 < 4; ++w2) t += red[w2][tid];
+      if_part[((int64_t)seg * n_rows + rbase + r) * NOUT + n] = t;
+    }
   }
 }
 
@@ -650,25 +662,19 @@ int mlstm_qkv_if(const float* x_conv, const float* x_m, int64_t ld_xm, const flo
                  al16(ks),
              "mlstm_qkv_if: inner %d, %d gate rows, %d segments or alignment unsupported", inner,
              n_out, segs);
-  const dim3 grid(segs, n_rows), block(256);
+  // R rows per work-group share each block's weight loads (R * n_out <= 64).
+  const dim3 block(256);
+#define HK_QKV_IF(NOUT, R)                                                                      \
+  hipLaunchKernelGGL((mlstm_qkv_if_kernel<NOUT, R>), dim3(segs, (n_rows + (R)-1) / (R)), block, \
+                     0, s, x_conv, x_m, ld_xm, wq, wk, wv, n_rows, inner, k_div, w_if, b_if, qkv, \
+                     ks, if_part)
   switch (n_out) {
-    case 4:
-      hipLaunchKernelGGL(mlstm_qkv_if_kernel<4>, grid, block, 0, s, x_conv, x_m, ld_xm, wq, wk, wv,
-                         n_rows, inner, k_div, w_if, b_if, qkv, ks, if_part);
-      break;
-    case 8:
-      hipLaunchKernelGGL(mlstm_qkv_if_kernel<8>, grid, block, 0, s, x_conv, x_m, ld_xm, wq, wk, wv,
-                         n_rows, inner, k_div, w_if, b_if, qkv, ks, if_part);
-      break;
-    case 16:
-      hipLaunchKernelGGL(mlstm_qkv_if_kernel<16>, grid, block, 0, s, x_conv, x_m, ld_xm, wq, wk,
-                         wv, n_rows, inner, k_div, w_if, b_if, qkv, ks, if_part);
-      break;
-    default:
-      hipLaunchKernelGGL(mlstm_qkv_if_kernel<32>, grid, block, 0, s, x_conv, x_m, ld_xm, wq, wk,
-                         wv, n_rows, inner, k_div, w_if, b_if, qkv, ks, if_part);
-      break;
+    case 4: HK_QKV_IF(4, 4); break;
+    case 8: HK_QKV_IF(8, 4); break;
+    case 16: HK_QKV_IF(16, 4); break;
+    default: HK_QKV_IF(32, 2); break;
   }
+#undef HK_QKV_IF
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
