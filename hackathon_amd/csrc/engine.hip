@@ -251,7 +251,8 @@ struct Engine {
   int* d_act2 = nullptr;     // [max_rows]
   unsigned long long* d_xch = nullptr;   // [max_rows][H]: sLSTM h exchange words
   unsigned long long* d_xch2 = nullptr;  // the same for the second xLSTM group
-  unsigned int xch_tag = 0;              // tag of the last sLSTM launch
+  unsigned int xch_tag[2] = {0, 0};      // tag of the last sLSTM launch on d_xch / d_xch2
+  bool sl_overlap = false;  // the two groups' persistent launches can be co-resident together
   int* d_err = nullptr;      // [1]: set by a kernel whose barrier timed out
   uint64_t* d_trace = nullptr;  // HK_TRACE_SLSTM: per-step stamps of layer 0's sLSTM
   int* h_stage = nullptr;    // pinned [2][stage_ints()]
@@ -268,8 +269,8 @@ struct Engine {
   hipStream_t side[kSide] = {nullptr, nullptr, nullptr};
   hipEvent_t fork_ev = nullptr;
   hipEvent_t join_ev[kSide] = {nullptr, nullptr, nullptr};
-  // Per layer, the two xLSTM groups' persistent sLSTM launches alternate
-  // (group 2 then group 1): two such launches never share the GPU.
+  // Where two persistent sLSTM launches cannot be co-resident at once, the
+  // two xLSTM groups' launches alternate per layer (group 2 then group 1).
   std::vector<hipEvent_t> sl_ev[2];
   std::vector<char> seen;
   // Optional per-launch timing of the matrix-state scans (kind 0 mLSTM,
@@ -434,6 +435,10 @@ int build_workspace(Engine& e) {
   for (auto& v : e.sl_ev) {
     v.assign(d.D, nullptr);
     for (auto& ev : v) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  }
+  {
+    const int st = slstm_persist_pair_fits(d.H, d.nh_s, e.max_runs, e.max_rows, &e.sl_overlap);
+    if (st != HK_OK) return st;
   }
 
   return HK_OK;
@@ -625,18 +630,20 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
                       w.GIN, 4 * H, s));
   if (slstm_persist_supported(H, d.nh_s)) {
     if (ord.wait) HK_CHECK_HIP(hipStreamWaitEvent(s, ord.wait, 0));
-    if (++e.xch_tag == 0) {
-      // Tags wrapped: clear both exchange buffers (words that could carry a
-      // reused tag). Every earlier sLSTM launch is ordered before this point:
-      // this stream's by stream order, the other group's by the wait above.
-      HK_CHECK_HIP(hipMemsetAsync(e.d_xch, 0, (size_t)e.max_rows * H * 8, s));
-      HK_CHECK_HIP(hipMemsetAsync(e.d_xch2, 0, (size_t)e.max_rows * H * 8, s));
-      e.xch_tag = 1;
+    // Each exchange buffer has its own tag sequence and is used by one
+    // group, on one stream.
+    unsigned int& tag = e.xch_tag[xch == e.d_xch2 ? 1 : 0];
+    if (++tag == 0) {
+      // Tags wrapped: clear this buffer (words that could carry a reused
+      // tag). Every earlier launch on it is ordered before this point by
+      // stream order.
+      HK_CHECK_HIP(hipMemsetAsync(xch, 0, (size_t)e.max_rows * H * 8, s));
+      tag = 1;
     }
     HK_TRY(timed(e, 3, s, [&] {
       return slstm_persist(r, g.act_dev, (int)act.size(), w.GIN, H, d.nh_s,
                            F32(e, kXLSTM, l, X_S_ST_W), F32(e, kXLSTM, l, X_S_ST_B), st[XS_S_H],
-                           st[XS_S_C], st[XS_S_N], st[XS_S_M], w.SY, xch, e.xch_tag, e.d_err,
+                           st[XS_S_C], st[XS_S_N], st[XS_S_M], w.SY, xch, tag, e.d_err,
                            (l == 0 && xch == e.d_xch) ? e.d_trace : nullptr, s);
     }));
     if (ord.rec) HK_CHECK_HIP(hipEventRecord(ord.rec, s));
@@ -872,9 +879,12 @@ int run_towers(Engine& e, const Group& all, const Group& g1, const Group* g2, hi
   if (g2) HK_TRY(tower_head(e, kXLSTM, w2, *g2, e.side[0]));
   for (int l = 0; l < e.d.D; ++l) {
     if (g2) {
-      SlOrder o2{l > 0 ? e.sl_ev[0][l - 1] : nullptr, e.sl_ev[1][l]};
+      // The groups' persistent sLSTM launches run side by side when two fit
+      // on the device at once, else they alternate layer by layer.
+      const bool alt = !e.sl_overlap;
+      SlOrder o2{alt && l > 0 ? e.sl_ev[0][l - 1] : nullptr, alt ? e.sl_ev[1][l] : nullptr};
       HK_TRY(tower_layer(e, kXLSTM, w2, *g2, l, e.d_xch2, o2, e.side[0]));
-      SlOrder o1{e.sl_ev[1][l], e.sl_ev[0][l]};
+      SlOrder o1{alt ? e.sl_ev[1][l] : nullptr, alt ? e.sl_ev[0][l] : nullptr};
       HK_TRY(tower_layer(e, kXLSTM, w1, g1, l, e.d_xch, o1, s));
     } else {
       HK_TRY(tower_layer(e, kXLSTM, w1, g1, l, e.d_xch, SlOrder{}, s));

@@ -131,6 +131,10 @@ int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* 
                   float* c_state, float* n_state, float* m_state, float* y,
                   unsigned long long* xch, unsigned int tag, int* err, uint64_t* trace,
                   hipStream_t s);
+// Whether two persistent launches (each at most max_runs runs over
+// max_rounds steps) can be co-resident at once, so that two run groups'
+// recurrences may overlap.
+int slstm_persist_pair_fits(int hidden, int heads, int max_runs, int max_rounds, bool* ok);
 // After the last round: h_state[slot] = y[last row of the run].
 int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipStream_t s);
 

@@ -909,6 +909,37 @@ int launch_persist(const SlstmPersistArgs& a, size_t smem, hipStream_t s) {
   return HK_OK;
 }
 
+// LDS bytes of a persistent launch over n_runs runs and n_rounds steps.
+size_t persist_smem(int hs, int n_runs, int n_rounds) {
+  return (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float) +
+         (size_t)persist_meta_ints(n_runs, n_rounds) * sizeof(int);
+}
+
+template <int HS>
+int persist_pair_fits(size_t smem, int heads, bool* ok) {
+  int dev = 0, cus = 0, per_cu = 0;
+  HK_CHECK_HIP(hipGetDevice(&dev));
+  HK_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  HK_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, slstm_persist_kernel<HS>,
+                                                            kPersistThreads, smem));
+  *ok = 2LL * heads * (HS / 16) <= (int64_t)cus * per_cu;
+  return HK_OK;
+}
+
+int slstm_persist_pair_fits(int hidden, int heads, int max_runs, int max_rounds, bool* ok) {
+  *ok = false;
+  if (!slstm_persist_supported(hidden, heads)) return HK_OK;
+  const int hs = hidden / heads;
+  const size_t smem = persist_smem(hs, max_runs, max_rounds);
+  switch (hs) {
+    case 32: return persist_pair_fits<32>(smem, heads, ok);
+    case 64: return persist_pair_fits<64>(smem, heads, ok);
+    case 128: return persist_pair_fits<128>(smem, heads, ok);
+    case 256: return persist_pair_fits<256>(smem, heads, ok);
+    default: return persist_pair_fits<512>(smem, heads, ok);
+  }
+}
+
 int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* gin, int hidden,
                   int heads, const float* w_state, const float* b_state, float* h_state,
                   float* c_state, float* n_state, float* m_state, float* y,
@@ -922,8 +953,7 @@ int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* 
   SlstmPersistArgs a{r.slot_ids, r.run_off, act_dev, n_rounds, r.n_runs, gin, hidden, heads,
                      w_state, b_state, h_state, c_state, n_state, m_state, y, xch, tag, err,
                      trace};
-  size_t smem = (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float) +
-                (size_t)persist_meta_ints(r.n_runs, n_rounds) * sizeof(int);
+  size_t smem = persist_smem(hs, r.n_runs, n_rounds);
   HK_REQUIRE(smem <= 96 * 1024, "slstm_persist: %d runs over %d steps exceed the LDS descriptor copy",
              r.n_runs, n_rounds);
   if (trace != nullptr) {
