@@ -5,10 +5,11 @@
 // 128-byte slabs (64 bf16 or 32 fp32 per row) that travel global -> LDS
 // directly (global_load_lds_dwordx4) through a ring of kStages LDS stages,
 // with one barrier per slab and counted vmcnt waits, so kStages - 2 slabs stay
-// in flight behind the one being multiplied (the memory latency is covered by
-// bytes in flight, not by occupancy: at M <= 256 there is about one
-// work-group per CU). Chunks are XOR-swizzled within a row so the 16-byte
-// fragment reads of one wave spread over the LDS banks.
+// in flight behind the one being multiplied. Three stages (48 KB) measure as
+// fast as four to six (the L2 -> LDS rate per CU, not latency, bounds a
+// slab) and let three work-groups share a CU, so launches of just over 256
+// or 512 work-groups leave no tail round. Chunks are XOR-swizzled within a
+// row so the 16-byte fragment reads of one wave spread over the LDS banks.
 //
 // The flat work-group id is remapped so that consecutive tiles (the M tiles
 // that share one slab of W) land on the same XCD and therefore the same L2:
@@ -33,7 +34,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int BM = 64;
 constexpr int BN = 64;
 #ifndef HK_GEMM_STAGES
-#define HK_GEMM_STAGES 4
+#define HK_GEMM_STAGES 3
 #endif
 constexpr int kStages = HK_GEMM_STAGES;  // LDS ring depth (16 KB per stage)
 
