@@ -253,7 +253,8 @@ def bench_cell_step(args) -> int:
         "config": {"workload": name, "batch": main_b,
                    "entry_point": "hk_mamba2_step" if c2 else "hk_mlstm_step"},
         "roofline": {
-            "kernel": "mat_scan_kernel (per-row mode, the kernel API)",
+            "kernel": ("mamba2_row_step_kernel<1>" if c2 else "hcontract_row_step_kernel<1>")
+            + " (the kernel API)",
             "bound": "hbm",
             "achieved": head["achieved_GBs"],
             "peak": HBM_PEAK_GBS,

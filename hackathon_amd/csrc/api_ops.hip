@@ -24,12 +24,60 @@ void set_error(const char* fmt, ...) {
 
 namespace {
 
+// Element at a 32-bit byte offset from a wave-uniform base (global memory
+// access with a scalar base and a vector offset).
+__device__ __forceinline__ float* at_bytes(float* base, uint32_t bytes) {
+  return reinterpret_cast<float*>(reinterpret_cast<char*>(base) + bytes);
+}
+
+// One chunk of RC state rows h0 .. h0+RC-1 of mamba2_row_step_kernel (sb,
+// xr, yo already offset to row h0). GUARD = false: every row and column of
+// the chunk exists (no predication, so the loads issue back to back).
+template <int CPL, int RC, bool GUARD>
+__device__ __forceinline__ void mamba2_chunk(float* sb, const float* xr, float* yo, int rows_left,
+                                             float a, const float (&coef)[CPL],
+                                             const float (&cw)[CPL], const bool (&cok)[CPL],
+                                             int lane, int size_c) {
+  float sv[RC][CPL], xv[RC], p[RC];
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    const bool hok = !GUARD || i < rows_left;
+    xv[i] = hok ? xr[i] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t off = 4u * (uint32_t)(i * size_c + lane + 64 * j);
+      sv[i][j] = (!GUARD || (hok && cok[j])) ? *at_bytes(sb, off) : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      sv[i][j] = a * sv[i][j] + coef[j] * xv[i];
+      acc += cw[j] * sv[i][j];
+    }
+    p[i] = acc;
+  }
+#pragma unroll
+  for (int i = 0; i < RC; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t off = 4u * (uint32_t)(i * size_c + lane + 64 * j);
+      if (!GUARD || (i < rows_left && cok[j])) *at_bytes(sb, off) = sv[i][j];
+    }
+  const float sum = transposed_wave_sum<RC>(p);  // lane i * 64 / RC holds row i
+  constexpr int kShift = RC == 16 ? 2 : RC == 8 ? 3 : RC == 4 ? 4 : RC == 2 ? 5 : 6;
+  const int r = lane >> kShift;
+  if ((lane & ((1 << kShift) - 1)) == 0 && (!GUARD || r < rows_left)) yo[r] = sum;
+}
+
 // Mamba2 step in the reference's state layout [B][heads][h][c], where c (the
 // axis y contracts over) is contiguous: one work-group per (row, head), lane
 // = column c (CPL columns per lane, so a state row is one coalesced wave
-// access), each wave 16 rows h at a time; the 16 row sums over c come out
-// of one transposed butterfly (lane 4i holds row i). Idle rows: state
-// untouched, output zero.
+// access), each wave 16 rows h at a time (full chunks unpredicated, a
+// ragged one 4 rows at a time); the row sums over c come out of one
+// transposed butterfly. Idle rows: state untouched, output zero.
 template <int CPL>
 __global__ __launch_bounds__(256) void mamba2_row_step_kernel(
     float* __restrict__ ssm, const float* __restrict__ x, const float* __restrict__ b,
@@ -38,7 +86,7 @@ __global__ __launch_bounds__(256) void mamba2_row_step_kernel(
   const int head = blockIdx.x;
   const int row = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t rh = (int64_t)row * heads + head;
   float* yo = y + rh * size_h;
   if (mask != nullptr && mask[row] == 0) {
@@ -58,34 +106,109 @@ __global__ __launch_bounds__(256) void mamba2_row_step_kernel(
   }
   float* st = ssm + rh * size_h * size_c;
   const float* xr = x + rh * size_h;
+  const bool full_c = size_c == 64 * CPL;
   for (int h0 = wave * 16; h0 < size_h; h0 += 64) {
-    float sv[16][CPL], xv[16], p[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const bool hok = h0 + i < size_h;
-      xv[i] = hok ? xr[h0 + i] : 0.0f;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j)
-        sv[i][j] = (hok && cok[j]) ? st[(int64_t)(h0 + i) * size_c + lane + 64 * j] : 0.0f;
+    float* sb = st + (int64_t)h0 * size_c;  // uniform per wave
+    if (full_c && h0 + 16 <= size_h) {
+      mamba2_chunk<CPL, 16, false>(sb, xr + h0, yo + h0, 16, a, coef, cw, cok, lane, size_c);
+    } else {
+      for (int r = 0; r < 16 && h0 + r < size_h; r += 4)
+        mamba2_chunk<CPL, 4, true>(sb + (int64_t)r * size_c, xr + h0 + r, yo + h0 + r,
+                                   size_h - h0 - r, a, coef, cw, cok, lane, size_c);
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        sv[i][j] = a * sv[i][j] + coef[j] * xv[i];
-        acc += cw[j] * sv[i][j];
-      }
-      p[i] = acc;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j)
-        if (h0 + i < size_h && cok[j]) st[(int64_t)(h0 + i) * size_c + lane + 64 * j] = sv[i][j];
-    const float sum = transposed_wave_sum<16>(p);
-    if ((lane & 3) == 0 && h0 + (lane >> 2) < size_h) yo[h0 + (lane >> 2)] = sum;
   }
+}
+
+// One chunk of RC state rows h0 .. h0+RC-1 of hcontract_row_step_kernel.
+// GUARD = false: every row and column of the chunk exists (no predication,
+// so the row scalars and the state loads issue back to back).
+template <int CPL, int RC, bool GUARD>
+__device__ __forceinline__ void hcontract_chunk(float* sb, const float* bh, const float* wh,
+                                                int rows_left, float a, float sc,
+                                                const float (&g)[CPL], const bool (&cok)[CPL],
+                                                float (&acc)[CPL], int lane, int size_k) {
+  float sv[RC][CPL], bb[RC], ww[RC];
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    const bool hok = !GUARD || i < rows_left;
+    bb[i] = hok ? sc * bh[i] : 0.0f;  // (scale * beta): the reference's association
+    ww[i] = hok ? wh[i] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t off = 4u * (uint32_t)(i * size_k + lane + 64 * j);
+      sv[i][j] = (!GUARD || (hok && cok[j])) ? *at_bytes(sb, off) : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RC; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      sv[i][j] = a * sv[i][j] + bb[i] * g[j];
+      acc[j] += ww[i] * sv[i][j];
+    }
+#pragma unroll
+  for (int i = 0; i < RC; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t off = 4u * (uint32_t)(i * size_k + lane + 64 * j);
+      if (!GUARD || (i < rows_left && cok[j])) *at_bytes(sb, off) = sv[i][j];
+    }
+}
+
+// One step of S <- alpha S + (scale beta) (x) gamma, out_k = sum_h w_h
+// S_new[h, k] on the reference's [B][heads][h][k] layout (k contiguous:
+// mlstm_step, retnet_step). One work-group per (row, head); lane = column k
+// (CPL columns per lane); wave v takes chunks of RC = 16 / CPL rows, 4 RC
+// apart, starting at row v RC, the chunk's 16 state values per lane loaded
+// together. The four waves' column sums meet once in LDS, added in wave
+// order. Idle rows: state untouched, output zero.
+template <int CPL, int RC = 16 / CPL>
+__global__ __launch_bounds__(256) void hcontract_row_step_kernel(
+    float* __restrict__ S, const float* __restrict__ alpha, int64_t alpha_head_stride,
+    int64_t alpha_row_stride, const float* __restrict__ scale, const float* __restrict__ beta,
+    const float* __restrict__ gamma, const float* __restrict__ w, const uint8_t* __restrict__ mask,
+    float* __restrict__ out, int heads, int size_h, int size_k) {
+  __shared__ float red[4][64 * CPL];
+  const int head = blockIdx.x;
+  const int row = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t rh = (int64_t)row * heads + head;
+  float* o = out + rh * size_k;
+  if (mask != nullptr && mask[row] == 0) {
+    for (int k = threadIdx.x; k < size_k; k += blockDim.x) o[k] = 0.0f;
+    return;
+  }
+  const float a = alpha[(int64_t)row * alpha_row_stride + (int64_t)head * alpha_head_stride];
+  const float sc = scale ? scale[rh] : 1.0f;
+  float g[CPL], acc[CPL];
+  bool cok[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    cok[j] = c < size_k;
+    g[j] = cok[j] ? gamma[rh * size_k + c] : 0.0f;
+    acc[j] = 0.0f;
+  }
+  float* st = S + rh * size_h * size_k;
+  const float* bh = beta + rh * size_h;
+  const float* wh = w + rh * size_h;
+  const bool full_k = size_k == 64 * CPL;
+  for (int h0 = wave * RC; h0 < size_h; h0 += 4 * RC) {
+    float* sb = st + (int64_t)h0 * size_k;  // uniform per wave
+    if (full_k && h0 + RC <= size_h) {
+      hcontract_chunk<CPL, RC, false>(sb, bh + h0, wh + h0, RC, a, sc, g, cok, acc, lane, size_k);
+    } else {  // ragged chunk: 4 rows at a time (keeps the register count of the full path)
+      for (int r = 0; r < RC && h0 + r < size_h; r += 4)
+        hcontract_chunk<CPL, 4, true>(sb + (int64_t)r * size_k, bh + h0 + r, wh + h0 + r,
+                                      size_h - h0 - r, a, sc, g, cok, acc, lane, size_k);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) red[wave][lane + 64 * j] = acc[j];
+  lds_barrier();
+  for (int k = threadIdx.x; k < size_k; k += blockDim.x)
+    o[k] = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
 }
 
 // Depthwise causal conv step in the reference's layout: state [B][C][K-1]
@@ -196,6 +319,31 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
+int hcontract_row_step(float* S, const float* alpha, int64_t alpha_head_stride,
+                       int64_t alpha_row_stride, const float* scale, const float* beta,
+                       const float* gamma, const float* w, const uint8_t* mask, float* out,
+                       int batch, int heads, int size_h, int size_k, hipStream_t s) {
+  const dim3 grid(heads, batch), block(256);
+#define HK_HC(C)                                                                           \
+  hipLaunchKernelGGL(hcontract_row_step_kernel<C>, grid, block, 0, s, S, alpha,            \
+                     alpha_head_stride, alpha_row_stride, scale, beta, gamma, w, mask, out, \
+                     heads, size_h, size_k)
+  if (size_k <= 64) {
+    HK_HC(1);
+  } else if (size_k <= 128) {
+    HK_HC(2);
+  } else {
+    HK_HC(4);
+  }
+#undef HK_HC
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+namespace {
+
+}  // namespace
+
 }  // namespace hk
 
 extern "C" {
@@ -209,6 +357,11 @@ int hk_mlstm_step(float* cell, const float* q, const float* k, const float* v,
                   int batch, int heads, int size_h, int size_k, void* stream) {
   HK_REQUIRE(batch >= 0 && heads > 0 && size_h > 0 && size_k > 0,
              "hk_mlstm_step: bad shape B=%d n=%d h=%d k=%d", batch, heads, size_h, size_k);
+  if (batch == 0) return HK_OK;
+  if (size_k <= 256 && batch <= 65535 && heads <= 65535) {
+    return hk::hcontract_row_step(cell, f_gate, 1, heads, i_gate, k, v, q, mask, out, batch,
+                                  heads, size_h, size_k, (hipStream_t)stream);
+  }
   hk::MatScanDesc d;
   d.state = cell;
   d.rows = size_h;
@@ -237,6 +390,12 @@ int hk_retnet_step(float* state, const float* k_rope, const float* v, const floa
                    int size_h, int size_k, void* stream) {
   HK_REQUIRE(batch >= 0 && heads > 0 && size_h > 0 && size_k > 0,
              "hk_retnet_step: bad shape B=%d n=%d h=%d k=%d", batch, heads, size_h, size_k);
+  if (batch == 0) return HK_OK;
+  if (size_k <= 256 && batch <= 65535 && heads <= 65535) {
+    // one decay per head, shared by every row
+    return hk::hcontract_row_step(state, decay, 1, 0, nullptr, k_rope, v, q_scaled, mask, out,
+                                  batch, heads, size_h, size_k, (hipStream_t)stream);
+  }
   hk::MatScanDesc d;
   d.state = state;
   d.rows = size_h;
