@@ -584,7 +584,8 @@ def main() -> int:
         "p99_us": float(np.percentile(lat_us, 99)),
         "roofline": {
             "kernel": "mat_scan_kernel, mLSTM cell launches (8 heads x 512x512 fp32 state): "
-                      "<64, 8, 1, true, false> whole tiles, <32, 4, 1, true, true> 128-row parts",
+                      "<64, 8, 1, true, false, true> whole tiles, <32, 4, 1, true, true, true> "
+                      "128-row parts",
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,

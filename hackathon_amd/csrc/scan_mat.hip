@@ -17,6 +17,15 @@ namespace {
 
 constexpr int kSteps = 8;  // steps whose row vectors are staged per LDS block
 
+// Raw buffer resource over `bytes` bytes from `base` (gfx9 word 3: 32-bit
+// data format, no stride, no swizzle). A buffer access takes the row offset
+// as a scalar operand and the lane's column offset as its one vector operand,
+// and one past `bytes` reads zero and drops stores instead of faulting.
+constexpr int kBufWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, kBufWord3);
+}
+
 // NW waves split the tile's rows (RPW each); every lane owns VW adjacent
 // columns, so a work-group covers 64*VW columns and each wave instruction
 // moves 256*VW contiguous bytes of a state row.
@@ -24,8 +33,10 @@ constexpr int kSteps = 8;  // steps whose row vectors are staged per LDS block
 // SIMD) so that two work-groups share a CU: one streams its state tile in or
 // out while the other computes.
 // SPLIT: the launch splits tile rows (row_parts > 1); without it the
-// row-part arithmetic folds away.
-template <int RPW, int NW, int VW, bool VEC, bool SPLIT>
+// row-part arithmetic folds away. FULL: every wave's slice of every tile
+// exists (part rows = NW * RPW, whole column tiles), so the tile moves
+// without predication.
+template <int RPW, int NW, int VW, bool VEC, bool SPLIT, bool FULL>
 __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_scan_kernel(
     MatScanDesc d) {
   constexpr int kRows = NW * RPW;
@@ -94,19 +105,42 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
   const uint32_t rstride = (uint32_t)d.row_stride;
   const uint32_t off0 = (uint32_t)colv * (uint32_t)d.col_stride + (uint32_t)rbase * rstride;
   const int rlim = prows - rbase;  // rows of this wave's slice that exist
+  // FULL: the tile moves without predication through a buffer resource on
+  // the wave's first row, row i at scalar offset i * row bytes, the lane's
+  // columns at one vector offset, so the RPW loads issue back to back and
+  // hold no per-row address registers. The resource spans exactly the slice.
+  constexpr bool full = FULL;
+  const int rsb = 4 * (int)d.row_stride;  // row bytes
+  const int lane_b = 4 * colv * (int)d.col_stride;
+  const __amdgpu_buffer_rsrc_t rs =
+      tile_rsrc(tbase + (int64_t)rbase * d.row_stride,
+                4u * (uint32_t)((RPW - 1) * d.row_stride + (int64_t)(col0 + CW - 1) * d.col_stride + 1));
   float s[RPW][VW];
+  if constexpr (full) {
 #pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    const uint32_t o = off0 + (uint32_t)i * rstride;
-    if constexpr (VW == 2) {
-      float2 v2 = make_float2(0.0f, 0.0f);
-      if (cok[0] && cok[1] && i < rlim) v2 = *reinterpret_cast<const float2*>(tbase + o);
-      s[i][0] = v2.x;
-      s[i][1] = v2.y;
-    } else {
+    for (int i = 0; i < RPW; ++i) {
+      if constexpr (VW == 2) {  // unit column stride
+        const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(rs, lane_b, i * rsb, 0);
+        s[i][0] = __builtin_bit_cast(float, v2[0]);
+        s[i][1] = __builtin_bit_cast(float, v2[1]);
+      } else {
+        s[i][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_b, i * rsb, 0));
+      }
+    }
+  } else {
 #pragma unroll
-      for (int v = 0; v < VW; ++v)
-        s[i][v] = (cok[v] && i < rlim) ? tbase[o + (uint32_t)v * (uint32_t)d.col_stride] : 0.0f;
+    for (int i = 0; i < RPW; ++i) {
+      const uint32_t o = off0 + (uint32_t)i * rstride;
+      if constexpr (VW == 2) {
+        float2 v2 = make_float2(0.0f, 0.0f);
+        if (cok[0] && cok[1] && i < rlim) v2 = *reinterpret_cast<const float2*>(tbase + o);
+        s[i][0] = v2.x;
+        s[i][1] = v2.y;
+      } else {
+#pragma unroll
+        for (int v = 0; v < VW; ++v)
+          s[i][v] = (cok[v] && i < rlim) ? tbase[o + (uint32_t)v * (uint32_t)d.col_stride] : 0.0f;
+      }
     }
   }
 
@@ -281,6 +315,21 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
     return;
   }
 
+  if constexpr (full) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      if constexpr (VW == 2) {
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v2 = {__builtin_bit_cast(unsigned int, s[i][0]),
+                          __builtin_bit_cast(unsigned int, s[i][1])};
+        __builtin_amdgcn_raw_buffer_store_b64(v2, rs, lane_b, i * rsb, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, s[i][0]), rs, lane_b,
+                                              i * rsb, 0);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const uint32_t o = off0 + (uint32_t)i * rstride;
@@ -410,8 +459,8 @@ int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
                                 !d.per_row && d.log_hdr && d.log_b && d.log_g),
              "mat_scan: bad write-back log");
   const int prows = d.rows / d.row_parts;
-  HK_REQUIRE((int64_t)d.rows * d.row_stride + (int64_t)d.cols * d.col_stride < (1LL << 32),
-             "mat_scan: tile too large for 32-bit offsets");
+  HK_REQUIRE((int64_t)d.rows * d.row_stride + (int64_t)d.cols * d.col_stride < (1LL << 30),
+             "mat_scan: tile too large for 32-bit byte offsets");
   if (d.n_runs == 0) return HK_OK;
   HK_REQUIRE(d.n_runs <= 65535, "mat_scan: at most 65535 runs per launch");
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -424,15 +473,22 @@ int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
   const bool wide = prows > 128 && d.cols % 128 == 0 && d.col_stride == 1 &&
                     d.row_stride % 2 == 0 && d.head_stride % 2 == 0 && d.slot_stride % 2 == 0 &&
                     (reinterpret_cast<uintptr_t>(d.state) & 7) == 0;
-#define HK_SCAN_LAUNCH_S(R, NW, VW, SP)                                                     \
+#define HK_SCAN_LAUNCH_F(R, NW, VW, SP, FU)                                                \
   {                                                                                          \
     dim3 grid((d.cols + 64 * VW - 1) / (64 * VW), d.heads * d.row_parts, d.n_runs);          \
     if (vec)                                                                                 \
-      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, true, SP>), grid, dim3(64 * NW), 0, stream, \
-                         d);                                                                 \
-    else                                                                                     \
-      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, false, SP>), grid, dim3(64 * NW), 0,      \
+      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, true, SP, FU>), grid, dim3(64 * NW), 0,   \
                          stream, d);                                                         \
+    else                                                                                     \
+      hipLaunchKernelGGL((mat_scan_kernel<R, NW, VW, false, SP, FU>), grid, dim3(64 * NW), 0,  \
+                         stream, d);                                                         \
+  }
+#define HK_SCAN_LAUNCH_S(R, NW, VW, SP)                                   \
+  {                                                                        \
+    if (prows == R * NW && d.cols % (64 * VW) == 0)                        \
+      HK_SCAN_LAUNCH_F(R, NW, VW, SP, true)                                \
+    else                                                                   \
+      HK_SCAN_LAUNCH_F(R, NW, VW, SP, false)                               \
   }
 #define HK_SCAN_LAUNCH(R, NW, VW)                              \
   {                                                            \
@@ -454,6 +510,7 @@ int launch_mat_scan(const MatScanDesc& d, hipStream_t stream) {
   }
 #undef HK_SCAN_LAUNCH
 #undef HK_SCAN_LAUNCH_S
+#undef HK_SCAN_LAUNCH_F
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
