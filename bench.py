@@ -440,7 +440,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the path shards by symbol with no inter-GPU "
-              "traffic per tick, and this build runs on a single MI355X; use --gpus 1.",
+              "traffic per tick, and the engine runs on a single MI355X; use --gpus 1.",
               file=sys.stderr)
         return 2
 
