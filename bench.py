@@ -148,6 +148,53 @@ def _stream_handle(torch, dev):
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def isolated_mlstm_scan(torch, dev, batch: int = 112, calls: int = 20) -> dict:
+    """The tick's whole-tile mLSTM scan instance on its own: hk_mlstm_step at
+    8 heads x 512 x 512 runs mat_scan_kernel<64, 8, 1, true, false, true> in
+    per-row mode (one step per row, the state read and written once per
+    call), here over `batch` rows (about a tick's distinct symbols), timed
+    with HIP events on the stream it is launched on."""
+    from hackathon_amd import _lib
+
+    lib = _lib.lib()
+    heads, sh, sk = 8, 512, 512
+    g = torch.Generator(device=dev).manual_seed(1)
+    state = torch.randn(batch, heads, sh, sk, device=dev, generator=g) * 0.01
+    q = torch.randn(batch, heads, sh, device=dev, generator=g) / 32
+    k = torch.randn(batch, heads, sh, device=dev, generator=g) / 32
+    v = torch.randn(batch, heads, sk, device=dev, generator=g)
+    ig = torch.rand(batch, heads, device=dev, generator=g)
+    fg = torch.rand(batch, heads, device=dev, generator=g)
+    out = torch.empty(batch, heads, sk, device=dev)
+    stream = _stream_handle(torch, dev)
+    args = (state.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), ig.data_ptr(),
+            fg.data_ptr(), None, out.data_ptr(), batch, heads, sh, sk, stream)
+
+    def go(n):
+        for _ in range(n):
+            if lib.hk_mlstm_step(*args) != 0:
+                raise RuntimeError(lib.hk_last_error().decode())
+
+    go(3)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    go(calls)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / calls
+    assert torch.isfinite(out).all()
+    # state r+w, q, k, v, i, f, out
+    b = 4.0 * (2 * batch * heads * sh * sk + 2 * batch * heads * sh + 2 * batch * heads * sk +
+               2 * batch * heads)
+    del state
+    torch.cuda.empty_cache()
+    return {"kernel": "mat_scan_kernel<64, 8, 1, true, false, true> alone (hk_mlstm_step, "
+                      "8 heads x 512 x 512, one step per row)",
+            "batch": batch, "us_per_launch": us, "algorithmic_bytes_per_launch": b,
+            "achieved": b / us / 1e3, "frac": b / us / 1e3 / HBM_PEAK_GBS}
+
+
 def bench_cell_step(args) -> int:
     """C2 (Mamba2 step, B=256, 8 heads x headdim 64, d_state 64, 128 steps from
     a zero state) or C3 (mLSTM step, B=1024, 4 heads x 64 x 64, 256 steps from
@@ -596,6 +643,7 @@ def main() -> int:
             "traffic_source": "rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated: "
                               "profiles/mat_scan_mlstm_1024sym_hbm_counters.txt",
             "algorithmic_bytes_per_launch": per_launch_bytes,
+            "isolated": isolated_mlstm_scan(torch, dev),
         },
         "kernels": kernels,
     }
