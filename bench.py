@@ -468,12 +468,103 @@ def bench_c1(args) -> int:
     return 0
 
 
+def bench_client(args) -> int:
+    """The serving path end to end on C4's configuration (1024 symbols,
+    default dims, bf16 CastLinear weights, 256 Zipf(1.1) requests per batch):
+    NnInferenceClient.process_batch on dicts of PendingRequest objects (the
+    reference's interface, example_model.py:769-905) and process_arrays on
+    flat arrays, wall-clock per call, host packing, pinned staging, the
+    PCIe copies and the tick included. Also times the host packing of the
+    same batches alone: hk_pack_tick against the per-round Python loops it
+    replaces."""
+    import torch
+
+    from hackathon_amd import spec, weights
+    from hackathon_amd.client import NnInferenceClient, PendingRequest
+    from hackathon_amd.engine import pack_runs, pack_tick
+
+    cfg = spec.DEFAULT
+    K, W = args.steps, args.warmup
+    nf = cfg.num_features
+    client = NnInferenceClient(args.symbols, config=cfg, weights=weights.generate(cfg, 0),
+                               linear_dtype="bf16", max_rows=max(1024, args.symbols))
+    ticks = zipf_ticks(W + K, args.symbols, args.batch, 1.1, seed=0)
+    rng = np.random.default_rng(1)
+    batches, arrays = [], []
+    uid = 0
+    for syms, counts in ticks:
+        feats = np.clip(rng.standard_normal((int(counts.sum()), nf)), -5, 5).astype(np.float32)
+        names = [f"SYM_{int(s):05d}" for s in syms]
+        d, j = {}, 0
+        for name, c in zip(names, counts):
+            d[name] = [PendingRequest(uid + j + k, name, feats[j + k].tolist()) for k in range(c)]
+            j += int(c)
+        uid += j
+        batches.append(d)
+        arrays.append((names, counts, feats))
+
+    def timed(fn, items):
+        for x in items[:W]:
+            fn(x)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for x in items[W:]:
+            fn(x)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t
+
+    reqs = float(sum(int(c.sum()) for _, c in ticks[W:]))
+    t_batch = timed(client.process_batch, batches)
+    t_arr = timed(lambda a: client.process_arrays(*a), arrays)
+
+    def python_pack(slots, lens):  # the per-round loops hk_pack_tick replaces
+        runs, order = pack_runs(slots, lens)
+        row_of_item = np.empty(len(slots), dtype=np.int64)
+        for pos, i in enumerate(order):
+            row_of_item[i] = int(runs.run_off[pos])
+        resp = []
+        for k in range(max(lens)):
+            for i in range(len(slots)):
+                if lens[i] > k:
+                    resp.append(row_of_item[i] + k)
+        return resp
+
+    pack_us = {}
+    for name, fn in (("python_loops", python_pack), ("hk_pack_tick", pack_tick)):
+        t = time.perf_counter()
+        for syms, counts in ticks:
+            fn(syms, counts)
+        pack_us[name] = 1e6 * (time.perf_counter() - t) / len(ticks)
+    line = {
+        "metric": "serving path requests/s through NnInferenceClient.process_batch",
+        "value": reqs / t_batch,
+        "unit": "requests/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": 1000.0 * t_batch / K,
+        "higher_is_better": True,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "serving path: 1024 symbols, 256 Zipf(1.1) requests per "
+                               "process_batch call, default dims",
+                   "symbols": args.symbols, "requests_per_call": args.batch},
+        "process_arrays": {"requests_per_s": reqs / t_arr, "ms_per_call": 1000.0 * t_arr / K},
+        "host_pack_us_per_call": pack_us,
+        "note": "wall clock per call: host packing, pinned H2D/D2H copies and the tick",
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=("c4", "c1", "c2", "c3", "c5"), default="c4",
+    ap.add_argument("--workload", choices=("c4", "c1", "c2", "c3", "c5", "client"),
+                    default="c4",
                     help="c4 (default): the headline ensemble tick; c1, c2, c3, c5: the other "
-                         "configurations (one JSON line each)")
+                         "configurations; client: the serving path end to end (one JSON "
+                         "line each)")
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--symbols", type=int, default=1024)
@@ -497,6 +588,8 @@ def main() -> int:
         return bench_c5(args)
     if args.workload == "c1":
         return bench_c1(args)
+    if args.workload == "client":
+        return bench_client(args)
 
     import torch
 

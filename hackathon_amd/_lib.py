@@ -47,6 +47,7 @@ _SIGNATURES = {
     "hk_rglru_step": (c_int, [c_void_p] * 5 + [c_float] + [c_void_p] * 2 + [c_int] * 2
                       + [c_void_p]),
     "hk_slstm_step": (c_int, [c_void_p] * 9 + [c_int] * 2 + [c_void_p]),
+    "hk_pack_tick": (c_int, [c_void_p] * 2 + [c_int] + [c_void_p] * 6),
 }
 
 _lib = None

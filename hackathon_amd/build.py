@@ -1,7 +1,8 @@
 """Build the gfx950 shared library `libhackathon_amd.so` in-tree with hipcc.
 
-Every `csrc/*.hip` file is compiled to an object under `_build/` (in
-parallel), then linked into `hackathon_amd/libhackathon_amd.so`. The build
+Every `csrc/*.hip` file (device and host code) and `csrc/*.cpp` file (host
+code only) is compiled to an object under `_build/` (in parallel), then
+linked into `hackathon_amd/libhackathon_amd.so`. The build
 runs on a machine without a GPU: hipcc cross-compiles for gfx950.
 """
 
@@ -46,7 +47,7 @@ def _compile(src: Path) -> Path:
 
 def build(verbose: bool = True) -> Path:
     BUILD.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if not sources:
         raise RuntimeError(f"no sources under {CSRC}")
     workers = min(len(sources), max(1, (os.cpu_count() or 2)))

@@ -30,7 +30,7 @@ from typing import Dict, List
 import numpy as np
 import torch
 
-from .engine import Engine, pack_runs
+from .engine import Engine, pack_tick
 from .spec import DEFAULT, ModelConfig
 
 
@@ -159,23 +159,47 @@ class NnInferenceClient:
     def _run_items(self, items, all_ids, all_preds):
         """One engine tick over (slot, requests) pairs; appends the answers
         round by round."""
-        lengths = [len(r) for _, r in items]
-        runs, order = pack_runs([s for s, _ in items], lengths)
+        flat = [q for _, reqs in items for q in reqs]
+        feats = np.asarray([q.features for q in flat], dtype=np.float32)
+        runs, req_row, resp_req = pack_tick([s for s, _ in items], [len(r) for _, r in items])
+        preds = self._tick_rows(runs, req_row, feats)
+        all_ids.extend(flat[j].unique_id for j in resp_req)
+        all_preds.extend(preds[resp_req].tolist())
+
+    def _tick_rows(self, runs, rows, feats):
+        """One engine tick over packed runs: feats[j] goes to row rows[j]
+        (pinned staging, one H2D copy), and the predictions come back in the
+        same order as float64 [len(rows), 4] (one D2H copy)."""
         n = runs.n_rows
-        feats = self._feat_host.numpy()
-        row_of_item = np.empty(len(items), dtype=np.int64)
-        for pos, i in enumerate(order):
-            r0 = int(runs.run_off[pos])
-            row_of_item[i] = r0
-            reqs = items[i][1]
-            feats[r0:r0 + len(reqs)] = np.asarray([q.features for q in reqs], dtype=np.float32)
+        self._feat_host.numpy()[rows] = feats
         self._feat_dev[:n].copy_(self._feat_host[:n], non_blocking=True)
         self.engine.tick(runs, self._feat_dev[:n], self._preds_dev[:n])
         self._preds_host[:n].copy_(self._preds_dev[:n], non_blocking=True)
         self.engine.check()  # synchronises; raises if an in-kernel barrier timed out
-        preds = self._preds_host[:n].numpy().astype(float)
-        for k in range(max(lengths)):
-            for i, (_, reqs) in enumerate(items):
-                if len(reqs) > k:
-                    all_ids.append(reqs[k].unique_id)
-                    all_preds.append(preds[row_of_item[i] + k].tolist())
+        return self._preds_host[:n].numpy()[rows].astype(np.float64)
+
+    def process_arrays(self, symbols, counts, features):
+        """process_batch for callers holding flat arrays: `symbols` in dict
+        order with `counts[i]` requests each, `features` [sum(counts),
+        num_features] float32 with each symbol's requests together, in
+        order. Returns (resp_req, predictions): the request index answered at
+        each response position (the reference's order) and a float64
+        [n_req, 4] array in that order. Same slot assignment and zero
+        answers as process_batch; at most max_rows slotted requests."""
+        counts = np.asarray(counts, dtype=np.int64)
+        feats = np.ascontiguousarray(features, dtype=np.float32)
+        if feats.shape != (int(counts.sum()), self.num_features):
+            raise ValueError(f"features {feats.shape} do not match counts (sum {counts.sum()})")
+        slots = np.full(len(counts), -1, dtype=np.int32)
+        for i, (sym, c) in enumerate(zip(symbols, counts)):
+            if c > 0:
+                row = self._row_for(sym)
+                slots[i] = -1 if row is None else row
+        runs, req_row, resp_req = pack_tick(slots, counts)
+        if runs.n_rows > self.engine.max_rows:
+            raise ValueError(f"process_arrays: more than {self.engine.max_rows} slotted requests")
+        out = np.zeros((len(req_row), self.num_outputs), dtype=np.float64)
+        if runs.n_rows:
+            sel = np.flatnonzero(req_row >= 0)
+            out[sel] = self._tick_rows(runs, req_row[sel], feats[sel])
+        return resp_req, out[resp_req]

@@ -350,7 +350,7 @@ extern "C" {
 
 const char* hk_last_error(void) { return hk::g_last_error.c_str(); }
 
-int hk_version(void) { return 1; }
+int hk_version(void) { return 2; }
 
 int hk_mlstm_step(float* cell, const float* q, const float* k, const float* v,
                   const float* i_gate, const float* f_gate, const uint8_t* mask, float* out,

@@ -135,6 +135,33 @@ def pack_runs(slots, lengths) -> tuple[Runs, np.ndarray]:
     return Runs(np.ascontiguousarray(slot_ids), run_off), order
 
 
+def pack_tick(item_slots, item_lens):
+    """Native packing of one process_batch call (hk_pack_tick; the loops of
+    example_model.py:819-905). Items are the batch's symbols in dict order,
+    slot -1 meaning "no slot" (answered with zeros). Returns the runs for
+    Engine.tick, `req_row` (each request's row in the tick, -1 if unslotted;
+    requests numbered item by item) and `resp_req` (the request answered at
+    each response position, in the reference's order)."""
+    slots = np.ascontiguousarray(item_slots, dtype=np.int32)
+    lens = np.ascontiguousarray(item_lens, dtype=np.int32)
+    n_items = len(slots)
+    if len(lens) != n_items:
+        raise ValueError("pack_tick: item_slots and item_lens differ in length")
+    n_req = int(lens.sum(dtype=np.int64)) if n_items else 0
+    slot_ids = np.empty(max(n_items, 1), dtype=np.int32)
+    run_off = np.empty(n_items + 1, dtype=np.int32)
+    req_row = np.empty(max(n_req, 1), dtype=np.int32)
+    resp_req = np.empty(max(n_req, 1), dtype=np.int32)
+    n_runs = ctypes.c_int(0)
+    n_rows = ctypes.c_int(0)
+    _lib.check(_lib.lib().hk_pack_tick(
+        slots.ctypes.data, lens.ctypes.data, n_items, slot_ids.ctypes.data, run_off.ctypes.data,
+        req_row.ctypes.data, resp_req.ctypes.data, ctypes.byref(n_runs), ctypes.byref(n_rows)),
+        "hk_pack_tick")
+    runs = Runs(slot_ids[:n_runs.value].copy(), run_off[:n_runs.value + 1].copy())
+    return runs, req_row[:n_req], resp_req[:n_req]
+
+
 class Engine:
     def __init__(
         self,

@@ -102,6 +102,23 @@ int hk_slstm_step(float* c_state, float* n_state, float* m_state, const float* i
                   const float* f_pre, const float* z_pre, const float* o_pre,
                   const uint8_t* mask, float* y, int batch, int width, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Host-side tick packing (host memory, no GPU).
+ * Replaces the per-round loops of process_batch (example_model.py:819-905).
+ * ------------------------------------------------------------------------- */
+
+/* Items = the batch's symbols in dict order; item i has item_len[i] requests
+ * (numbered item by item) and slot item_slot[i] (-1 = no slot: answered with
+ * zeros, example_model.py:826-839). Writes the runs for hk_engine_tick
+ * (slot_ids[n_runs], run_off[n_runs+1]: one per slotted item with requests,
+ * by non-increasing length, ties in item order), req_row[n_req] (each
+ * request's row, -1 if unslotted) and resp_req[n_req] (the request answered
+ * at each response position: unslotted items' requests first, then round by
+ * round, items in dict order within a round, example_model.py:881-899).
+ * Slots must be distinct. Arrays are host memory; slot_ids and run_off hold
+ * at least n_items (+1) entries. */
+int hk_pack_tick(const int* item_slot, const int* item_len, int n_items, int* slot_ids,
+                 int* run_off, int* req_row, int* resp_req, int* n_runs_out, int* n_rows_out);
 
 /* ---------------------------------------------------------------------------
  * Deterministic parameter initialisation (host, no GPU).

@@ -62,3 +62,26 @@ class OracleClient:
                 ids.append(r.unique_id)
                 preds.append(out[row].to(torch.float64).tolist())
         return ids, preds
+
+
+def response_order(item_slots, item_lens):
+    """The answer order of process_batch without the model
+    (example_model.py:826-839, :881-899): items are the batch's symbols in
+    dict order (slot None or -1: no row), their requests numbered item by
+    item. Returns the request index at each response position."""
+    base = np.concatenate([[0], np.cumsum(item_lens)]).astype(np.int64)
+    order, items = [], []
+    for i, (slot, n) in enumerate(zip(item_slots, item_lens)):
+        if n == 0:
+            continue
+        if slot is None or slot < 0:
+            order.extend(range(base[i], base[i] + n))
+            continue
+        items.append(i)
+    if not items:
+        return order
+    for k in range(max(item_lens[i] for i in items)):
+        for i in items:
+            if item_lens[i] > k:
+                order.append(base[i] + k)
+    return order

@@ -110,6 +110,35 @@ def test_process_batch_matches_reference_rounds_fp32(dev, small_params):
     eng.close()
 
 
+def test_process_arrays_matches_reference_rounds_fp32(dev, small_params):
+    """process_arrays (flat arrays, packing by hk_pack_tick) answers like the
+    oracle's literal process_batch: same order, predictions, zero answers
+    past capacity."""
+    from hackathon_amd.client import NnInferenceClient
+
+    cfg = spec.SMALL
+    capacity = 5
+    eng = _engine(cfg, small_params, capacity=capacity, max_rows=64)
+    client = NnInferenceClient(capacity, engine=eng)
+    oracle = OracleClient(om.Params(small_params), cfg, capacity)
+    rng = np.random.default_rng(11)
+    symbols = [f"SYM_{i:03d}" for i in range(7)]  # 7 symbols > 5 slots: overflow path
+    uid = 0
+    for batch in range(4):
+        reqs = _requests(rng, symbols, 40, uid, cfg.num_features)
+        uid += 40
+        names = list(reqs)
+        flat = [r for s in names for r in reqs[s]]
+        feats = np.asarray([r.features for r in flat], dtype=np.float32)
+        resp, preds = client.process_arrays(names, [len(reqs[s]) for s in names], feats)
+        want_ids, want_preds = oracle.process_batch(reqs)
+        assert [flat[j].unique_id for j in resp] == want_ids, f"batch {batch}: order differs"
+        assert client.symbol_to_idx == oracle.symbol_to_idx
+        _close(torch.tensor(preds), torch.tensor(want_preds), P_RTOL, P_ATOL,
+               f"batch {batch} preds")
+    eng.close()
+
+
 def test_long_runs_chunked_fp32(dev, small_params):
     # More requests than max_rows: split into round-major chunks.
     from hackathon_amd.client import NnInferenceClient, PendingRequest
