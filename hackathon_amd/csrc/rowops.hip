@@ -303,7 +303,11 @@ __global__ void slstm_post_kernel(const float* __restrict__ y, const float* __re
   }
 }
 
-// One wave per head (= GroupNorm group).
+// One wave per head (= GroupNorm group); U values per lane (head size <=
+// 64 U). Every operand of the head is loaded before the two reductions, so
+// the kernel waits for memory once. FULL: the head size is exactly 64 U and
+// nothing is predicated.
+template <int U, bool FULL>
 __global__ void mlstm_post_kernel(const float* __restrict__ num, int n_parts, int64_t part_stride,
                                   const float* __restrict__ den, int den_ld,
                                   const float* __restrict__ gn_w, const float* __restrict__ gn_b,
@@ -315,31 +319,42 @@ __global__ void mlstm_post_kernel(const float* __restrict__ num, int n_parts, in
   const int head = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t base = row * inner + (int64_t)head * hs;
+  const float* gate = x_gate + row * ld_gate + (int64_t)head * hs;
+  float hv[U], gw[U], gb[U], sk[U], xc[U], xg[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = lane + 64 * u;
+    const bool ok = FULL || j < hs;
+    const int c = head * hs + j;
+    hv[u] = ok ? plane_sum(num, base + j, n_parts, part_stride) : 0.0f;
+    gw[u] = ok ? gn_w[c] : 0.0f;
+    gb[u] = ok ? gn_b[c] : 0.0f;
+    sk[u] = ok ? skip_w[c] : 0.0f;
+    xc[u] = ok ? x_conv[base + j] : 0.0f;
+    xg[u] = ok ? gate[j] : 0.0f;
+  }
   const float dn = den[row * den_ld + head];
-  float hv[kHeadPostMax];  // num / den of this lane's elements
   float s = 0.0f;
 #pragma unroll
-  for (int u = 0; u < kHeadPostMax; ++u) {
-    const int j = lane + 64 * u;
-    hv[u] = j < hs ? plane_sum(num, base + j, n_parts, part_stride) / dn : 0.0f;
+  for (int u = 0; u < U; ++u) {
+    // num / den of this lane's elements; absent ones stay zero
+    hv[u] = (FULL || lane + 64 * u < hs) ? hv[u] / dn : 0.0f;
     s += hv[u];
   }
   const float mean = wave_sum(s) / (float)hs;
   float v = 0.0f;
 #pragma unroll
-  for (int u = 0; u < kHeadPostMax; ++u) {
-    const int j = lane + 64 * u;
-    const float dlt = j < hs ? hv[u] - mean : 0.0f;
+  for (int u = 0; u < U; ++u) {
+    const float dlt = (FULL || lane + 64 * u < hs) ? hv[u] - mean : 0.0f;
     v += dlt * dlt;
   }
   const float rstd = 1.0f / sqrtf(wave_sum(v) / (float)hs + 1e-5f);
 #pragma unroll
-  for (int u = 0; u < kHeadPostMax; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int j = lane + 64 * u;
-    if (j < hs) {
-      const int c = head * hs + j;
-      const float gnv = ((hv[u] - mean) * rstd) * gn_w[c] + gn_b[c];
-      const float h = (gnv + skip_w[c] * x_conv[base + j]) * silu(x_gate[row * ld_gate + c]);
+    if (FULL || j < hs) {
+      const float gnv = ((hv[u] - mean) * rstd) * gw[u] + gb[u];
+      const float h = (gnv + sk[u] * xc[u]) * silu(xg[u]);
       if (out) out[base + j] = h;
       if (out_lp) out_lp[base + j] = f32_to_bf16_bits(h);
     }
@@ -625,9 +640,23 @@ int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* 
   HK_REQUIRE(heads >= 1 && heads <= 16 && inner % heads == 0 &&
                  inner / heads <= 64 * kHeadPostMax && n_parts >= 1,
              "mlstm_post: %d heads of %d unsupported", heads, inner / std::max(heads, 1));
-  hipLaunchKernelGGL(mlstm_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, num, n_parts,
-                     part_stride, den, den_ld, gn_w, gn_b, skip_w, x_conv, x_gate, ld_gate, inner,
-                     inner / heads, out, out_lp);
+  const int hs = inner / heads;
+#define HK_POST(U, F)                                                                     \
+  hipLaunchKernelGGL((mlstm_post_kernel<U, F>), dim3(n_rows), dim3(64 * heads), 0, s, num, \
+                     n_parts, part_stride, den, den_ld, gn_w, gn_b, skip_w, x_conv, x_gate,  \
+                     ld_gate, inner, hs, out, out_lp)
+  if (hs == 512) {
+    HK_POST(8, true);
+  } else if (hs == 256) {
+    HK_POST(4, true);
+  } else if (hs == 128) {
+    HK_POST(2, true);
+  } else if (hs == 64) {
+    HK_POST(1, true);
+  } else {
+    HK_POST(kHeadPostMax, false);
+  }
+#undef HK_POST
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
