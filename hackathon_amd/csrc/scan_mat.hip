@@ -120,9 +120,10 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       if constexpr (VW == 2) {  // unit column stride
-        const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(rs, lane_b, i * rsb, 0);
-        s[i][0] = __builtin_bit_cast(float, v2[0]);
-        s[i][1] = __builtin_bit_cast(float, v2[1]);
+        // two adjacent 32-bit loads, which the compiler merges into one
+        // buffer_load_dwordx2 (its 64-bit load builtin emits a single dword)
+        s[i][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_b, i * rsb, 0));
+        s[i][1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_b + 4, i * rsb, 0));
       } else {
         s[i][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_b, i * rsb, 0));
       }
@@ -319,10 +320,10 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       if constexpr (VW == 2) {
-        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 v2 = {__builtin_bit_cast(unsigned int, s[i][0]),
-                          __builtin_bit_cast(unsigned int, s[i][1])};
-        __builtin_amdgcn_raw_buffer_store_b64(v2, rs, lane_b, i * rsb, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, s[i][0]), rs, lane_b,
+                                              i * rsb, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, s[i][1]), rs,
+                                              lane_b + 4, i * rsb, 0);
       } else {
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, s[i][0]), rs, lane_b,
                                               i * rsb, 0);

@@ -267,6 +267,31 @@ def test_default_dims_fp32_golden(dev):
     e.close()
 
 
+def test_default_dims_fp32_past_log_cap(dev):
+    """Default dims, 4 symbols, 12 steps against the oracle: past the
+    8-entry pending-update log, so matrix-state tiles are written back and
+    read again (every scan instance of the default dims, including the
+    256-row float2 tiles, on a non-zero state)."""
+    cfg = spec.DEFAULT
+    params = weights.generate(cfg, 0)
+    e = _engine(cfg, params, capacity=4, max_rows=16)
+    P32 = om.Params(params)
+    s32 = om.init_state(cfg, 4)
+    rng = np.random.default_rng(5)
+    for t in range(12):
+        x = torch.from_numpy(
+            np.clip(rng.standard_normal((4, cfg.num_features)), -5, 5).astype(np.float32))
+        got = e.forward_masked(x.to(dev), None).cpu()
+        with torch.inference_mode():
+            want, s32 = om.forward(P32, cfg, x, s32)
+        # |d| / (|ref| + 2): the default dims' fp32 RetNet scatter (module
+        # docstring) stays near 2.5e-5 of it; a wrong tile is of order 1
+        rel = float(((got.double() - want.double()).abs() / (want.double().abs() + 2)).max())
+        assert rel <= 1e-4, f"default dims step {t}: |d| / (|ref| + 2) = {rel:.3e}"
+    e.check()
+    e.close()
+
+
 def test_state_roundtrip_and_reset(dev, small_params):
     from hackathon_amd.engine import pack_runs
 

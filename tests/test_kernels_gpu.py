@@ -70,6 +70,9 @@ CASES = [
     ("mamba2", 6, (8, 16, 24)), ("mamba2", 6, (2, 64, 128)), ("mamba2", 5, (5, 40, 96)),
     # the isolated Mamba2 and mLSTM step configurations
     ("mamba2", 256, (8, 64, 64)), ("mlstm", 64, (4, 64, 64)),
+    # past 256 columns the generic scan runs: 256-row tiles of float2 columns,
+    # whole (256 rows) and partial (192 rows), on a non-zero state
+    ("retnet", 6, (2, 256, 384)), ("mlstm", 5, (2, 192, 384)),
 ]
 
 
