@@ -400,11 +400,12 @@ def bench_c1(args) -> int:
     import torch
 
     from hackathon_amd import spec, weights
-    from hackathon_amd.engine import Engine
+    from hackathon_amd.engine import Engine, Runs
 
     dev = torch.device("cuda:0")
     cfg = spec.DEFAULT
     B, steps = 4, 256
+    every_symbol = Runs(np.arange(B, dtype=np.int32), np.arange(B + 1, dtype=np.int32))
     params = weights.generate(cfg, 0)
     eng = Engine(cfg, capacity=B, max_rows=16, linear_dtype="fp32", device=dev)
     eng.load_weights(params)
@@ -417,7 +418,7 @@ def bench_c1(args) -> int:
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for t in range(steps):
-        preds.append(eng.forward_masked(x[t], None))
+        preds.append(eng.tick(every_symbol, x[t]))
     e1.record(stream)
     torch.cuda.synchronize()
     gpu_ms = e0.elapsed_time(e1) / steps

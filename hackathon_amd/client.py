@@ -23,6 +23,7 @@ can be passed in and the response serialises the same way.
 
 from __future__ import annotations
 
+import os
 import time
 from dataclasses import dataclass, field
 from typing import Dict, List
@@ -30,8 +31,24 @@ from typing import Dict, List
 import numpy as np
 import torch
 
-from .engine import Engine, pack_tick
+from .engine import LINEAR_DTYPES, Engine, pack_tick
 from .spec import DEFAULT, ModelConfig
+
+# The reference client's precision default and its override
+# (example_model.py:150-157, :306-313).
+DEFAULT_LINEAR_DTYPE = "fp16"
+
+
+def requested_linear_dtype() -> str:
+    """LINEAR_DTYPE from the environment as the reference reads it: case-
+    and space-insensitive, an unknown value falls back to the default with a
+    message (example_model.py:306-313)."""
+    requested = os.environ.get("LINEAR_DTYPE", DEFAULT_LINEAR_DTYPE).strip().lower()
+    if requested not in LINEAR_DTYPES:
+        print(f"LINEAR_DTYPE={requested!r} is not one of {sorted(LINEAR_DTYPES)}; "
+              f"falling back to {DEFAULT_LINEAR_DTYPE}")
+        requested = DEFAULT_LINEAR_DTYPE
+    return requested
 
 
 @dataclass
@@ -69,12 +86,14 @@ class NnInferenceClient:
         engine: Engine | None = None,
         config: ModelConfig = DEFAULT,
         weights: dict | None = None,
-        linear_dtype: str = "bf16",
+        linear_dtype: str | None = None,
         max_rows: int = 1024,
         device: str = "cuda:0",
         seed: int = 0,
     ):
         if engine is None:
+            if linear_dtype is None:
+                linear_dtype = requested_linear_dtype()
             engine = Engine(config, capacity=num_symbols, max_rows=max(max_rows, num_symbols),
                             linear_dtype=linear_dtype, device=device)
             if weights is None:

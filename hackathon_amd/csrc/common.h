@@ -79,6 +79,47 @@ __host__ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_bits_to_f32(f32_to_bf16_bits(f));
 }
 
+// Round-to-nearest-even fp32 -> IEEE binary16 bits, overflow to infinity
+// (torch's fp32 -> fp16 cast). Normal results: drop 13 mantissa bits with a
+// round-half-even bias, the carry stepping into the exponent. Subnormal
+// results: adding 0.5 (whose ulp is 2^-24, the fp16 subnormal step) makes
+// the fp32 adder round |f| to a multiple of 2^-24; the low bits of the sum
+// are that multiple.
+__host__ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return sign | 0x7c00u | (a > 0x7f800000u ? 0x200u : 0u);
+  if (a >= 0x477ff000u) return sign | 0x7c00u;  // >= 65520 rounds past 65504
+  if (a >= 0x38800000u) {                       // >= 2^-14: normal fp16
+    const uint32_t r = a - 0x38000000u;         // rebias the exponent (127 -> 15)
+    return sign | (uint16_t)((r + 0xfffu + ((r >> 13) & 1u)) >> 13);
+  }
+  const float t = __builtin_bit_cast(float, a) + 0.5f;
+  return sign | (uint16_t)(__builtin_bit_cast(uint32_t, t) - 0x3f000000u);
+}
+
+__host__ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) {  // zero / subnormal: m * 2^-24, exact in fp32
+    const float v = (float)m * 5.9604644775390625e-08f;
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) | sign);
+  }
+  if (e == 31) return __builtin_bit_cast(float, sign | 0x7f800000u | (m << 13));
+  return __builtin_bit_cast(float, sign | ((e + 112u) << 23) | (m << 13));
+}
+
+// The 16-bit compute formats of CastLinear (example_model.py:150-155).
+enum LpFmt : int { kLpBF16 = 0, kLpF16 = 1 };
+
+__host__ __device__ __forceinline__ uint16_t f32_to_lp_bits(float f, int fmt) {
+  return fmt == kLpF16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f);
+}
+__host__ __device__ __forceinline__ float round_lp(float f, int fmt) {
+  return fmt == kLpF16 ? f16_bits_to_f32(f32_to_f16_bits(f)) : round_bf16(f);
+}
+
 // Global-memory loads through explicit address-space-1 pointers. Pointers
 // that reach a kernel inside an argument struct are generic to the compiler,
 // which then emits flat loads (slower, and their waits also cover LDS);

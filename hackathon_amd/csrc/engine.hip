@@ -68,13 +68,13 @@ enum { KS_CONV, KS_H, KS_N };
 struct SlotDef {
   const char* name;
   int64_t numel;
-  bool lp;          // a CastLinear weight: bf16 storage in reduced-precision mode
-  bool lp_bias;     // a CastLinear bias: rounded to bf16 in reduced-precision mode
+  bool lp;          // a CastLinear weight: 16-bit storage in reduced-precision mode
+  bool lp_bias;     // a CastLinear bias: rounded to 16 bits in reduced-precision mode
 };
 
 struct Slot {
   SlotDef def{};
-  void* ptr = nullptr;   // device storage (bf16 when def.lp && lowp, else fp32)
+  void* ptr = nullptr;   // device storage (16-bit when def.lp && lowp, else fp32)
   bool bound = false;
 };
 
@@ -190,7 +190,7 @@ struct DevBuf {
   }
 };
 
-struct Act {  // an activation: fp32 copy and (reduced-precision mode) bf16 copy
+struct Act {  // an activation: fp32 copy and (reduced-precision mode) 16-bit copy
   float* f = nullptr;
   uint16_t* l = nullptr;
 };
@@ -220,7 +220,10 @@ struct TowerWS {
 struct Engine {
   Dims d{};
   int capacity = 0, max_rows = 0, max_runs = 0;
+  // CastLinear mode (example_model.py:150-157): lowp = the converted
+  // linears store and compute in lp_fmt (bf16 or fp16), else all fp32.
   bool lowp = false;
+  int lp_fmt = kLpBF16;
   std::vector<std::unique_ptr<DevBuf>> bufs;
   // slots[tower][layer+1][slot]; layer index 0 holds the tower-level slots.
   std::vector<std::vector<std::vector<Slot>>> slots;
@@ -477,9 +480,9 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
            int64_t ldl, hipStream_t s) {
   GemmArgs g;
   const bool lp = lin.w->def.lp && e.lowp;
-  g.type = lp ? GemmType::kBF16 : GemmType::kF32;
+  g.type = !lp ? GemmType::kF32 : e.lp_fmt == kLpF16 ? GemmType::kF16 : GemmType::kBF16;
   g.A = lp ? (const void*)x.l : (const void*)x.f;
-  HK_REQUIRE(g.A != nullptr, "linear %s: missing %s input", lin.w->def.name, lp ? "bf16" : "fp32");
+  HK_REQUIRE(g.A != nullptr, "linear %s: missing %s input", lin.w->def.name, lp ? "16-bit" : "fp32");
   g.lda = ldx;
   g.W = lin.w->ptr;
   g.ldw = K;
@@ -488,6 +491,7 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
   g.K = K;
   g.ep.bias = lin.b ? static_cast<const float*>(lin.b->ptr) : nullptr;
   g.ep.round_lp = lp;
+  g.ep.lp_fmt = e.lp_fmt;
   g.ep.act = act;
   g.ep.residual = residual;
   g.ep.ldr = ldr;
@@ -656,7 +660,7 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
     HK_TRY(slstm_final(r, w.SY, H, st[XS_S_H], s));
   }
   HK_TRY(slstm_post(w.SY, w.A.f, F32(e, kXLSTM, l, X_S_GN_W), F32(e, kXLSTM, l, X_S_GN_B), d.nh_s,
-                    F32(e, kXLSTM, l, X_L_NORM), n, H, w.X1, w.XN2.f, w.XN2.l, s));
+                    F32(e, kXLSTM, l, X_L_NORM), n, H, w.X1, w.XN2.f, w.XN2.l, e.lp_fmt, s));
   // mLSTM block (model/xlstm.py:298-325).
   HK_TRY(linear(e, w, w.XN2, H, {S(e, kXLSTM, l, X_L_XG_W), nullptr}, n, 2 * I, H, 0, nullptr, 0,
                 w.XMG, 2 * I, nullptr, 0, s));
@@ -700,7 +704,7 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(mlstm_post(w.NUM, m.row_parts, m.out_part_stride, w.DEN, d.nh, F32(e, kXLSTM, l, X_L_GN_W), F32(e, kXLSTM, l, X_L_GN_B),
                     F32(e, kXLSTM, l, X_L_SKIP), w.XMC, w.XMG + I, 2 * I, n, I, d.nh, w.HS.f,
-                    w.HS.l, s));
+                    w.HS.l, e.lp_fmt, s));
   HK_TRY(linear(e, w, w.HS, I, {S(e, kXLSTM, l, X_L_DOWN_W), nullptr}, n, H, I, 0, w.X1, H, w.X2,
                 H, nullptr, 0, s));
   // final_norm and the Block's residual (x = final_norm(x2) + x) are applied
@@ -743,7 +747,7 @@ int run_mamba2(Engine& e, int l, const Runs& r, hipStream_t s) {
   HK_TRY(timed_mat_scan(e, 1, m, s));
   HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(mamba2_post(w.YS, m.row_parts, m.out_part_stride, w.MXC, C, w.PROJ + C, W, F32(e, kMamba2, l, M_D),
-                     F32(e, kMamba2, l, M_NORM), n, I, d.hm, w.YN.f, w.YN.l, s));
+                     F32(e, kMamba2, l, M_NORM), n, I, d.hm, w.YN.f, w.YN.l, e.lp_fmt, s));
   HK_TRY(linear(e, w, w.YN, I, {S(e, kMamba2, l, M_OUT_W), nullptr}, n, H, I, 0, w.X.f, H, w.X.f,
                 H, nullptr, 0, s));
   return HK_OK;
@@ -779,7 +783,7 @@ int run_retnet(Engine& e, int l, const Runs& r, hipStream_t s) {
   HK_TRY(timed_mat_scan(e, 2, m, s));
   HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(retnet_post(w.O, m.row_parts, m.out_part_stride, w.QKVG + 3 * H, 4 * H, n, H, d.hs_r,
-                     w.YO.f, w.YO.l, s));
+                     w.YO.f, w.YO.l, e.lp_fmt, s));
   HK_TRY(linear(e, w, w.YO, H, {S(e, kRetNet, l, R_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f,
                 H, nullptr, 0, s));
   return HK_OK;
@@ -801,7 +805,7 @@ int run_hawk(Engine& e, int l, const Runs& r, hipStream_t s) {
   HK_TRY(block_linear(e, w, w.KXC, nullptr, 0, H, F32(e, kHawk, l, K_GATES_W), 2, d.nb_h, d.bs_h,
                       n, w.GATES, 2 * H, s));
   HK_TRY(rglru_scan(r, w.KXC, w.GATES, w.GATES + H, 2 * H, w.GRP, 2 * H, F32(e, kHawk, l, K_A),
-                    8.0f, H, st[KS_H], w.GH.f, w.GH.l, s));
+                    8.0f, H, st[KS_H], w.GH.f, w.GH.l, e.lp_fmt, s));
   HK_TRY(linear(e, w, w.GH, H, {S(e, kHawk, l, K_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f, H,
                 nullptr, 0, s));
   return HK_OK;
@@ -829,9 +833,9 @@ int tower_layer(Engine& e, int t, TowerWS& w, const Group& g, int l, unsigned lo
   if (t == kXLSTM) {
     // A = RMSNorm(x); XN = slstm.norm(A) (model/xlstm.py:314)
     HK_TRY(rms_ln_rows(w.X.f, F32(e, t, l, B_NORM1), kRmsEps, F32(e, t, l, X_S_NORM), n, H, w.A.f,
-                       w.A.l, w.XN, s));
+                       w.A.l, e.lp_fmt, w.XN, s));
   } else {
-    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM1), kRmsEps, n, H, w.A.f, H, w.A.l, H, s));
+    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM1), kRmsEps, n, H, w.A.f, H, w.A.l, e.lp_fmt, H, s));
   }
   switch (t) {
     case kXLSTM: HK_TRY(run_xlstm(e, w, l, g, xch, ord, s)); break;
@@ -842,9 +846,9 @@ int tower_layer(Engine& e, int t, TowerWS& w, const Group& g, int l, unsigned lo
   if (t == kXLSTM) {
     // x = final_norm(x2) + x (model/xlstm.py:365, inference_model.py:66); A = RMSNorm(x)
     HK_TRY(ln_res_rms_rows(w.X2, F32(e, t, l, X_F_NORM), w.X.f, F32(e, t, l, B_NORM2), kRmsEps, n,
-                           H, w.A.f, w.A.l, s));
+                           H, w.A.f, w.A.l, e.lp_fmt, s));
   } else {
-    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM2), kRmsEps, n, H, w.A.f, H, w.A.l, H, s));
+    HK_TRY(rmsnorm_rows(w.X.f, H, F32(e, t, l, B_NORM2), kRmsEps, n, H, w.A.f, H, w.A.l, e.lp_fmt, H, s));
   }
   HK_TRY(linear(e, w, w.A, H, {S(e, t, l, B_FC1_W), S(e, t, l, B_FC1_B)}, n, P, H, 1, nullptr, 0,
                 w.H1.f, P, w.H1.l, P, s));
@@ -945,7 +949,7 @@ using hk::Engine;
 extern "C" {
 
 // cfg: hidden, proj, depth, heads, features, mamba_head, mamba_bc, capacity,
-//      max_rows, max_runs, lowp
+//      max_rows, max_runs, lp (0 fp32, 1 bf16, 2 fp16 CastLinear)
 int hk_engine_create(const int* cfg, int n_cfg, void** out) {
   HK_REQUIRE(cfg && out && n_cfg == 11, "hk_engine_create: expected 11 config ints");
   *out = nullptr;
@@ -961,7 +965,9 @@ int hk_engine_create(const int* cfg, int n_cfg, void** out) {
   e->capacity = cfg[7];
   e->max_rows = cfg[8];
   e->max_runs = cfg[9];
+  HK_REQUIRE(cfg[10] >= 0 && cfg[10] <= 2, "hk_engine_create: lp must be 0 (fp32), 1 (bf16) or 2 (fp16)");
   e->lowp = cfg[10] != 0;
+  e->lp_fmt = cfg[10] == 2 ? hk::kLpF16 : hk::kLpBF16;
   HK_REQUIRE(d.H > 0 && d.P > 0 && d.D > 0 && d.nh > 0 && d.F > 0 && d.hm > 0 && d.bc > 0,
              "hk_engine_create: non-positive dimension");
   HK_REQUIRE(e->capacity > 0 && e->max_rows > 0 && e->max_runs > 0,
@@ -1079,8 +1085,9 @@ int hk_engine_param_numel(void* h, int tower, int layer, int slot, int64_t* nume
 }
 
 // Synchronous: copies `numel` fp32 values from host memory into the slot,
-// converting to bf16 (weights) or rounding through bf16 (biases) when the
-// slot is a reduced-precision linear and the engine runs in that mode.
+// converting to the engine's 16-bit format (weights) or rounding through it
+// (biases) when the slot is a reduced-precision linear and the engine runs
+// in that mode.
 int hk_engine_load_param(void* h, int tower, int layer, int slot, const float* host,
                          int64_t numel) {
   HK_REQUIRE(h && host, "hk_engine_load_param: null argument");
@@ -1093,7 +1100,7 @@ int hk_engine_load_param(void* h, int tower, int layer, int slot, const float* h
     float* tmp = nullptr;
     HK_CHECK_HIP(hipMalloc(&tmp, (size_t)numel * 4));
     hipError_t err = hipMemcpy(tmp, host, (size_t)numel * 4, hipMemcpyHostToDevice);
-    int st = err == hipSuccess ? hk::to_bf16(tmp, static_cast<uint16_t*>(s->ptr), numel, nullptr)
+    int st = err == hipSuccess ? hk::to_lp(tmp, static_cast<uint16_t*>(s->ptr), numel, e.lp_fmt, nullptr)
                                : HK_ERR_HIP;
     if (st == HK_OK) err = hipDeviceSynchronize();
     (void)hipFree(tmp);
@@ -1104,7 +1111,7 @@ int hk_engine_load_param(void* h, int tower, int layer, int slot, const float* h
     if (st != HK_OK) return st;
   } else if (s->def.lp_bias && e.lowp) {
     std::vector<float> v(host, host + numel);
-    for (auto& x : v) x = hk::round_bf16(x);
+    for (auto& x : v) x = hk::round_lp(x, e.lp_fmt);
     HK_CHECK_HIP(hipMemcpy(s->ptr, v.data(), (size_t)numel * 4, hipMemcpyHostToDevice));
   } else {
     HK_CHECK_HIP(hipMemcpy(s->ptr, host, (size_t)numel * 4, hipMemcpyHostToDevice));
@@ -1342,7 +1349,7 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   all.r = hk::Runs{e.d_slots, e.d_off, n_runs, n_rows, steps};
   all.act_dev = e.d_act;
   all.act.assign(h_act, h_act + steps);
-  HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, s));
+  HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, e.lp_fmt, s));
   HK_CHECK_HIP(hipEventRecord(e.fork_ev, s));
   for (int i = 0; i < Engine::kSide; ++i) HK_CHECK_HIP(hipStreamWaitEvent(e.side[i], e.fork_ev, 0));
   if (split < n_runs) {

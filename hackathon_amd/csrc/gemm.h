@@ -1,7 +1,8 @@
 // Projection GEMMs on gfx950 matrix cores: Y[M,N] = A[M,K] . W[N,K]^T with a
-// fused epilogue. Two operand types share one kernel template:
-//   bf16 (v_mfma_f32_16x16x32_bf16) - the reduced-precision linears, output
-//        rounded to bf16 after the bias add exactly as CastLinear does
+// fused epilogue. Three operand types share one kernel template:
+//   bf16 (v_mfma_f32_16x16x32_bf16) and fp16 (v_mfma_f32_16x16x32_f16) - the
+//        reduced-precision linears, output rounded to the operand format
+//        after the bias add exactly as CastLinear does
 //        (example_model.py:92-95);
 //   fp32 (v_mfma_f32_16x16x4_f32)   - the fp32 path and the linears kept fp32
 //        (example_model.py:106), plus the fp32 BlockLinear products
@@ -12,7 +13,7 @@
 
 namespace hk {
 
-enum class GemmType { kBF16 = 0, kF32 = 1 };
+enum class GemmType { kBF16 = 0, kF32 = 1, kF16 = 2 };
 
 struct GemmEpilogue {
   const float* bias = nullptr;      // [N] (per batch: + b*c_bstride)
@@ -20,17 +21,18 @@ struct GemmEpilogue {
   int64_t ldr = 0;
   float* out = nullptr;             // fp32 result [M, ldo]
   int64_t ldo = 0;
-  uint16_t* out_lp = nullptr;       // optional bf16 copy [M, ldl]
+  uint16_t* out_lp = nullptr;       // optional 16-bit copy [M, ldl] in format lp_fmt
   int64_t ldl = 0;
-  bool round_lp = false;            // round (acc + bias) to bf16 first
+  int lp_fmt = kLpBF16;             // LpFmt of round_lp and out_lp
+  bool round_lp = false;            // round (acc + bias) to lp_fmt first
   int act = 0;                      // 0 none, 1 relu (after rounding)
 };
 
 struct GemmArgs {
   GemmType type = GemmType::kBF16;
-  const void* A = nullptr;  // [M, lda] of bf16 or fp32
+  const void* A = nullptr;  // [M, lda] of bf16, fp16 or fp32
   int64_t lda = 0;
-  const void* W = nullptr;  // [N, ldw] of bf16 or fp32
+  const void* W = nullptr;  // [N, ldw] of bf16, fp16 or fp32
   int64_t ldw = 0;
   int M = 0, N = 0, K = 0;
   // Block-diagonal batches: batch b reads A + b*a_bstride (elements), W +
@@ -56,7 +58,7 @@ struct GemmWorkspace {
   int64_t arrival_elems = 0;
 };
 
-// K must be a multiple of 64 (bf16) or 16 (fp32); lda/ldw multiples of 8 / 4.
+// K must be a multiple of 64 (bf16, fp16) or 16 (fp32); lda/ldw multiples of 8 / 4.
 int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int splits_hint = 0);
 
 }  // namespace hk

@@ -2,7 +2,7 @@
 //
 // 64x64 output tile per 256-thread work-group, 4 wave64s in a 2x2 layout,
 // each wave owning a 32x32 sub-tile = 2x2 MFMA 16x16 fragments. K advances in
-// 128-byte slabs (64 bf16 or 32 fp32 per row) that travel global -> LDS
+// 128-byte slabs (64 bf16/fp16 or 32 fp32 per row) that travel global -> LDS
 // directly (global_load_lds_dwordx4) through a ring of kStages LDS stages,
 // with one barrier per slab and counted vmcnt waits, so kStages - 2 slabs stay
 // in flight behind the one being multiplied. Three stages (48 KB) measure as
@@ -29,6 +29,7 @@ namespace hk {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 64;
@@ -42,6 +43,11 @@ template <GemmType T>
 struct Tr;
 template <>
 struct Tr<GemmType::kBF16> {
+  using E = uint16_t;
+  static constexpr int BK = 64;       // 128-byte slab rows
+};
+template <>
+struct Tr<GemmType::kF16> {
   using E = uint16_t;
   static constexpr int BK = 64;       // 128-byte slab rows
 };
@@ -251,6 +257,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
                 acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                     __builtin_bit_cast(bf16x8, fa[ii]), __builtin_bit_cast(bf16x8, fb[q]),
                     acc[ii][q], 0, 0, 0);
+          } else if constexpr (T == GemmType::kF16) {
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+              for (int q = 0; q < 2; ++q)
+                acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(halfx8, fa[ii]), __builtin_bit_cast(halfx8, fb[q]),
+                    acc[ii][q], 0, 0, 0);
           } else {
             // k-step (ks, c) of a lane in k group fk covers k = 16*ks + 4*fk
             // + c for A and B alike, so one 16-byte read feeds four MFMAs.
@@ -377,7 +391,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float v = acc[i][j][e] + bias_v[j];
-        if (ep.round_lp) v = round_bf16(v);
+        if (ep.round_lp) v = round_lp(v, ep.lp_fmt);
         if (ep.act == 1) v = fmaxf(v, 0.0f);
         outv[i][j][e] = v + res[i][j][e];
       }
@@ -393,7 +407,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
         const int m = m0 + wm * 32 + i * 16 + fk * 4 + e;
         if (m >= g.M) continue;
         if (ep.out) ep.out[(int64_t)m * ep.ldo + nc] = outv[i][j][e];
-        if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_bf16_bits(outv[i][j][e]);
+        if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_lp_bits(outv[i][j][e], ep.lp_fmt);
       }
     }
   }
@@ -407,10 +421,11 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
   HK_REQUIRE(g.M >= 0 && g.N > 0 && g.K > 0 && g.batch > 0, "gemm: bad shape M=%d N=%d K=%d",
              g.M, g.N, g.K);
   const bool narrow = g.type == GemmType::kF32 && g.K % Tr<GemmType::kF32>::BK != 0;
-  const int BK = g.type == GemmType::kBF16 ? Tr<GemmType::kBF16>::BK
-                 : narrow                  ? Tr<GemmType::kF32>::BK_NARROW
-                                           : Tr<GemmType::kF32>::BK;
-  const int align = g.type == GemmType::kBF16 ? 8 : 4;
+  const bool half = g.type != GemmType::kF32;  // bf16 or fp16 operands
+  const int BK = half     ? Tr<GemmType::kBF16>::BK
+                 : narrow ? Tr<GemmType::kF32>::BK_NARROW
+                          : Tr<GemmType::kF32>::BK;
+  const int align = half ? 8 : 4;
   HK_REQUIRE(g.K % BK == 0, "gemm: K=%d is not a multiple of %d", g.K, BK);
   HK_REQUIRE(g.lda % align == 0 && g.ldw % align == 0 && g.a_bstride % align == 0 &&
                  g.w_bstride % align == 0,
@@ -435,6 +450,10 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
   HK_REQUIRE(nwg < (1LL << 31), "gemm: grid too large");
   if (g.type == GemmType::kBF16) {
     hipLaunchKernelGGL((gemm_kernel<GemmType::kBF16, Tr<GemmType::kBF16>::BK, kStages>),
+                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, ws.arrivals, splits,
+                       tiles_m, tiles_n);
+  } else if (g.type == GemmType::kF16) {
+    hipLaunchKernelGGL((gemm_kernel<GemmType::kF16, Tr<GemmType::kF16>::BK, kStages>),
                        dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, ws.arrivals, splits,
                        tiles_m, tiles_n);
   } else if (!narrow) {

@@ -70,4 +70,14 @@ int hk_fill_uniform_host(float* dst, int64_t n, uint64_t key, float lo, float hi
   return HK_OK;
 }
 
+// Host conversion to the CastLinear 16-bit formats, with the same routine
+// the kernels use (common.h).
+int hk_to_lp_host(const float* src, uint16_t* dst, int64_t n, int fmt) {
+  HK_REQUIRE((src && dst) || n == 0, "hk_to_lp_host: null argument");
+  HK_REQUIRE(n >= 0 && (fmt == hk::kLpBF16 || fmt == hk::kLpF16),
+             "hk_to_lp_host: bad size or format %d", fmt);
+  for (int64_t i = 0; i < n; ++i) dst[i] = hk::f32_to_lp_bits(src[i], fmt);
+  return HK_OK;
+}
+
 }  // extern "C"

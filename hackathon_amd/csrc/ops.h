@@ -20,12 +20,12 @@ struct Runs {
 // ---- row kernels (rowops.hip) ---------------------------------------------
 
 // out = x * rsqrt(mean(x^2) + eps) * w (model/inference_model.py:58,60;
-// model/mamba2.py:45). out_lp (bf16) optional.
+// model/mamba2.py:45). out_lp (16-bit copy in format lp_fmt, LpFmt) optional.
 int rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, int n_rows, int width,
-                 float* out, int64_t ldo, uint16_t* out_lp, int64_t ldl, hipStream_t s);
+                 float* out, int64_t ldo, uint16_t* out_lp, int lp_fmt, int64_t ldl, hipStream_t s);
 
-// Features [n, f] -> zero-padded GEMM operand [n, kpad] (fp32 and/or bf16).
-int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, uint16_t* out_lp,
+// Features [n, f] -> zero-padded GEMM operand [n, kpad] (fp32 and/or 16-bit).
+int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, uint16_t* out_lp, int lp_fmt,
                    hipStream_t s);
 
 // Mamba2 tail before out_proj (model/mamba2.py:158-164):
@@ -33,7 +33,7 @@ int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, u
 // the sum of n_parts planes part_stride floats apart (split-row scan).
 int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const float* x,
                 int64_t ldx, const float* z, int64_t ldz, const float* d, const float* w,
-                int n_rows, int inner, int head_size, float* out, uint16_t* out_lp,
+                int n_rows, int inner, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
                 hipStream_t s);
 
 // dt = softplus(dt_raw); decay = exp(a[head] * dt) (model/mamba2.py:92-97).
@@ -43,26 +43,26 @@ int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float*
 // RetNet tail before out_proj (model/retnet.py:168-169): per-head RMSNorm
 // (eps 1e-6, no affine), times silu(g). o is the sum of n_parts planes.
 int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g, int64_t ldg,
-                int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp,
+                int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
                 hipStream_t s);
 
 // sLSTM block tail + mLSTM block norm (model/xlstm.py:422-424, :308):
 // x1 = GroupNorm(groups)(y) + skip; xn = LayerNorm(x1) * w_ln.
 int slstm_post(const float* y, const float* skip, const float* gn_w, const float* gn_b,
                int groups, const float* ln_w, int n_rows, int hidden, float* x1, float* xn,
-               uint16_t* xn_lp, hipStream_t s);
+               uint16_t* xn_lp, int lp_fmt, hipStream_t s);
 
 // Fused row pairs of the xLSTM block (model/inference_model.py:63-68 around
 // model/xlstm.py:355-367): a = RMSNorm(x) * w_rms, xn = LayerNorm(a) * w_ln;
 // and x = LayerNorm(y) * w_ln + x, a = RMSNorm(x) * w_rms.
 int rms_ln_rows(const float* x, const float* w_rms, float eps, const float* w_ln, int n_rows,
-                int width, float* a, uint16_t* a_lp, float* xn, hipStream_t s);
+                int width, float* a, uint16_t* a_lp, int lp_fmt, float* xn, hipStream_t s);
 int ln_res_rms_rows(const float* y, const float* w_ln, float* x, const float* w_rms, float eps,
-                    int n_rows, int width, float* a, uint16_t* a_lp, hipStream_t s);
+                    int n_rows, int width, float* a, uint16_t* a_lp, int lp_fmt, hipStream_t s);
 
 // out = LayerNorm(x) * w (+ residual) (no bias; eps 1e-5).
 int layernorm_rows(const float* x, const float* w, const float* residual, int n_rows, int width,
-                   float* out, uint16_t* out_lp, hipStream_t s);
+                   float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s);
 
 // mLSTM cell/block tail (model/xlstm.py:236-241, :321-322):
 // out = GroupNorm(num / den) ; h = (out + skip * x_conv) * silu(x_gate).
@@ -70,7 +70,7 @@ int layernorm_rows(const float* x, const float* w, const float* residual, int n_
 int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* den, int den_ld,
                const float* gn_w, const float* gn_b, const float* skip_w, const float* x_conv,
                const float* x_gate, int64_t ld_gate, int n_rows, int inner, int heads,
-               float* out, uint16_t* out_lp, hipStream_t s);
+               float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s);
 
 // preds[r, col] = x[r] . w + b (shared output_proj, model/inference_model.py:142).
 int output_proj(const float* x, const float* w, const float* b, int n_rows, int hidden,
@@ -93,8 +93,8 @@ int mlstm_qkv_if(const float* x_conv, const float* x_m, int64_t ld_xm, const flo
                  const float* w_if, const float* b_if, int n_out, float* qkv, float* ks,
                  float* if_part, int segs, hipStream_t s);
 
-// bf16 copy of an fp32 matrix (weights at bind time).
-int to_bf16(const float* src, uint16_t* dst, int64_t n, hipStream_t s);
+// 16-bit copy (LpFmt lp_fmt) of an fp32 matrix (weights at bind time).
+int to_lp(const float* src, uint16_t* dst, int64_t n, int lp_fmt, hipStream_t s);
 // fill with a constant
 int fill_f32(float* dst, int64_t n, float v, hipStream_t s);
 
@@ -115,7 +115,7 @@ int retnet_prep(const Runs& r, const float* qkvg, int64_t ld, int hidden, int he
 // Hawk RG-LRU over each run, times gelu(gate) (model/hawk.py:31-37, :77, :83).
 int rglru_scan(const Runs& r, const float* x, const float* gi, const float* gr, int64_t ldg,
                const float* gate, int64_t ld_gate, const float* a, float c_exp, int hidden,
-               float* h_state, float* out, uint16_t* out_lp, hipStream_t s);
+               float* h_state, float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s);
 
 // One sLSTM step for the first n_active runs (model/xlstm.py:414-421, :355-369).
 int slstm_round(const Runs& r, int step, int n_active, const float* gin, int hidden, int heads,

@@ -50,7 +50,7 @@ template <int V>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ w, float eps,
                                                       int width, float* __restrict__ out,
-                                                      int64_t ldo, uint16_t* __restrict__ out_lp,
+                                                      int64_t ldo, uint16_t* __restrict__ out_lp, int lp_fmt,
                                                       int64_t ldl) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     if (c < width) {
       const float o = (r.v[i] * inv) * w[c];
       if (out) out[row * ldo + c] = o;
-      if (out_lp) out_lp[row * ldl + c] = f32_to_bf16_bits(o);
+      if (out_lp) out_lp[row * ldl + c] = f32_to_lp_bits(o, lp_fmt);
     }
   }
 }
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
                                                         const float* __restrict__ w,
                                                         const float* __restrict__ residual,
                                                         int width, float* __restrict__ out,
-                                                        uint16_t* __restrict__ out_lp) {
+                                                        uint16_t* __restrict__ out_lp, int lp_fmt) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   RowRegs<V> r;
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
       float o = ((r.v[i] - mean) * rstd) * w[c];
       if (residual) o += residual[row * width + c];
       if (out) out[row * width + c] = o;
-      if (out_lp) out_lp[row * width + c] = f32_to_bf16_bits(o);
+      if (out_lp) out_lp[row * width + c] = f32_to_lp_bits(o, lp_fmt);
     }
   }
 }
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void rms_ln_kernel(const float* __restrict__ x
                                                      const float* __restrict__ w_rms, float eps,
                                                      const float* __restrict__ w_ln, int width,
                                                      float* __restrict__ a,
-                                                     uint16_t* __restrict__ a_lp,
+                                                     uint16_t* __restrict__ a_lp, int lp_fmt,
                                                      float* __restrict__ xn) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void rms_ln_kernel(const float* __restrict__ x
     r.v[i] = c < width ? (r.v[i] * inv) * w_rms[min(c, width - 1)] : 0.0f;
     if (c < width) {
       a[row * width + c] = r.v[i];
-      if (a_lp) a_lp[row * width + c] = f32_to_bf16_bits(r.v[i]);
+      if (a_lp) a_lp[row * width + c] = f32_to_lp_bits(r.v[i], lp_fmt);
     }
   }
   const float mean = block_sum(r.sum(width), red) / (float)width;
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256) void ln_res_rms_kernel(const float* __restrict
                                                          const float* __restrict__ w_rms,
                                                          float eps, int width,
                                                          float* __restrict__ a,
-                                                         uint16_t* __restrict__ a_lp) {
+                                                         uint16_t* __restrict__ a_lp, int lp_fmt) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   RowRegs<V> r, xr;
@@ -156,13 +156,13 @@ __global__ __launch_bounds__(256) void ln_res_rms_kernel(const float* __restrict
     if (c < width) {
       const float o = (r.v[i] * inv) * w_rms[c];
       a[row * width + c] = o;
-      if (a_lp) a_lp[row * width + c] = f32_to_bf16_bits(o);
+      if (a_lp) a_lp[row * width + c] = f32_to_lp_bits(o, lp_fmt);
     }
   }
 }
 
 __global__ void stage_features_kernel(const float* __restrict__ feat, int n_rows, int f, int kpad,
-                                      float* __restrict__ out, uint16_t* __restrict__ out_lp) {
+                                      float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt) {
   const int64_t total = (int64_t)n_rows * kpad;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -170,7 +170,7 @@ __global__ void stage_features_kernel(const float* __restrict__ feat, int n_rows
     const int c = (int)(i % kpad);
     const float v = c < f ? feat[r * f + c] : 0.0f;
     if (out) out[i] = v;
-    if (out_lp) out_lp[i] = f32_to_bf16_bits(v);
+    if (out_lp) out_lp[i] = f32_to_lp_bits(v, lp_fmt);
   }
 }
 
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void mamba2_post_kernel(
     const float* __restrict__ ssm_out, int n_parts, int64_t part_stride,
     const float* __restrict__ x, int64_t ldx, const float* __restrict__ z, int64_t ldz,
     const float* __restrict__ d, const float* __restrict__ w, int inner, int head_size,
-    float* __restrict__ out, uint16_t* __restrict__ out_lp) {
+    float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const float* xr = x + row * ldx;
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) void mamba2_post_kernel(
     if (c < inner) {
       const float o = (yv[u] * inv) * w[c];
       if (out) out[row * inner + c] = o;
-      if (out_lp) out_lp[row * inner + c] = f32_to_bf16_bits(o);
+      if (out_lp) out_lp[row * inner + c] = f32_to_lp_bits(o, lp_fmt);
     }
   }
 }
@@ -228,7 +228,7 @@ constexpr int kHeadPostMax = 16;
 __global__ void retnet_post_kernel(const float* __restrict__ o, int n_parts, int64_t part_stride,
                                    const float* __restrict__ g, int64_t ldg, int hidden,
                                    int head_size, float* __restrict__ out,
-                                   uint16_t* __restrict__ out_lp) {
+                                   uint16_t* __restrict__ out_lp, int lp_fmt) {
   const int64_t row = blockIdx.x;
   const int head = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -250,7 +250,7 @@ __global__ void retnet_post_kernel(const float* __restrict__ o, int n_parts, int
     if (j < head_size) {
       const float v = silu(grow[j]) * (ov[u] * inv);
       if (out) out[ob + j] = v;
-      if (out_lp) out_lp[ob + j] = f32_to_bf16_bits(v);
+      if (out_lp) out_lp[ob + j] = f32_to_lp_bits(v, lp_fmt);
     }
   }
 }
@@ -260,7 +260,7 @@ __global__ void slstm_post_kernel(const float* __restrict__ y, const float* __re
                                   const float* __restrict__ gn_w, const float* __restrict__ gn_b,
                                   const float* __restrict__ ln_w, int hidden, int gsize,
                                   float* __restrict__ x1, float* __restrict__ xn,
-                                  uint16_t* __restrict__ xn_lp) {
+                                  uint16_t* __restrict__ xn_lp, int lp_fmt) {
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
   const int grp = threadIdx.x >> 6;
@@ -299,7 +299,7 @@ __global__ void slstm_post_kernel(const float* __restrict__ y, const float* __re
     const int c = grp * gsize + j;
     const float o = ((x1[base + j] - rmean) * rrstd) * ln_w[c];
     if (xn) xn[base + j] = o;
-    if (xn_lp) xn_lp[base + j] = f32_to_bf16_bits(o);
+    if (xn_lp) xn_lp[base + j] = f32_to_lp_bits(o, lp_fmt);
   }
 }
 
@@ -314,7 +314,7 @@ __global__ void mlstm_post_kernel(const float* __restrict__ num, int n_parts, in
                                   const float* __restrict__ skip_w,
                                   const float* __restrict__ x_conv,
                                   const float* __restrict__ x_gate, int64_t ld_gate, int inner,
-                                  int hs, float* __restrict__ out, uint16_t* __restrict__ out_lp) {
+                                  int hs, float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt) {
   const int64_t row = blockIdx.x;
   const int head = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -356,7 +356,7 @@ __global__ void mlstm_post_kernel(const float* __restrict__ num, int n_parts, in
       const float gnv = ((hv[u] - mean) * rstd) * gw[u] + gb[u];
       const float h = (gnv + sk[u] * xc[u]) * silu(xg[u]);
       if (out) out[base + j] = h;
-      if (out_lp) out_lp[base + j] = f32_to_bf16_bits(h);
+      if (out_lp) out_lp[base + j] = f32_to_lp_bits(h, lp_fmt);
     }
   }
 }
@@ -493,11 +493,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   }
 }
 
-__global__ void to_bf16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
-                               int64_t n) {
+__global__ void to_lp_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                             int64_t n, int lp_fmt) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
-    dst[i] = f32_to_bf16_bits(src[i]);
+    dst[i] = f32_to_lp_bits(src[i], lp_fmt);
 }
 
 __global__ void fill_f32_kernel(float* __restrict__ dst, int64_t n, float v) {
@@ -528,11 +528,11 @@ inline unsigned grid_for(int64_t total, int block = 256) {
   } while (0)
 
 int rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, int n_rows, int width,
-                 float* out, int64_t ldo, uint16_t* out_lp, int64_t ldl, hipStream_t s) {
+                 float* out, int64_t ldo, uint16_t* out_lp, int lp_fmt, int64_t ldl, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
 #define L(V)                                                                              \
   hipLaunchKernelGGL(rmsnorm_kernel<V>, dim3(n_rows), dim3(256), 0, s, x, ldx, w, eps, width, \
-                     out, ldo, out_lp, ldl)
+                     out, ldo, out_lp, lp_fmt, ldl)
   HK_ROW_DISPATCH(width, L);
 #undef L
   HK_LAUNCH_CHECK();
@@ -540,11 +540,11 @@ int rmsnorm_rows(const float* x, int64_t ldx, const float* w, float eps, int n_r
 }
 
 int rms_ln_rows(const float* x, const float* w_rms, float eps, const float* w_ln, int n_rows,
-                int width, float* a, uint16_t* a_lp, float* xn, hipStream_t s) {
+                int width, float* a, uint16_t* a_lp, int lp_fmt, float* xn, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
 #define L(V)                                                                                \
   hipLaunchKernelGGL(rms_ln_kernel<V>, dim3(n_rows), dim3(256), 0, s, x, w_rms, eps, w_ln, width, \
-                     a, a_lp, xn)
+                     a, a_lp, lp_fmt, xn)
   HK_ROW_DISPATCH(width, L);
 #undef L
   HK_LAUNCH_CHECK();
@@ -552,35 +552,35 @@ int rms_ln_rows(const float* x, const float* w_rms, float eps, const float* w_ln
 }
 
 int ln_res_rms_rows(const float* y, const float* w_ln, float* x, const float* w_rms, float eps,
-                    int n_rows, int width, float* a, uint16_t* a_lp, hipStream_t s) {
+                    int n_rows, int width, float* a, uint16_t* a_lp, int lp_fmt, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
 #define L(V)                                                                                  \
   hipLaunchKernelGGL(ln_res_rms_kernel<V>, dim3(n_rows), dim3(256), 0, s, y, w_ln, x, w_rms, eps, \
-                     width, a, a_lp)
+                     width, a, a_lp, lp_fmt)
   HK_ROW_DISPATCH(width, L);
 #undef L
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
 
-int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, uint16_t* out_lp,
+int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, uint16_t* out_lp, int lp_fmt,
                    hipStream_t s) {
   if (n_rows == 0) return HK_OK;
   hipLaunchKernelGGL(stage_features_kernel, dim3(grid_for((int64_t)n_rows * kpad)), dim3(256), 0,
-                     s, feat, n_rows, f, kpad, out, out_lp);
+                     s, feat, n_rows, f, kpad, out, out_lp, lp_fmt);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
 
 int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const float* x,
                 int64_t ldx, const float* z, int64_t ldz, const float* d, const float* w,
-                int n_rows, int inner, int head_size, float* out, uint16_t* out_lp,
+                int n_rows, int inner, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
                 hipStream_t s) {
   if (n_rows == 0) return HK_OK;
   HK_REQUIRE(inner <= 256 * kMambaPostMax && n_parts >= 1,
              "mamba2_post: inner %d above %d or no planes", inner, 256 * kMambaPostMax);
   hipLaunchKernelGGL(mamba2_post_kernel, dim3(n_rows), dim3(256), 0, s, ssm_out, n_parts,
-                     part_stride, x, ldx, z, ldz, d, w, inner, head_size, out, out_lp);
+                     part_stride, x, ldx, z, ldz, d, w, inner, head_size, out, out_lp, lp_fmt);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
@@ -595,7 +595,7 @@ int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float*
 }
 
 int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g, int64_t ldg,
-                int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp,
+                int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
                 hipStream_t s) {
   if (n_rows == 0) return HK_OK;
   const int heads = hidden / head_size;
@@ -603,29 +603,29 @@ int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g
                  n_parts >= 1,
              "retnet_post: %d heads of %d unsupported", heads, head_size);
   hipLaunchKernelGGL(retnet_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, o, n_parts,
-                     part_stride, g, ldg, hidden, head_size, out, out_lp);
+                     part_stride, g, ldg, hidden, head_size, out, out_lp, lp_fmt);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
 
 int slstm_post(const float* y, const float* skip, const float* gn_w, const float* gn_b,
                int groups, const float* ln_w, int n_rows, int hidden, float* x1, float* xn,
-               uint16_t* xn_lp, hipStream_t s) {
+               uint16_t* xn_lp, int lp_fmt, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
   HK_REQUIRE(groups >= 1 && groups <= 16 && hidden % groups == 0,
              "slstm_post: %d groups unsupported", groups);
   hipLaunchKernelGGL(slstm_post_kernel, dim3(n_rows), dim3(64 * groups), 0, s, y, skip, gn_w,
-                     gn_b, ln_w, hidden, hidden / groups, x1, xn, xn_lp);
+                     gn_b, ln_w, hidden, hidden / groups, x1, xn, xn_lp, lp_fmt);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
 
 int layernorm_rows(const float* x, const float* w, const float* residual, int n_rows, int width,
-                   float* out, uint16_t* out_lp, hipStream_t s) {
+                   float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
 #define L(V)                                                                                \
   hipLaunchKernelGGL(layernorm_kernel<V>, dim3(n_rows), dim3(256), 0, s, x, w, residual, width, \
-                     out, out_lp)
+                     out, out_lp, lp_fmt)
   HK_ROW_DISPATCH(width, L);
 #undef L
   HK_LAUNCH_CHECK();
@@ -635,7 +635,7 @@ int layernorm_rows(const float* x, const float* w, const float* residual, int n_
 int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* den, int den_ld,
                const float* gn_w, const float* gn_b, const float* skip_w, const float* x_conv,
                const float* x_gate, int64_t ld_gate, int n_rows, int inner, int heads,
-               float* out, uint16_t* out_lp, hipStream_t s) {
+               float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
   HK_REQUIRE(heads >= 1 && heads <= 16 && inner % heads == 0 &&
                  inner / heads <= 64 * kHeadPostMax && n_parts >= 1,
@@ -644,7 +644,7 @@ int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* 
 #define HK_POST(U, F)                                                                     \
   hipLaunchKernelGGL((mlstm_post_kernel<U, F>), dim3(n_rows), dim3(64 * heads), 0, s, num, \
                      n_parts, part_stride, den, den_ld, gn_w, gn_b, skip_w, x_conv, x_gate,  \
-                     ld_gate, inner, hs, out, out_lp)
+                     ld_gate, inner, hs, out, out_lp, lp_fmt)
   if (hs == 512) {
     HK_POST(8, true);
   } else if (hs == 256) {
@@ -713,9 +713,9 @@ bool mlstm_qkv_if_supported(int inner, int n_out, int segs) {
          (inner / 4) % segs == 0;
 }
 
-int to_bf16(const float* src, uint16_t* dst, int64_t n, hipStream_t s) {
+int to_lp(const float* src, uint16_t* dst, int64_t n, int lp_fmt, hipStream_t s) {
   if (n == 0) return HK_OK;
-  hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
+  hipLaunchKernelGGL(to_lp_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n, lp_fmt);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }

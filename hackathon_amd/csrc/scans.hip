@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void rglru_scan_kernel(
     const float* __restrict__ gi, const float* __restrict__ gr, int64_t ldg,
     const float* __restrict__ gate, int64_t ld_gate, const float* __restrict__ a, float c_exp,
     int hidden, float* __restrict__ h_state, float* __restrict__ out,
-    uint16_t* __restrict__ out_lp) {
+    uint16_t* __restrict__ out_lp, int lp_fmt) {
   const int run = blockIdx.x;
   const int c = blockIdx.y * 256 + threadIdx.x;
   if (c >= hidden) return;
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(256) void rglru_scan_kernel(
         const float o = og[k] * h;
         const int64_t ri = (int64_t)(rb + k);
         if (out) out[ri * hidden + c] = o;
-        if (out_lp) out_lp[ri * hidden + c] = f32_to_bf16_bits(o);
+        if (out_lp) out_lp[ri * hidden + c] = f32_to_lp_bits(o, lp_fmt);
       }
     }
   };
@@ -845,11 +845,11 @@ int retnet_prep(const Runs& r, const float* qkvg, int64_t ld, int hidden, int he
 
 int rglru_scan(const Runs& r, const float* x, const float* gi, const float* gr, int64_t ldg,
                const float* gate, int64_t ld_gate, const float* a, float c_exp, int hidden,
-               float* h_state, float* out, uint16_t* out_lp, hipStream_t s) {
+               float* h_state, float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s) {
   if (r.n_runs == 0) return HK_OK;
   dim3 grid(r.n_runs, (hidden + 255) / 256);
   hipLaunchKernelGGL(rglru_scan_kernel, grid, dim3(256), 0, s, r.slot_ids, r.run_off, x, gi, gr,
-                     ldg, gate, ld_gate, a, c_exp, hidden, h_state, out, out_lp);
+                     ldg, gate, ld_gate, a, c_exp, hidden, h_state, out, out_lp, lp_fmt);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }

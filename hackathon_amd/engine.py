@@ -39,7 +39,9 @@ _lib.register("hk_engine_check", c_int, [c_void_p])
 _lib.register("hk_engine_profile", c_int, [c_void_p, c_int])
 _lib.register("hk_engine_profile_read", c_int, [c_void_p, c_int, ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_double)])
 
-LINEAR_DTYPES = ("bf16", "fp32")
+# CastLinear modes (example_model.py:150-157): the converted linears' storage
+# and compute format; "fp32" leaves every linear in fp32.
+LINEAR_DTYPES = {"fp32": 0, "bf16": 1, "fp16": 2}
 SCAN_KINDS = {"mlstm": 0, "mamba2": 1, "retnet": 2, "slstm": 3, "gemm": 4}
 
 # Slot order per tower type; must match the enums in csrc/engine.hip.
@@ -173,7 +175,7 @@ class Engine:
         device: str | torch.device = "cuda:0",
     ):
         if linear_dtype not in LINEAR_DTYPES:
-            raise ValueError(f"linear_dtype must be one of {LINEAR_DTYPES}")
+            raise ValueError(f"linear_dtype must be one of {tuple(LINEAR_DTYPES)}")
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise _lib.HipLibraryError("the engine needs a GPU device")
@@ -185,7 +187,7 @@ class Engine:
         vals = [
             cfg.hidden_size, cfg.proj_size, cfg.tower_depth, cfg.num_heads, cfg.num_features,
             cfg.mamba_head_size, cfg.mamba_bc_size, capacity, max_rows, self.max_runs,
-            1 if linear_dtype == "bf16" else 0,
+            LINEAR_DTYPES[linear_dtype],
         ]
         arr = (c_int * len(vals))(*vals)
         handle = c_void_p()
@@ -379,25 +381,3 @@ class Engine:
         _lib.check(_lib.lib().hk_engine_profile_read(self._h, SCAN_KINDS[kind], ctypes.byref(n), ctypes.byref(ms)),
                    "hk_engine_profile_read")
         return n.value, ms.value
-
-    def forward_masked(self, x: torch.Tensor, mask: torch.Tensor | None) -> torch.Tensor:
-        """MultiTowerModel.forward(x, state, mask) with the state held in the
-        store (model/inference_model.py:119-143): slot b advances by one step
-        with x[b] iff mask[b] (mask None: every slot). Returns preds [B, 4];
-        rows whose mask is False come back as zeros."""
-        B = x.shape[0]
-        assert B <= self.capacity
-        if mask is None:
-            active = np.arange(B, dtype=np.int32)
-        else:
-            assert mask.dtype == torch.bool and tuple(mask.shape) == (B,)
-            active = np.nonzero(mask.cpu().numpy())[0].astype(np.int32)
-        out = torch.zeros(B, 4, dtype=torch.float32, device=self.device)
-        if len(active) == 0:
-            return out
-        runs, _ = pack_runs(active, np.ones(len(active)))
-        idx = torch.as_tensor(active.astype(np.int64), device=self.device)
-        feats = x.to(self.device, torch.float32).index_select(0, idx).contiguous()
-        preds = self.tick(runs, feats)
-        out.index_copy_(0, idx, preds)
-        return out

@@ -18,6 +18,9 @@ _lib.register(
     ctypes.c_int,
     [ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_int],
 )
+_lib.register("hk_to_lp_host", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int])
+
+LP_FORMATS = {"bf16": 0, "fp16": 1}
 
 
 def param_key(seed: int, name: str) -> int:
@@ -39,4 +42,15 @@ def generate(cfg: ModelConfig, seed: int = 0) -> dict[str, torch.Tensor]:
     out = {}
     for p in param_specs(cfg):
         out[p.name] = fill_uniform(torch.empty(p.shape, dtype=torch.float32), seed, p.name, p.lo, p.hi)
+    return out
+
+
+def to_lp_bits(x: torch.Tensor, fmt: str) -> torch.Tensor:
+    """16-bit patterns (int16 tensor) of fp32 values in CastLinear format
+    `fmt` ("bf16" / "fp16"), by the library's conversion (hk_to_lp_host),
+    the one its kernels apply to weights, biases and activations."""
+    x = x.detach().to(torch.float32).contiguous().cpu()
+    out = torch.empty(x.shape, dtype=torch.int16)
+    _lib.check(_lib.lib().hk_to_lp_host(x.data_ptr(), out.data_ptr(), x.numel(), LP_FORMATS[fmt]),
+               "hk_to_lp_host")
     return out

@@ -135,6 +135,13 @@ uint64_t hk_param_key(uint64_t seed, const char* name);
  * fp32 with two roundings; `threads` host threads. */
 int hk_fill_uniform_host(float* dst, int64_t n, uint64_t key, float lo, float hi, int threads);
 
+/* dst[i] = the 16-bit pattern of src[i] in CastLinear format fmt (0 bf16,
+ * 1 fp16), round to nearest even, fp16 overflowing to infinity: torch's
+ * .to(torch.bfloat16) / .to(torch.float16), which CastLinear applies to its
+ * weights, biases, inputs and outputs (example_model.py:82-95). The engine's
+ * kernels use the same conversion. Host memory, no GPU. */
+int hk_to_lp_host(const float* src, uint16_t* dst, int64_t n, int fmt);
+
 /* ---------------------------------------------------------------------------
  * Ensemble engine: packed weights + slot-indexed HBM state store + tick.
  * Replaces MultiTowerModel(config) + init_state + forward
@@ -143,7 +150,9 @@ int hk_fill_uniform_host(float* dst, int64_t n, uint64_t key, float lo, float hi
  * ------------------------------------------------------------------------- */
 
 /* cfg[11] = {hidden, proj, depth, heads, features, mamba_head, mamba_bc,
- *            capacity (slots), max_rows, max_runs, lowp (1 = bf16 linears)}.
+ *            capacity (slots), max_rows, max_runs, lp}: lp 0 = every linear
+ *            fp32, 1 = bf16 CastLinear, 2 = fp16 CastLinear (the reference's
+ *            LINEAR_DTYPE values fp32 / bf16 / fp16, example_model.py:150-157).
  * Allocates weights, the state store (capacity slots) and workspaces on the
  * current device. Replaces ModelConfig/MultiTowerModel construction
  * (model/inference_model.py:21-27, :103-117) and convert_linears
@@ -159,9 +168,10 @@ int hk_engine_destroy(void* handle);
 int hk_engine_param_numel(void* handle, int tower, int layer, int slot, int64_t* numel);
 
 /* Synchronous bind of one packed weight slot from host fp32 values; converted
- * to bf16 on the device for CastLinear weights in bf16 mode, biases rounded
- * through bf16 (example_model.py:82-90). Replaces load_state_dict +
- * convert_linears (example_model.py:301-331). */
+ * to the engine's 16-bit format (bf16 or fp16, round to nearest even) on the
+ * device for CastLinear weights, biases rounded through it
+ * (example_model.py:82-90). Replaces load_state_dict + convert_linears
+ * (example_model.py:301-331). */
 int hk_engine_load_param(void* handle, int tower, int layer, int slot, const float* host,
                          int64_t numel);
 

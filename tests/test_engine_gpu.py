@@ -53,25 +53,29 @@ def _engine(cfg, params, capacity, dtype="fp32", max_rows=256):
 
 
 def test_small_fixture_masked_steps_fp32(dev, small_params):
+    # The reference's model call shape (model/inference_model.py:119-146):
+    # state = model.init_state(B, device); preds, state = model(x, state, mask)
+    from hackathon_amd.model import MultiTowerModel
+
     fx = np.load(GOLDEN / "small.npz")
-    e = _engine(spec.SMALL, small_params, capacity=6)
+    model = MultiTowerModel(spec.SMALL, capacity=6, linear_dtype="fp32", weights=small_params)
+    state = model.init_state(6, dev)
     for t in range(16):
         x = torch.from_numpy(fx[f"x/{t}"]).to(dev)
         mask = torch.from_numpy(fx[f"mask/{t}"])
-        preds = e.forward_masked(x, mask.to(dev))
+        preds, state = model(x, state, mask)
         torch.cuda.synchronize()
         want = torch.from_numpy(fx[f"preds/{t}"])
         _close(preds.cpu()[mask], want[mask], P_RTOL, P_ATOL, f"step {t} preds")
         assert torch.all(preds.cpu()[~mask] == 0)
-    e.check()
-    state = list(om.flatten(e.export_state(0, 6)))
-    for i, leaf in enumerate(state):
+    model.engine.check()
+    for i, leaf in enumerate(om.flatten(state.export())):
         want = torch.from_numpy(fx[f"state/{i}"])
         if want.dtype == torch.int32:
             assert torch.equal(leaf.cpu(), want), f"leaf {i}"
         else:
             _close(leaf, want, 10 * P_RTOL, 10 * P_ATOL, f"state leaf {i} {tuple(want.shape)}")
-    e.close()
+    model.close()
 
 
 def _requests(rng, symbols, n_req, uid0, F):
@@ -246,12 +250,17 @@ def test_default_dims_fp32_golden(dev):
     fx = np.load(GOLDEN / "default.npz")
     cfg = spec.DEFAULT
     params = weights.generate(cfg, 0)
-    e = _engine(cfg, params, capacity=4, max_rows=16)
+    from hackathon_amd.model import MultiTowerModel
+
+    model = MultiTowerModel(cfg, capacity=4, linear_dtype="fp32", weights=params)
+    e = model.engine
+    st = model.init_state(4, dev)
     P32 = om.Params(params)
     s32 = om.init_state(cfg, 4)
     for t in range(4):
         x = torch.from_numpy(fx[f"x/{t}"])
-        preds = e.forward_masked(x.to(dev), None).cpu().double()
+        preds, st = model(x.to(dev), st)
+        preds = preds.cpu().double()
         ref32 = torch.from_numpy(fx[f"preds/{t}"]).double()
         ref64 = torch.from_numpy(fx[f"preds64/{t}"]).double()
         with torch.inference_mode():
@@ -274,14 +283,19 @@ def test_default_dims_fp32_past_log_cap(dev):
     256-row float2 tiles, on a non-zero state)."""
     cfg = spec.DEFAULT
     params = weights.generate(cfg, 0)
-    e = _engine(cfg, params, capacity=4, max_rows=16)
+    from hackathon_amd.model import MultiTowerModel
+
+    model = MultiTowerModel(cfg, capacity=4, linear_dtype="fp32", weights=params)
+    e = model.engine
+    st = model.init_state(4, dev)
     P32 = om.Params(params)
     s32 = om.init_state(cfg, 4)
     rng = np.random.default_rng(5)
     for t in range(12):
         x = torch.from_numpy(
             np.clip(rng.standard_normal((4, cfg.num_features)), -5, 5).astype(np.float32))
-        got = e.forward_masked(x.to(dev), None).cpu()
+        got, st = model(x.to(dev), st)
+        got = got.cpu()
         with torch.inference_mode():
             want, s32 = om.forward(P32, cfg, x, s32)
         # |d| / (|ref| + 2): the default dims' fp32 RetNet scatter (module

@@ -5,7 +5,10 @@ golden vectors written from the reference itself (tests/golden/make_golden.py):
   shapes): every output for 12 steps, full state after steps 0, 3 and 11;
 - the small MultiTowerModel over 16 masked steps with the client's fold:
   predictions every step and the final state;
-- the default-dims model (4 symbols, 4 steps): predictions.
+- the default-dims model (4 symbols, 4 steps): predictions;
+- the CastLinear emulation (Params(lp="bf16"/"fp16")) against the
+  reference's own convert_linears on the small model (16 masked steps,
+  predictions and final state) and at the default dims (2 steps).
 
 Plus library-routine checks of the building blocks (conv1d, BlockLinear),
 written independently of the oracle's own expressions.
@@ -138,3 +141,46 @@ def test_slstm_cell_first_step_and_scale_invariance():
     _, (c2, n2, _) = om.slstm_cell(i, f, z, o, c0 * torch.exp(torch.tensor(-2.0, dtype=torch.float64)),
                                    n0 * torch.exp(torch.tensor(-2.0, dtype=torch.float64)), m0 + 2.0)
     torch.testing.assert_close(c1 / n1, c2 / n2, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("lp", ["bf16", "fp16"])
+def test_castlinear_small_model_masked_steps(lp):
+    """The oracle's CastLinear emulation (Params(lp=...)) against the
+    reference's own convert_linears(model, dtype) on the small model: the
+    16 masked steps of small.npz, predictions every step and the final state
+    (tests/golden/small_lp.npz)."""
+    fx = np.load(GOLDEN / "small_lp.npz")
+    cfg = spec.SMALL
+    params = weights.generate(cfg, 0)
+    P = om.Params(params, lp=lp)
+    state = om.init_state(cfg, 6)
+    for t in range(16):
+        preds, state = om.forward(P, cfg, _t(fx[f"x/{t}"]), state, _t(fx[f"mask/{t}"]))
+        torch.testing.assert_close(preds, _t(fx[f"{lp}/preds/{t}"]), rtol=RTOL, atol=ATOL)
+    for i, leaf in enumerate(om.flatten(state)):
+        torch.testing.assert_close(leaf, _t(fx[f"{lp}/state/{i}"]), rtol=RTOL, atol=ATOL)
+    # The conversion leaves exactly the FP32_LINEAR_NAMES sites in fp32
+    # (example_model.py:106): with lp set, one of them computes in fp32 and a
+    # converted linear does not.
+    assert fx[f"{lp}/converted"][1] > 0
+    x = torch.randn(3, cfg.hidden_size, dtype=torch.float32)
+    assert torch.equal(P.linear(x, "output_proj"), torch.nn.functional.linear(
+        x, params["output_proj.weight"], params["output_proj.bias"]))
+    name = "towers.0.blocks.0.mlp.fc1"
+    lpd = {"bf16": torch.bfloat16, "fp16": torch.float16}[lp]
+    assert torch.equal(P.linear(x, name), torch.nn.functional.linear(
+        x.to(lpd), params[name + ".weight"].to(lpd), params[name + ".bias"].to(lpd)).float())
+
+
+@pytest.mark.parametrize("lp", ["bf16", "fp16"])
+def test_castlinear_default_dims_predictions(lp):
+    """Default dims after the reference's convert_linears: the first two
+    steps of default.npz's inputs (tests/golden/default_lp.npz)."""
+    fx = np.load(GOLDEN / "default_lp.npz")
+    cfg = spec.DEFAULT
+    P = om.Params(weights.generate(cfg, 0), lp=lp)
+    state = om.init_state(cfg, 4)
+    with torch.inference_mode():
+        for t in range(2):
+            preds, state = om.forward(P, cfg, _t(fx[f"x/{t}"]), state)
+            torch.testing.assert_close(preds, _t(fx[f"{lp}/preds/{t}"]), rtol=RTOL, atol=ATOL)
