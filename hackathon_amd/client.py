@@ -138,75 +138,35 @@ class NnInferenceClient:
 
     @torch.inference_mode()
     def process_batch(self, requests_by_symbol: Dict[str, List[PendingRequest]]) -> InferenceResponse:
-        all_ids: list = []
-        all_preds: list = []
-        items = []  # (slot, reqs) in dict order
+        symbols, counts, flat = [], [], []
         for symbol, reqs in requests_by_symbol.items():
-            if not reqs:
-                continue
-            slot = self._row_for(symbol)
-            if slot is None:
-                for req in reqs:
-                    all_ids.append(req.unique_id)
-                    all_preds.append([0.0] * self.num_outputs)
-                continue
-            items.append((slot, reqs))
-        if not items:
-            return InferenceResponse(all_ids, all_preds, time.time())
-
-        if sum(len(r) for _, r in items) <= self.engine.max_rows:
-            self._run_items(items, all_ids, all_preds)
-        else:
-            # Round-major chunks of at most max_rows requests: chunk j holds
-            # rounds [k0, k1) of every symbol, which keeps each symbol's order
-            # and the reference's response order.
-            maxlen = max(len(r) for _, r in items)
-            k0 = 0
-            while k0 < maxlen:
-                k1, rows = k0, 0
-                while k1 < maxlen:
-                    add = sum(1 for _, r in items if len(r) > k1)
-                    if rows + add > self.engine.max_rows and k1 > k0:
-                        break
-                    rows += add
-                    k1 += 1
-                part = [(slot, reqs[k0:k1]) for slot, reqs in items if len(reqs) > k0]
-                self._run_items(part, all_ids, all_preds)
-                k0 = k1
-        return InferenceResponse(all_ids, all_preds, time.time())
-
-    def _run_items(self, items, all_ids, all_preds):
-        """One engine tick over (slot, requests) pairs; appends the answers
-        round by round."""
-        flat = [q for _, reqs in items for q in reqs]
+            symbols.append(symbol)
+            counts.append(len(reqs))
+            flat.extend(reqs)
+        if not flat:
+            return InferenceResponse([], [], time.time())
         feats = np.asarray([q.features for q in flat], dtype=np.float32)
-        runs, req_row, resp_req = pack_tick([s for s, _ in items], [len(r) for _, r in items])
-        preds = self._tick_rows(runs, req_row, feats)
-        all_ids.extend(flat[j].unique_id for j in resp_req)
-        all_preds.extend(preds[resp_req].tolist())
+        order, preds = self.process_arrays(symbols, counts, feats)
+        return InferenceResponse([flat[j].unique_id for j in order], preds.tolist(), time.time())
 
-    def _tick_rows(self, runs, rows, feats):
-        """One engine tick over packed runs: feats[j] goes to row rows[j]
-        (pinned staging, one H2D copy), and the predictions come back in the
-        same order as float64 [len(rows), 4] (one D2H copy)."""
-        n = runs.n_rows
-        self._feat_host.numpy()[rows] = feats
-        self._feat_dev[:n].copy_(self._feat_host[:n], non_blocking=True)
-        self.engine.tick(runs, self._feat_dev[:n], self._preds_dev[:n])
-        self._preds_host[:n].copy_(self._preds_dev[:n], non_blocking=True)
-        self.engine.check()  # synchronises; raises if an in-kernel barrier timed out
-        return self._preds_host[:n].numpy()[rows].astype(np.float64)
-
+    @torch.inference_mode()
     def process_arrays(self, symbols, counts, features):
         """process_batch for callers holding flat arrays: `symbols` in dict
         order with `counts[i]` requests each, `features` [sum(counts),
         num_features] float32 with each symbol's requests together, in
-        order. Returns (resp_req, predictions): the request index answered at
+        order. Returns (order, predictions): the request index answered at
         each response position (the reference's order) and a float64
         [n_req, 4] array in that order. Same slot assignment and zero
-        answers as process_batch; at most max_rows slotted requests."""
+        answers as process_batch.
+
+        A batch of more slotted requests than the engine's max_rows runs as
+        several ticks, each a range of rounds (round k = the k-th request of
+        every symbol with more than k), which keeps each symbol's order and
+        the reference's response order."""
         counts = np.asarray(counts, dtype=np.int64)
         feats = np.ascontiguousarray(features, dtype=np.float32)
+        if len(counts) != len(symbols):
+            raise ValueError("symbols and counts differ in length")
         if feats.shape != (int(counts.sum()), self.num_features):
             raise ValueError(f"features {feats.shape} do not match counts (sum {counts.sum()})")
         slots = np.full(len(counts), -1, dtype=np.int32)
@@ -214,11 +174,56 @@ class NnInferenceClient:
             if c > 0:
                 row = self._row_for(sym)
                 slots[i] = -1 if row is None else row
-        runs, req_row, resp_req = pack_tick(slots, counts)
-        if runs.n_rows > self.engine.max_rows:
-            raise ValueError(f"process_arrays: more than {self.engine.max_rows} slotted requests")
-        out = np.zeros((len(req_row), self.num_outputs), dtype=np.float64)
-        if runs.n_rows:
-            sel = np.flatnonzero(req_row >= 0)
-            out[sel] = self._tick_rows(runs, req_row[sel], feats[sel])
-        return resp_req, out[resp_req]
+        n_req = int(counts.sum())
+        out = np.zeros((n_req, self.num_outputs), dtype=np.float64)
+        base = np.concatenate([[0], np.cumsum(counts)])
+        parts = []
+        # symbols without a slot are answered first, with zeros
+        # (example_model.py:826-839)
+        unslotted = np.flatnonzero((slots < 0) & (counts > 0))
+        if len(unslotted):
+            parts.append(np.concatenate([np.arange(base[i], base[i + 1]) for i in unslotted]))
+        items = np.flatnonzero(slots >= 0)
+        for k0, k1 in self._round_chunks(counts[items]):
+            c = np.clip(counts[items] - k0, 0, k1 - k0)
+            keep = c > 0
+            it, c = items[keep], c[keep]
+            runs, req_row, resp = pack_tick(slots[it], c)
+            # the chunk's requests (numbered item by item) -> global request index
+            sub0 = np.concatenate([[0], np.cumsum(c)[:-1]])
+            glob = np.repeat(base[it] + k0 - sub0, c) + np.arange(int(c.sum()))
+            out[glob] = self._tick_rows(runs, req_row, feats[glob])
+            parts.append(glob[resp])
+        order = np.concatenate(parts) if parts else np.zeros(0, dtype=np.int64)
+        return order, out[order]
+
+    def _round_chunks(self, counts):
+        """Round ranges [k0, k1) whose requests fit one tick each."""
+        if len(counts) == 0:
+            return []
+        maxlen = int(counts.max())
+        if int(counts.sum()) <= self.engine.max_rows:
+            return [(0, maxlen)]
+        # requests in round k: symbols with more than k requests
+        per_round = np.cumsum(np.bincount(counts, minlength=maxlen + 1)[::-1])[::-1][1:]
+        chunks, k0, rows = [], 0, 0
+        for k in range(maxlen):
+            if rows + per_round[k] > self.engine.max_rows and k > k0:
+                chunks.append((k0, k))
+                k0, rows = k, 0
+            rows += int(per_round[k])
+        chunks.append((k0, maxlen))
+        return chunks
+
+    def _tick_rows(self, runs, rows, feats):
+        """One engine tick over packed runs: feats[j] goes to row rows[j]
+        (pinned staging, one H2D copy), and the predictions come back in the
+        same order as float64 [len(rows), 4] (one D2H copy, then a wait for
+        this stream only)."""
+        n = runs.n_rows
+        self._feat_host.numpy()[rows] = feats
+        self._feat_dev[:n].copy_(self._feat_host[:n], non_blocking=True)
+        self.engine.tick(runs, self._feat_dev[:n], self._preds_dev[:n])
+        self._preds_host[:n].copy_(self._preds_dev[:n], non_blocking=True)
+        self.engine.check()  # waits for the stream; raises if an in-kernel barrier timed out
+        return self._preds_host[:n].numpy()[rows].astype(np.float64)

@@ -259,6 +259,7 @@ struct Engine {
   int* d_err = nullptr;      // [1]: set by a kernel whose barrier timed out
   uint64_t* d_trace = nullptr;  // HK_TRACE_SLSTM: per-step stamps of layer 0's sLSTM
   int* h_stage = nullptr;    // pinned [2][stage_ints()]
+  int* h_err = nullptr;      // pinned [1]: d_err read back by hk_engine_check
   int stage_ints() const { return 3 * max_runs + 2 + 3 * max_rows; }
   hipEvent_t stage_done[2] = {nullptr, nullptr};
   int stage_idx = 0;
@@ -300,6 +301,7 @@ struct Engine {
     for (auto& e : stage_done)
       if (e) (void)hipEventDestroy(e);
     if (h_stage) (void)hipHostFree(h_stage);
+    if (h_err) (void)hipHostFree(h_err);
   }
 
   void* alloc_bytes(size_t bytes) {
@@ -427,6 +429,7 @@ int build_workspace(Engine& e) {
   }
   HK_CHECK_HIP(hipMemset(e.d_xch, 0, (size_t)e.max_rows * d.H * 8));
   HK_CHECK_HIP(hipMemset(e.d_xch2, 0, (size_t)e.max_rows * d.H * 8));
+  HK_CHECK_HIP(hipHostMalloc((void**)&e.h_err, 4, hipHostMallocDefault));
   HK_CHECK_HIP(hipHostMalloc((void**)&e.h_stage, (size_t)2 * e.stage_ints() * 4,
                              hipHostMallocDefault));
   for (auto& ev : e.stage_done) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
@@ -1187,21 +1190,27 @@ int hk_engine_reset_slots(void* h, const int* slots_host, int n, void* stream) {
   return HK_OK;
 }
 
-// Synchronises the device and reports a step barrier that timed out in any
-// earlier tick (then returns -2 and clears the flag).
-int hk_engine_check(void* h) {
+// Waits for the work enqueued on `stream` so far (a tick ends with every side
+// stream joined back into its stream, so waiting for the tick's stream waits
+// for the whole tick; nothing else on the device is waited for) and reports a
+// step barrier that timed out in any earlier tick (then returns -2 and clears
+// the flag). The flag travels with the stream's work: one copy into pinned
+// host memory, then one stream synchronisation.
+int hk_engine_check(void* h, void* stream) {
   HK_REQUIRE(h, "hk_engine_check: null handle");
   Engine& e = *static_cast<Engine*>(h);
-  HK_CHECK_HIP(hipDeviceSynchronize());
-  int flag = 0;
-  HK_CHECK_HIP(hipMemcpy(&flag, e.d_err, 4, hipMemcpyDeviceToHost));
+  hipStream_t s = (hipStream_t)stream;
+  HK_CHECK_HIP(hipMemcpyAsync(e.h_err, e.d_err, 4, hipMemcpyDeviceToHost, s));
+  HK_CHECK_HIP(hipStreamSynchronize(s));
+  const int flag = *e.h_err;
   if (e.d_trace) {
     // Phases of the last tick's layer-0 sLSTM steps in microseconds
     // (s_memrealtime runs at 100 MHz), work-group 0, first chunk: poll for
     // h_{t-1}, staging barrier, product, cell update, later chunks, and the
     // gap to the next step.
     std::vector<uint64_t> tr((size_t)e.max_rows * 8);
-    HK_CHECK_HIP(hipMemcpy(tr.data(), e.d_trace, tr.size() * 8, hipMemcpyDeviceToHost));
+    HK_CHECK_HIP(hipMemcpyAsync(tr.data(), e.d_trace, tr.size() * 8, hipMemcpyDeviceToHost, s));
+    HK_CHECK_HIP(hipStreamSynchronize(s));
     static const char* names[6] = {"poll", "stage", "dot", "cell", "rest-chunks", "next"};
     double tot[6] = {0, 0, 0, 0, 0, 0};
     int n = 0;
@@ -1225,10 +1234,11 @@ int hk_engine_check(void* h) {
     fprintf(stderr, "slstm %d steps:", n);
     for (int k = 0; k < 6; ++k) fprintf(stderr, " %s %.1f", names[k], tot[k]);
     fprintf(stderr, " us\n");
-    HK_CHECK_HIP(hipMemset(e.d_trace, 0, tr.size() * 8));
+    HK_CHECK_HIP(hipMemsetAsync(e.d_trace, 0, tr.size() * 8, s));
   }
   if (flag) {
-    HK_CHECK_HIP(hipMemset(e.d_err, 0, 4));
+    HK_CHECK_HIP(hipMemsetAsync(e.d_err, 0, 4, s));
+    HK_CHECK_HIP(hipStreamSynchronize(s));
     hk::set_error("hk_engine_check: a kernel step barrier timed out (results invalid)");
     return HK_ERR_HIP;
   }

@@ -35,7 +35,7 @@ _lib.register(
 _lib.register("hk_engine_reset_slots", c_int, [c_void_p, c_void_p, c_int, c_void_p])
 _lib.register("hk_engine_tick", c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p])
 
-_lib.register("hk_engine_check", c_int, [c_void_p])
+_lib.register("hk_engine_check", c_int, [c_void_p, c_void_p])
 _lib.register("hk_engine_profile", c_int, [c_void_p, c_int])
 _lib.register("hk_engine_profile_read", c_int, [c_void_p, c_int, ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_double)])
 
@@ -359,8 +359,10 @@ class Engine:
         return preds
 
     def check(self):
-        """Synchronise and raise if any in-kernel step barrier timed out."""
-        _lib.check(_lib.lib().hk_engine_check(self._h), "hk_engine_check")
+        """Wait for the current stream's work (every tick enqueued on it) and
+        raise if any in-kernel step barrier timed out. Releases the GIL while
+        it waits (ctypes does), so a receive thread keeps running."""
+        _lib.check(_lib.lib().hk_engine_check(self._h, self._stream()), "hk_engine_check")
 
     # -- measurement ---------------------------------------------------------------
     def profile(self, kinds=True):

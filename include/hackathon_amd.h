@@ -199,10 +199,13 @@ int hk_engine_reset_slots(void* handle, const int* slots_host, int n, void* stre
 int hk_engine_tick(void* handle, const int* slot_ids_host, const int* run_off_host, int n_runs,
                    const float* features_dev, float* preds_dev, void* stream);
 
-/* Synchronises the device; returns -2 if a persistent kernel's step barrier
- * timed out in an earlier tick (its results are then invalid), else 0. No
- * reference counterpart: the reference has no in-kernel barriers. */
-int hk_engine_check(void* handle);
+/* Waits for the work enqueued on `stream` (a tick's stream: every tick joins
+ * its side streams back into it, so this covers whole ticks; other work on
+ * the device is not waited for); returns -2 if a persistent kernel's step
+ * barrier timed out in an earlier tick (its results are then invalid), else 0.
+ * No reference counterpart: the reference has no in-kernel barriers; its
+ * per-round host read-back (example_model.py:880) is the wait this replaces. */
+int hk_engine_check(void* handle, void* stream);
 
 /* Measurement hook (no reference counterpart; the reference times with CUDA
  * events and torch.profiler, profile_step.py:337-397): with bit k of `kinds`

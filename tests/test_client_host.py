@@ -1,0 +1,107 @@
+"""NnInferenceClient's host logic without a GPU: slot assignment, the
+round-major chunking of batches larger than a tick, and the response order
+(example_model.py:724-767, :819-905), with the engine tick replaced by a
+stand-in that checks each tick's packing and answers request j with its own
+first four features. Expected: the oracle's answer order (pinned against the
+oracle's literal process_batch in test_pack_tick.py), zeros for symbols past
+capacity, each symbol's requests in order within every tick."""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+from hackathon_amd.client import NnInferenceClient, PendingRequest
+from oracle.client import response_order
+
+
+def _client(capacity, max_rows, F=6):
+    c = NnInferenceClient.__new__(NnInferenceClient)
+    c.engine = SimpleNamespace(max_rows=max_rows)
+    c.capacity = capacity
+    c.symbol_to_idx = {}
+    c.num_outputs = 4
+    c.num_features = F
+    c.ticks = []
+
+    def fake_tick(runs, rows, feats):
+        n = runs.n_rows
+        assert n <= max_rows and len(rows) == n == len(feats)
+        assert sorted(rows.tolist()) == list(range(n))
+        lens = np.diff(runs.run_off)
+        assert np.all(lens >= 1) and np.all(np.diff(lens) <= 0)      # sorted runs
+        assert len(set(runs.slot_ids.tolist())) == len(runs.slot_ids)  # distinct slots
+        by_row = np.empty_like(feats)
+        by_row[rows] = feats
+        c.ticks.append((runs, by_row))
+        return feats[:, :4].astype(np.float64)
+
+    c._tick_rows = fake_tick
+    return c
+
+
+@pytest.mark.parametrize("max_rows", [64, 7, 3])
+def test_process_arrays_order_chunks_and_overflow(max_rows):
+    rng = np.random.default_rng(max_rows)
+    capacity = 5
+    client = _client(capacity, max_rows=max(max_rows, capacity))
+    seen = []
+    for batch in range(4):
+        names = [f"S{i}" for i in rng.permutation(8)[:6]]
+        counts = rng.integers(0, 9, size=len(names))
+        n = int(counts.sum())
+        feats = rng.standard_normal((n, 6)).astype(np.float32)
+        feats[:, 0] = np.arange(n)  # request id in column 0
+        for s, c in zip(names, counts):
+            if c and s not in seen:
+                seen.append(s)
+        order, preds = client.process_arrays(names, counts, feats)
+        slots = [client.symbol_to_idx.get(s, -1) if c else -1 for s, c in zip(names, counts)]
+        assert list(client.symbol_to_idx) == seen[:capacity]
+        assert order.tolist() == list(response_order(slots, counts.tolist()))
+        want = np.zeros((n, 4))
+        base = np.concatenate([[0], np.cumsum(counts)])
+        for i, sl in enumerate(slots):
+            if sl >= 0:
+                want[base[i]:base[i + 1]] = feats[base[i]:base[i + 1], :4]
+        assert np.array_equal(preds, want[order])
+    # every tick's runs hold a symbol's requests in order (ids in column 0)
+    for runs, feats in client.ticks:
+        for r in range(len(runs.slot_ids)):
+            ids = feats[runs.run_off[r]:runs.run_off[r + 1], 0]
+            assert np.all(np.diff(ids) == 1)
+
+
+def test_process_batch_response_shape():
+    client = _client(capacity=2, max_rows=4, F=3)
+    reqs = {"A": [PendingRequest(10 + k, "A", [k, 0.5, 1.0]) for k in range(5)],
+            "B": [PendingRequest(20, "B", [7.0, 0.0, 0.0])],
+            "C": [PendingRequest(30, "C", [9.0, 9.0, 9.0])],   # past capacity: zeros
+            "D": []}
+    client.num_outputs = 4
+    client.num_features = 3
+
+    def tick(runs, rows, feats):
+        return np.concatenate([feats, np.ones((len(feats), 1))], axis=1).astype(np.float64)
+
+    client._tick_rows = tick
+    resp = client.process_batch(reqs)
+    assert resp.unique_ids == [30, 10, 20, 11, 12, 13, 14]
+    assert resp.predictions[0] == [0.0] * 4
+    assert resp.predictions[1] == [0.0, 0.5, 1.0, 1.0]
+    assert resp.predictions[2] == [7.0, 0.0, 0.0, 1.0]
+    assert client.process_batch({}).unique_ids == []
+    assert client.process_batch({"E": []}).unique_ids == []
+
+
+def test_round_chunks_cover_rounds_within_max_rows():
+    rng = np.random.default_rng(0)
+    for max_rows in (4, 9, 33):
+        client = _client(capacity=64, max_rows=max_rows)
+        for _ in range(20):
+            counts = rng.integers(1, 12, size=rng.integers(1, max_rows + 1))
+            chunks = client._round_chunks(counts)
+            assert chunks[0][0] == 0 and chunks[-1][1] == counts.max()
+            assert all(a[1] == b[0] for a, b in zip(chunks, chunks[1:]))
+            for k0, k1 in chunks:
+                assert int(np.clip(counts - k0, 0, k1 - k0).sum()) <= max_rows or k1 == k0 + 1

@@ -1,18 +1,13 @@
-"""GPU parity of the ensemble engine (hackathon_amd.engine / .client) against
-the oracle and the reference's golden vectors.
+"""GPU parity of the ensemble engine (hackathon_amd.engine / .client /
+.model) against the oracle and the reference's golden vectors, at the small
+and mid widths (the default dims: test_default_dims_gpu.py).
 
 fp32 path: predictions within rtol 1e-5 of the reference with an absolute
-floor of 2e-5 for predictions near zero (|d| <= 2e-5 + 1e-5 |ref|); state
-leaves within the same bound scaled by 10 (the state accumulates 16 steps of
-reassociated sums). At the default dimensions the RetNet tower is
-ill-conditioned in fp32 (per-head RMSNorm of near-cancelling contractions):
-independent fp32 evaluations of the reference algorithm scatter by up to
-~1e-4 around the float64 result. There a prediction also passes when its
-distance to the reference's float64 result is within 4x the scatter of two
-independent fp32 evaluations (the reference's own fp32 run and the oracle's)
-at that tower and step. bf16 path (CastLinear semantics): mean squared error
-against the fp32 reference below 1e-3 of the predictions' mean square.
-"""
+floor of 1e-6 for predictions near zero (|d| <= 1e-6 + 1e-5 |ref|; 1e-5 at
+hidden 256, where the reference's own fp32 run scatters that far from its
+float64 result); state leaves within the same bound scaled by 10 (the state
+accumulates 16 steps of reassociated sums). Reduced precision (CastLinear bf16 / fp16): against the
+reference's own converted model, bars in test_castlinear_small_fixture."""
 
 from pathlib import Path
 
@@ -26,7 +21,11 @@ from oracle.client import OracleClient
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
-P_RTOL, P_ATOL = 1e-5, 2e-5
+P_RTOL, P_ATOL = 1e-5, 1e-6
+# At hidden 256 the reference's own fp32 model is up to 1e-5 absolute from its
+# float64 result (beyond 1e-5 relative by up to 7.4e-6, measured over 12
+# steps of 40 rows), so the mid-width tests take a 1e-5 absolute floor.
+MID_ATOL = 1e-5
 
 
 def _close(got, want, rtol, atol, what):
@@ -205,7 +204,7 @@ def test_persistent_slstm_skewed_runs_fp32(dev):
         got = client.process_batch(reqs)
         want_ids, want_preds = oracle.process_batch(reqs)
         assert got.unique_ids == want_ids
-        _close(torch.tensor(got.predictions), torch.tensor(want_preds), P_RTOL, P_ATOL,
+        _close(torch.tensor(got.predictions), torch.tensor(want_preds), P_RTOL, MID_ATOL,
                f"batch {b} preds")
     eng.check()
     for i, (leaf, want) in enumerate(zip(om.flatten(eng.export_state(0, capacity)),
@@ -213,97 +212,42 @@ def test_persistent_slstm_skewed_runs_fp32(dev):
         if want.dtype == torch.int32:
             assert torch.equal(leaf.cpu(), want), f"leaf {i}"
         else:
-            _close(leaf, want, 10 * P_RTOL, 10 * P_ATOL, f"state leaf {i} {tuple(want.shape)}")
+            _close(leaf, want, 10 * P_RTOL, 10 * MID_ATOL, f"state leaf {i} {tuple(want.shape)}")
     eng.close()
 
 
-def test_bf16_path_mse(dev, small_params):
-    from hackathon_amd.client import NnInferenceClient
-
-    cfg = spec.SMALL
-    eng = _engine(cfg, small_params, capacity=8, dtype="bf16", max_rows=64)
-    client = NnInferenceClient(8, engine=eng)
-    ref32 = OracleClient(om.Params(small_params), cfg, 8)
-    ref16 = OracleClient(om.Params(small_params, lp="bf16"), cfg, 8)
-    rng = np.random.default_rng(11)
-    symbols = [f"S{i}" for i in range(8)]
-    se32 = se16 = ms = 0.0
-    for b in range(5):
-        reqs = _requests(rng, symbols, 48, 1000 * b, cfg.num_features)
-        got = torch.tensor(client.process_batch(reqs).predictions, dtype=torch.float64)
-        ids32, p32 = ref32.process_batch(reqs)
-        _, p16 = ref16.process_batch(reqs)
-        p32, p16 = torch.tensor(p32, dtype=torch.float64), torch.tensor(p16, dtype=torch.float64)
-        se32 += float(((got - p32) ** 2).sum())
-        se16 += float(((got - p16) ** 2).sum())
-        ms += float((p32 ** 2).sum())
-    print(f"bf16 path: MSE vs fp32 ref {se32:.3e}, vs bf16-emulated ref {se16:.3e}, signal {ms:.3e}")
-    assert se32 <= 1e-3 * ms
-    assert se16 <= se32 + 1e-12
-    eng.close()
-
-
-def test_default_dims_fp32_golden(dev):
-    # The reference's CPU-runnable configuration at default dims (4 symbols),
-    # first 4 steps, against the reference's own predictions (fp32 and
-    # float64, tests/golden/make_golden.py).
-    fx = np.load(GOLDEN / "default.npz")
-    cfg = spec.DEFAULT
-    params = weights.generate(cfg, 0)
+@pytest.mark.parametrize("lp", ["bf16", "fp16"])
+def test_castlinear_small_fixture(dev, small_params, lp):
+    """Engine in CastLinear mode against the reference's own
+    convert_linears(model, dtype) run (tests/golden/small_lp.npz, the 16
+    masked steps of small.npz), through the reference's model call shape.
+    Bars: the engine's mean squared distance from the reference's
+    reduced-precision predictions at most 1% of that result's distance from
+    fp32, and the engine's distance from fp32 at most 1.1x the reference's
+    own (measured 0.15% and 1.0x for bf16, 5% and 1.06x for fp16)."""
     from hackathon_amd.model import MultiTowerModel
 
-    model = MultiTowerModel(cfg, capacity=4, linear_dtype="fp32", weights=params)
-    e = model.engine
-    st = model.init_state(4, dev)
-    P32 = om.Params(params)
-    s32 = om.init_state(cfg, 4)
-    for t in range(4):
-        x = torch.from_numpy(fx[f"x/{t}"])
-        preds, st = model(x.to(dev), st)
-        preds = preds.cpu().double()
-        ref32 = torch.from_numpy(fx[f"preds/{t}"]).double()
-        ref64 = torch.from_numpy(fx[f"preds64/{t}"]).double()
-        with torch.inference_mode():
-            o32, s32 = om.forward(P32, cfg, x, s32)
-        spread = torch.maximum((ref32 - ref64).abs(), (o32.double() - ref64).abs()).max(0).values
-        near_ref = (preds - ref32).abs() <= P_ATOL + P_RTOL * ref32.abs()
-        near_exact = (preds - ref64).abs() <= 4 * spread[None, :]
-        ok = near_ref | near_exact
-        assert bool(ok.all()), (
-            f"default step {t}: |gpu-ref32| {(preds - ref32).abs().max(0).values.tolist()}, "
-            f"|gpu-ref64| {(preds - ref64).abs().max(0).values.tolist()}, fp32 spread {spread.tolist()}")
-    e.check()
-    e.close()
-
-
-def test_default_dims_fp32_past_log_cap(dev):
-    """Default dims, 4 symbols, 12 steps against the oracle: past the
-    8-entry pending-update log, so matrix-state tiles are written back and
-    read again (every scan instance of the default dims, including the
-    256-row float2 tiles, on a non-zero state)."""
-    cfg = spec.DEFAULT
-    params = weights.generate(cfg, 0)
-    from hackathon_amd.model import MultiTowerModel
-
-    model = MultiTowerModel(cfg, capacity=4, linear_dtype="fp32", weights=params)
-    e = model.engine
-    st = model.init_state(4, dev)
-    P32 = om.Params(params)
-    s32 = om.init_state(cfg, 4)
-    rng = np.random.default_rng(5)
-    for t in range(12):
-        x = torch.from_numpy(
-            np.clip(rng.standard_normal((4, cfg.num_features)), -5, 5).astype(np.float32))
-        got, st = model(x.to(dev), st)
-        got = got.cpu()
-        with torch.inference_mode():
-            want, s32 = om.forward(P32, cfg, x, s32)
-        # |d| / (|ref| + 2): the default dims' fp32 RetNet scatter (module
-        # docstring) stays near 2.5e-5 of it; a wrong tile is of order 1
-        rel = float(((got.double() - want.double()).abs() / (want.double().abs() + 2)).max())
-        assert rel <= 1e-4, f"default dims step {t}: |d| / (|ref| + 2) = {rel:.3e}"
-    e.check()
-    e.close()
+    fx = np.load(GOLDEN / "small_lp.npz")
+    f32 = np.load(GOLDEN / "small.npz")
+    model = MultiTowerModel(spec.SMALL, capacity=6, linear_dtype=lp, weights=small_params)
+    state = model.init_state(6, dev)
+    got, ref, r32 = [], [], []
+    for t in range(16):
+        mask = torch.from_numpy(fx[f"mask/{t}"])
+        preds, state = model(torch.from_numpy(fx[f"x/{t}"]).to(dev), state, mask)
+        got.append(preds.cpu()[mask].double())
+        ref.append(torch.from_numpy(fx[f"{lp}/preds/{t}"])[mask].double())
+        r32.append(torch.from_numpy(f32[f"preds/{t}"])[mask].double())
+    model.engine.check()
+    model.close()
+    got, ref, r32 = torch.cat(got), torch.cat(ref), torch.cat(r32)
+    e_lp = float(((got - ref) ** 2).mean())
+    e_32 = float(((got - r32) ** 2).mean())
+    r_32 = float(((ref - r32) ** 2).mean())
+    print(f"{lp}: MSE engine-vs-reference {e_lp:.3e}, engine-vs-fp32 {e_32:.3e}, "
+          f"reference-vs-fp32 {r_32:.3e}")
+    assert e_lp <= (0.01 if lp == "bf16" else 0.1) * r_32
+    assert e_32 <= 1.1 * r_32
 
 
 def test_state_roundtrip_and_reset(dev, small_params):

@@ -17,7 +17,8 @@ from oracle import model as om
 from oracle.client import OracleClient
 
 pytestmark = pytest.mark.gpu
-P_RTOL, P_ATOL = 1e-5, 2e-5
+# hidden 256: the reference's own fp32 run is up to 1e-5 absolute from float64
+P_RTOL, P_ATOL = 1e-5, 1e-5
 MID = spec.ModelConfig(hidden_size=256, proj_size=512, tower_depth=2, num_heads=8,
                        num_features=7)
 
