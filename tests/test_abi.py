@@ -36,6 +36,7 @@ def test_library_exports_every_declared_symbol():
 def test_python_binding_covers_header():
     from hackathon_amd import _lib
     import hackathon_amd.engine  # noqa: F401  (registers the engine signatures)
+    import hackathon_amd.weights  # noqa: F401  (registers the host-side helpers)
 
     assert set(declared()) <= set(_lib.declared_symbols())
     lib = _lib.lib()
