@@ -20,6 +20,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -30,6 +31,32 @@
 
 namespace hk {
 namespace {
+
+// Staging area of hk_engine_load_param_noalloc: 4 Mi fp32 values (16 MiB) in
+// every GPU's memory for the life of the process. Host code never passes the
+// symbol itself to the device: each device's copy has its own address,
+// resolved once per device by scratch_on_current_device().
+constexpr int64_t kScratchFloats = 4LL << 20;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device.
+int scratch_on_current_device(float** out) {
+  int dev = 0;
+  HK_CHECK_HIP(hipGetDevice(&dev));
+  HK_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    HK_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return HK_OK;
+}
 
 enum TowerType { kXLSTM = 0, kMamba2 = 1, kRetNet = 2, kHawk = 3 };
 constexpr int kTowers = 4;
@@ -220,6 +247,8 @@ struct TowerWS {
 struct Engine {
   Dims d{};
   int capacity = 0, max_rows = 0, max_runs = 0;
+  int device = -1;            // the device current at creation (owns every buffer)
+  float* scratch = nullptr;   // that device's address of `scratch`
   // CastLinear mode (example_model.py:150-157): lowp = the converted
   // linears store and compute in lp_fmt (bf16 or fp16), else all fp32.
   bool lowp = false;
@@ -1068,6 +1097,8 @@ int hk_engine_create(const int* cfg, int n_cfg, void** out) {
     return st;
   }
   e->seen.assign(e->capacity, 0);
+  HK_CHECK_HIP(hipGetDevice(&e->device));
+  HK_TRY(hk::scratch_on_current_device(&e->scratch));
   *out = e.release();
   return HK_OK;
 }
@@ -1116,6 +1147,45 @@ int hk_engine_load_param(void* h, int tower, int layer, int slot, const float* h
     std::vector<float> v(host, host + numel);
     for (auto& x : v) x = hk::round_lp(x, e.lp_fmt);
     HK_CHECK_HIP(hipMemcpy(s->ptr, v.data(), (size_t)numel * 4, hipMemcpyHostToDevice));
+  } else {
+    HK_CHECK_HIP(hipMemcpy(s->ptr, host, (size_t)numel * 4, hipMemcpyHostToDevice));
+  }
+  s->bound = true;
+  return HK_OK;
+}
+
+// hk_engine_load_param with no device allocation: CastLinear weights travel
+// through this device's `scratch` array, kScratchFloats values at a time
+// (copy in, convert into the slot, wait, next chunk), so a slot of any size
+// binds through the 16 MiB array; biases are rounded in place in the slot and
+// fp32 slots copied straight in. Calls on one device share its array: two
+// calls that overlap in time race.
+int hk_engine_load_param_noalloc(void* h, int tower, int layer, int slot, const float* host,
+                                 int64_t numel) {
+  HK_REQUIRE(h && host, "hk_engine_load_param_noalloc: null argument");
+  Engine& e = *static_cast<Engine*>(h);
+  hk::Slot* s = hk::find_slot(e, tower, layer, slot);
+  HK_REQUIRE(s, "hk_engine_load_param_noalloc: no slot (%d, %d, %d)", tower, layer, slot);
+  HK_REQUIRE(numel == s->def.numel,
+             "hk_engine_load_param_noalloc: %s expects %lld values, got %lld", s->def.name,
+             (long long)s->def.numel, (long long)numel);
+  int dev = -1;
+  HK_CHECK_HIP(hipGetDevice(&dev));
+  HK_REQUIRE(dev == e.device && e.scratch != nullptr,
+             "hk_engine_load_param_noalloc: the engine lives on device %d, device %d is current",
+             e.device, dev);
+  if (s->def.lp && e.lowp) {
+    uint16_t* dst = static_cast<uint16_t*>(s->ptr);
+    for (int64_t off = 0; off < numel; off += hk::kScratchFloats) {
+      const int64_t n = std::min(hk::kScratchFloats, numel - off);
+      HK_CHECK_HIP(hipMemcpy(e.scratch, host + off, (size_t)n * 4, hipMemcpyHostToDevice));
+      HK_TRY(hk::to_lp(e.scratch, dst + off, n, e.lp_fmt, nullptr));
+      HK_CHECK_HIP(hipStreamSynchronize(nullptr));  // the next chunk overwrites the array
+    }
+  } else if (s->def.lp_bias && e.lowp) {
+    HK_CHECK_HIP(hipMemcpy(s->ptr, host, (size_t)numel * 4, hipMemcpyHostToDevice));
+    HK_TRY(hk::round_lp_inplace(static_cast<float*>(s->ptr), numel, e.lp_fmt, nullptr));
+    HK_CHECK_HIP(hipStreamSynchronize(nullptr));
   } else {
     HK_CHECK_HIP(hipMemcpy(s->ptr, host, (size_t)numel * 4, hipMemcpyHostToDevice));
   }

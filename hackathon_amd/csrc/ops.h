@@ -95,6 +95,8 @@ int mlstm_qkv_if(const float* x_conv, const float* x_m, int64_t ld_xm, const flo
 
 // 16-bit copy (LpFmt lp_fmt) of an fp32 matrix (weights at bind time).
 int to_lp(const float* src, uint16_t* dst, int64_t n, int lp_fmt, hipStream_t s);
+// v[i] = v[i] rounded through the 16-bit format lp_fmt, in place.
+int round_lp_inplace(float* v, int64_t n, int lp_fmt, hipStream_t s);
 // fill with a constant
 int fill_f32(float* dst, int64_t n, float v, hipStream_t s);
 

@@ -500,6 +500,12 @@ __global__ void to_lp_kernel(const float* __restrict__ src, uint16_t* __restrict
     dst[i] = f32_to_lp_bits(src[i], lp_fmt);
 }
 
+__global__ void round_lp_inplace_kernel(float* __restrict__ v, int64_t n, int lp_fmt) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    v[i] = round_lp(v[i], lp_fmt);
+}
+
 __global__ void fill_f32_kernel(float* __restrict__ dst, int64_t n, float v) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -716,6 +722,13 @@ bool mlstm_qkv_if_supported(int inner, int n_out, int segs) {
 int to_lp(const float* src, uint16_t* dst, int64_t n, int lp_fmt, hipStream_t s) {
   if (n == 0) return HK_OK;
   hipLaunchKernelGGL(to_lp_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n, lp_fmt);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int round_lp_inplace(float* v, int64_t n, int lp_fmt, hipStream_t s) {
+  if (n == 0) return HK_OK;
+  hipLaunchKernelGGL(round_lp_inplace_kernel, dim3(grid_for(n)), dim3(256), 0, s, v, n, lp_fmt);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }

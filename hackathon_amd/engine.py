@@ -28,6 +28,7 @@ _lib.register("hk_engine_create", c_int, [ctypes.POINTER(c_int), c_int, ctypes.P
 _lib.register("hk_engine_destroy", c_int, [c_void_p])
 _lib.register("hk_engine_param_numel", c_int, [c_void_p, c_int, c_int, c_int, ctypes.POINTER(c_int64)])
 _lib.register("hk_engine_load_param", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_int64])
+_lib.register("hk_engine_load_param_noalloc", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_int64])
 _lib.register("hk_engine_state_numel", c_int, [c_void_p, c_int, c_int, ctypes.POINTER(c_int64)])
 _lib.register(
     "hk_engine_state_copy", c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p]
@@ -213,18 +214,21 @@ class Engine:
         return _lib.current_stream(self.device)
 
     # -- weights -------------------------------------------------------------------
-    def _load(self, tower: int, layer: int, slot: int, t: torch.Tensor):
+    def load_param(self, tower: int, layer: int, slot: int, t: torch.Tensor, noalloc: bool = False):
+        """Bind one packed weight slot (hk_engine_load_param, or with noalloc
+        hk_engine_load_param_noalloc, which allocates no device memory)."""
         t = t.detach().to(torch.float32).contiguous().cpu()
         n = c_int64()
         _lib.check(_lib.lib().hk_engine_param_numel(self._h, tower, layer, slot, ctypes.byref(n)), "param_numel")
         if t.numel() != n.value:
             raise ValueError(f"slot ({tower},{layer},{slot}) expects {n.value} values, got {t.numel()}")
+        fn = "hk_engine_load_param_noalloc" if noalloc else "hk_engine_load_param"
         with torch.cuda.device(self.device):
-            _lib.check(_lib.lib().hk_engine_load_param(self._h, tower, layer, slot, t.data_ptr(), t.numel()),
-                       "hk_engine_load_param")
+            _lib.check(getattr(_lib.lib(), fn)(self._h, tower, layer, slot, t.data_ptr(), t.numel()), fn)
 
-    def load_weights(self, params: dict[str, torch.Tensor]):
-        """Bind a full parameter set keyed by the reference's state_dict names."""
+    def load_weights(self, params: dict[str, torch.Tensor], noalloc: bool = False):
+        """Bind a full parameter set keyed by the reference's state_dict names
+        (noalloc: through the entry point that allocates no device memory)."""
         cfg = self.cfg
         fpad = (cfg.num_features + 63) // 64 * 64
         for t, ltype in enumerate(TOWER_TYPES):
@@ -234,14 +238,14 @@ class Engine:
             up_pad[:, : up.shape[1]] = up
             for i, arr in enumerate([up_pad, params[pre + "input_up.bias"], params[pre + "input_down.weight"],
                                      params[pre + "input_down.bias"]]):
-                self._load(t, -1, i, arr)
+                self.load_param(t, -1, i, arr, noalloc=noalloc)
             for b in range(cfg.tower_depth):
                 bp = f"{pre}blocks.{b}."
                 arrs = [params[bp + n] for n in _COMMON] + _layer_slots(cfg, ltype, params, bp + "layer.")
                 for i, arr in enumerate(arrs):
-                    self._load(t, b, i, arr)
-        self._load(-1, -1, 0, params["output_proj.weight"].reshape(-1))
-        self._load(-1, -1, 1, params["output_proj.bias"].reshape(-1))
+                    self.load_param(t, b, i, arr, noalloc=noalloc)
+        self.load_param(-1, -1, 0, params["output_proj.weight"].reshape(-1), noalloc=noalloc)
+        self.load_param(-1, -1, 1, params["output_proj.bias"].reshape(-1), noalloc=noalloc)
         self._loaded = True
 
     # -- state -----------------------------------------------------------------------

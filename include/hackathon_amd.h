@@ -175,6 +175,18 @@ int hk_engine_param_numel(void* handle, int tower, int layer, int slot, int64_t*
 int hk_engine_load_param(void* handle, int tower, int layer, int slot, const float* host,
                          int64_t numel);
 
+/* hk_engine_load_param without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under graph capture, serving loops that swap weights in place, harnesses
+ * that forbid hipMalloc). CastLinear weights are staged through a 16 MiB
+ * array that the library holds in every GPU's memory for the life of the
+ * process, 4 Mi values at a time, so a slot of any size binds; results are
+ * bit-identical to hk_engine_load_param's. Synchronous. The engine's device
+ * must be current. Calls on one GPU share its array: calls that overlap in
+ * time race. */
+int hk_engine_load_param_noalloc(void* handle, int tower, int layer, int slot, const float* host,
+                                 int64_t numel);
+
 /* Elements per slot of state leaf `leaf` of tower `tower`. */
 int hk_engine_state_numel(void* handle, int tower, int leaf, int64_t* per_slot);
 
