@@ -524,6 +524,45 @@ int hk_block_linear(const float* x, const float* weight, const float* bias, floa
   return HK_OK;
 }
 
+// CastLinear.forward on 16-bit operands: the engine's projection GEMM with
+// its CastLinear epilogue. Workspace layout: kCastArrivals arrival counters,
+// then split-K partial sums.
+int hk_cast_linear(const uint16_t* x, const uint16_t* w, const float* bias, float* out, int M,
+                   int N, int K, int fmt, void* workspace, int64_t workspace_bytes,
+                   void* stream) {
+  constexpr int64_t kCastArrivals = 1 << 16;
+  HK_REQUIRE(x && w && out, "hk_cast_linear: null operand");
+  HK_REQUIRE(M >= 0 && N > 0 && K > 0 && K % 64 == 0,
+             "hk_cast_linear: bad shape M=%d N=%d K=%d (K a multiple of 64)", M, N, K);
+  HK_REQUIRE(fmt == hk::kLpBF16 || fmt == hk::kLpF16, "hk_cast_linear: format %d", fmt);
+  HK_REQUIRE(hk::aligned16(x) && hk::aligned16(w), "hk_cast_linear: operands must be 16-byte aligned");
+  HK_REQUIRE(workspace == nullptr || workspace_bytes >= kCastArrivals * 4,
+             "hk_cast_linear: a workspace needs at least %lld bytes", (long long)kCastArrivals * 4);
+  if (M == 0) return HK_OK;
+  hk::GemmArgs g;
+  g.type = fmt == hk::kLpF16 ? hk::GemmType::kF16 : hk::GemmType::kBF16;
+  g.A = x;
+  g.lda = K;
+  g.W = w;
+  g.ldw = K;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.ep.bias = bias;
+  g.ep.round_lp = true;
+  g.ep.lp_fmt = fmt;
+  g.ep.out = out;
+  g.ep.ldo = N;
+  hk::GemmWorkspace ws;
+  if (workspace != nullptr) {
+    ws.arrivals = static_cast<int*>(workspace);
+    ws.arrival_elems = kCastArrivals;
+    ws.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCastArrivals * 4);
+    ws.partial_elems = (workspace_bytes - kCastArrivals * 4) / 4;
+  }
+  return hk::gemm(g, ws, (hipStream_t)stream);
+}
+
 int hk_rglru_step(float* h, const float* x, const float* gate_i, const float* gate_r,
                   const float* a, float c, const uint8_t* mask, float* out, int batch, int width,
                   void* stream) {

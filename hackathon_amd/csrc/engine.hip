@@ -19,6 +19,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -283,7 +284,11 @@ struct Engine {
   int* d_act2 = nullptr;     // [max_rows]
   unsigned long long* d_xch = nullptr;   // [max_rows][H]: sLSTM h exchange words
   unsigned long long* d_xch2 = nullptr;  // the same for the second xLSTM group
-  unsigned int xch_tag[2] = {0, 0};      // tag of the last sLSTM launch on d_xch / d_xch2
+  // Exchange tags: eager launches count up from 1 per buffer below
+  // kGraphTag0; captured launches take tags from kGraphTag0 up, each used by
+  // one captured launch only (see GraphEntry).
+  unsigned int xch_tag[2] = {0, 0};      // tag of the last eager sLSTM launch on d_xch / d_xch2
+  unsigned int graph_tag_next = 0x80000000u;
   bool sl_overlap = false;  // the two groups' persistent launches can be co-resident together
   int* d_err = nullptr;      // [1]: set by a kernel whose barrier timed out
   uint64_t* d_trace = nullptr;  // HK_TRACE_SLSTM: per-step stamps of layer 0's sLSTM
@@ -300,6 +305,29 @@ struct Engine {
   // Hawk.
   static constexpr int kSide = 3;
   hipStream_t side[kSide] = {nullptr, nullptr, nullptr};
+  // hipGraph replay of small ticks (the reference captures its whole step
+  // once and replays it per round, example_model.py:444-492). A tick's work
+  // depends on its run lengths alone (the descriptors, features and
+  // predictions sit in fixed device buffers), so graphs are cached by that
+  // key. Each entry holds two executables that differ only in the tags of
+  // their persistent sLSTM launches, replayed alternately: between two
+  // replays of one executable the other one rewrote every exchange word the
+  // first polls, with other tags, so a poll never accepts a word left over
+  // from the previous replay of its own executable.
+  struct GraphEntry {
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
+    int next = 0;
+    uint64_t last_use = 0;
+  };
+  int graph_rows = 0;   // ticks of at most this many rows replay graphs (0: never)
+  int graph_cap = 0;    // shapes cached at most (least recently used evicted)
+  std::map<std::vector<int>, GraphEntry> graphs;
+  uint64_t graph_clock = 0;
+  int64_t graph_captures = 0, graph_replays = 0;
+  bool capturing = false;
+  hipStream_t cap_s = nullptr;   // capture origin
+  float* g_feat = nullptr;       // [max_rows][F] a replayed tick's features
+  float* g_pred = nullptr;       // [max_rows][4] its predictions
   hipEvent_t fork_ev = nullptr;
   hipEvent_t join_ev[kSide] = {nullptr, nullptr, nullptr};
   // Where two persistent sLSTM launches cannot be co-resident at once, the
@@ -313,6 +341,10 @@ struct Engine {
   size_t prof_used[5] = {0, 0, 0, 0, 0};
 
   ~Engine() {
+    for (auto& kv : graphs)
+      for (auto& x : kv.second.exec)
+        if (x) (void)hipGraphExecDestroy(x);
+    if (cap_s) (void)hipStreamDestroy(cap_s);
     for (auto& st : side)
       if (st) (void)hipStreamDestroy(st);
     if (fork_ev) (void)hipEventDestroy(fork_ev);
@@ -439,6 +471,9 @@ int build_workspace(Engine& e) {
     HK_CHECK_HIP(hipMemset(w.gemm_ws.arrivals, 0, (size_t)w.gemm_ws.arrival_elems * 4));
   }
   e.FE = e.alloc_act(R * d.Fpad, false);
+  e.g_feat = e.alloc_f(R * d.F);
+  e.g_pred = e.alloc_f(R * kTowers);
+  if (!e.g_feat || !e.g_pred) return HK_ERR_HIP;
   if (any_null(e.FE, false, e.lowp)) return HK_ERR_HIP;
   e.d_desc = static_cast<int*>(e.alloc_bytes((size_t)e.stage_ints() * 4));
   e.d_xch = static_cast<unsigned long long*>(e.alloc_bytes((size_t)e.max_rows * d.H * 8));
@@ -467,6 +502,7 @@ int build_workspace(Engine& e) {
     HK_CHECK_HIP(hipEventCreateWithFlags(&e.join_ev[i], hipEventDisableTiming));
   }
   HK_CHECK_HIP(hipEventCreateWithFlags(&e.fork_ev, hipEventDisableTiming));
+  HK_CHECK_HIP(hipStreamCreateWithFlags(&e.cap_s, hipStreamNonBlocking));
   for (auto& v : e.sl_ev) {
     v.assign(d.D, nullptr);
     for (auto& ev : v) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
@@ -666,15 +702,22 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
                       w.GIN, 4 * H, s));
   if (slstm_persist_supported(H, d.nh_s)) {
     if (ord.wait) HK_CHECK_HIP(hipStreamWaitEvent(s, ord.wait, 0));
-    // Each exchange buffer has its own tag sequence and is used by one
-    // group, on one stream.
-    unsigned int& tag = e.xch_tag[xch == e.d_xch2 ? 1 : 0];
-    if (++tag == 0) {
-      // Tags wrapped: clear this buffer (words that could carry a reused
-      // tag). Every earlier launch on it is ordered before this point by
-      // stream order.
-      HK_CHECK_HIP(hipMemsetAsync(xch, 0, (size_t)e.max_rows * H * 8, s));
-      tag = 1;
+    // Each exchange buffer has its own eager tag sequence and is used by
+    // one group, on one stream; a launch being captured takes a tag no other
+    // launch uses.
+    unsigned int tag;
+    if (e.capturing) {
+      tag = e.graph_tag_next++;
+    } else {
+      unsigned int& t = e.xch_tag[xch == e.d_xch2 ? 1 : 0];
+      if (++t >= 0x80000000u) {
+        // Eager tags wrapped: clear this buffer (words that could carry a
+        // reused tag). Every earlier launch on it is ordered before this
+        // point by stream order.
+        HK_CHECK_HIP(hipMemsetAsync(xch, 0, (size_t)e.max_rows * H * 8, s));
+        t = 1;
+      }
+      tag = t;
     }
     HK_TRY(timed(e, 3, s, [&] {
       return slstm_persist(r, g.act_dev, (int)act.size(), w.GIN, H, d.nh_s,
@@ -960,6 +1003,118 @@ int xlstm_split_point(const int* run_off, int n_runs) {
     }
   }
   return best < kGain * whole ? best_k : n_runs;
+}
+
+// What a tick's device work depends on besides its buffers: the run
+// layout (counts, the xLSTM groups) and the per-step active-run counts.
+struct TickShape {
+  int n_runs = 0, n_rows = 0, steps = 0;
+  int split = 0, row_split = 0, steps2 = 0;
+  std::vector<int> act, act1, act2;
+};
+
+// The device work of one tick on stream s, descriptors already in d_desc:
+// feature staging, every tower (forked to the side streams and joined back),
+// predictions into preds_dev.
+int enqueue_tick(Engine& e, const TickShape& sh, const float* features_dev, float* preds_dev,
+                 hipStream_t s) {
+  Group all;
+  all.r = Runs{e.d_slots, e.d_off, sh.n_runs, sh.n_rows, sh.steps};
+  all.act_dev = e.d_act;
+  all.act = sh.act;
+  HK_TRY(stage_features(features_dev, sh.n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, e.lp_fmt, s));
+  HK_CHECK_HIP(hipEventRecord(e.fork_ev, s));
+  for (int i = 0; i < Engine::kSide; ++i) HK_CHECK_HIP(hipStreamWaitEvent(e.side[i], e.fork_ev, 0));
+  if (sh.split < sh.n_runs) {
+    Group g1, g2;
+    g1.r = Runs{e.d_slots, e.d_off, sh.split, sh.row_split, sh.steps};
+    g1.act_dev = e.d_act1;
+    g1.act = sh.act1;
+    g2.r = Runs{e.d_slots + sh.split, e.d_off2, sh.n_runs - sh.split, sh.n_rows - sh.row_split,
+                sh.steps2};
+    g2.act_dev = e.d_act2;
+    g2.act = sh.act2;
+    g2.row0 = sh.row_split;
+    HK_TRY(run_towers(e, all, g1, &g2, s, preds_dev));
+  } else {
+    HK_TRY(run_towers(e, all, all, nullptr, s, preds_dev));
+  }
+  for (int i = 0; i < Engine::kSide; ++i) {
+    HK_CHECK_HIP(hipEventRecord(e.join_ev[i], e.side[i]));
+    HK_CHECK_HIP(hipStreamWaitEvent(s, e.join_ev[i], 0));
+  }
+  return HK_OK;
+}
+
+// Captures one tick of shape sh (features from g_feat, predictions to
+// g_pred) into an executable graph.
+int capture_tick(Engine& e, const TickShape& sh, hipGraphExec_t* out) {
+  *out = nullptr;
+  HK_CHECK_HIP(hipStreamBeginCapture(e.cap_s, hipStreamCaptureModeRelaxed));
+  e.capturing = true;
+  const int st = enqueue_tick(e, sh, e.g_feat, e.g_pred, e.cap_s);
+  e.capturing = false;
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(e.cap_s, &graph);
+  if (st != HK_OK) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return st;
+  }
+  if (end != hipSuccess) {
+    set_error("capture_tick: hipStreamEndCapture: %s", hipGetErrorString(end));
+    return HK_ERR_HIP;
+  }
+  const hipError_t inst = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (inst != hipSuccess) {
+    set_error("capture_tick: hipGraphInstantiate: %s", hipGetErrorString(inst));
+    return HK_ERR_HIP;
+  }
+  return HK_OK;
+}
+
+// A tick through the graph cache: features into g_feat, one graph launch
+// (captured on first sight of the shape), predictions out of g_pred, all on
+// stream s.
+int tick_replay(Engine& e, const std::vector<int>& key, const TickShape& sh,
+                const float* features_dev, float* preds_dev, hipStream_t s) {
+  auto it = e.graphs.find(key);
+  if (it == e.graphs.end()) {
+    // Two captures consume at most 2 * 2 * depth tags.
+    if (e.graph_tag_next > 0xFFFFFFFFu - 4u * (unsigned)e.d.D - 4u)
+      return enqueue_tick(e, sh, features_dev, preds_dev, s);  // tags exhausted: eager
+    if ((int)e.graphs.size() >= e.graph_cap) {
+      auto lru = e.graphs.begin();
+      for (auto j = e.graphs.begin(); j != e.graphs.end(); ++j)
+        if (j->second.last_use < lru->second.last_use) lru = j;
+      // its last replay must be done before the executable goes
+      HK_CHECK_HIP(hipStreamSynchronize(s));
+      for (auto& x : lru->second.exec)
+        if (x) HK_CHECK_HIP(hipGraphExecDestroy(x));
+      e.graphs.erase(lru);
+    }
+    Engine::GraphEntry g;
+    for (int p = 0; p < 2; ++p) {
+      const int st = capture_tick(e, sh, &g.exec[p]);
+      if (st != HK_OK) {
+        for (auto& x : g.exec)
+          if (x) (void)hipGraphExecDestroy(x);
+        return st;
+      }
+      ++e.graph_captures;
+    }
+    it = e.graphs.emplace(key, g).first;
+  }
+  Engine::GraphEntry& g = it->second;
+  g.last_use = ++e.graph_clock;
+  HK_CHECK_HIP(hipMemcpyAsync(e.g_feat, features_dev, (size_t)sh.n_rows * e.d.F * 4,
+                              hipMemcpyDeviceToDevice, s));
+  HK_CHECK_HIP(hipGraphLaunch(g.exec[g.next], s));
+  g.next ^= 1;
+  ++e.graph_replays;
+  HK_CHECK_HIP(hipMemcpyAsync(preds_dev, e.g_pred, (size_t)sh.n_rows * kTowers * 4,
+                              hipMemcpyDeviceToDevice, s));
+  return HK_OK;
 }
 
 Slot* find_slot(Engine& e, int tower, int layer, int slot) {
@@ -1425,30 +1580,50 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
                               s));
   HK_CHECK_HIP(hipEventRecord(e.stage_done[k], s));
 
-  hk::Group all;
-  all.r = hk::Runs{e.d_slots, e.d_off, n_runs, n_rows, steps};
-  all.act_dev = e.d_act;
-  all.act.assign(h_act, h_act + steps);
-  HK_TRY(hk::stage_features(features_dev, n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, e.lp_fmt, s));
-  HK_CHECK_HIP(hipEventRecord(e.fork_ev, s));
-  for (int i = 0; i < Engine::kSide; ++i) HK_CHECK_HIP(hipStreamWaitEvent(e.side[i], e.fork_ev, 0));
-  if (split < n_runs) {
-    hk::Group g1, g2;
-    g1.r = hk::Runs{e.d_slots, e.d_off, split, row_split, steps};
-    g1.act_dev = e.d_act1;
-    g1.act.assign(h_act1, h_act1 + steps);
-    g2.r = hk::Runs{e.d_slots + split, e.d_off2, n_runs - split, n_rows - row_split, steps2};
-    g2.act_dev = e.d_act2;
-    g2.act.assign(h_act2, h_act2 + steps2);
-    g2.row0 = row_split;
-    HK_TRY(hk::run_towers(e, all, g1, &g2, s, preds_dev));
-  } else {
-    HK_TRY(hk::run_towers(e, all, all, nullptr, s, preds_dev));
+  hk::TickShape sh;
+  sh.n_runs = n_runs;
+  sh.n_rows = n_rows;
+  sh.steps = steps;
+  sh.split = split;
+  sh.row_split = row_split;
+  sh.steps2 = steps2;
+  sh.act.assign(h_act, h_act + steps);
+  sh.act1.assign(h_act1, h_act1 + steps);
+  sh.act2.assign(h_act2, h_act2 + steps2);
+  if (e.graph_rows > 0 && n_rows <= e.graph_rows && e.prof == 0 && e.d_trace == nullptr) {
+    std::vector<int> key(n_runs);
+    for (int i = 0; i < n_runs; ++i) key[i] = run_off_host[i + 1] - run_off_host[i];
+    return hk::tick_replay(e, key, sh, features_dev, preds_dev, s);
   }
-  for (int i = 0; i < Engine::kSide; ++i) {
-    HK_CHECK_HIP(hipEventRecord(e.join_ev[i], e.side[i]));
-    HK_CHECK_HIP(hipStreamWaitEvent(s, e.join_ev[i], 0));
+  return hk::enqueue_tick(e, sh, features_dev, preds_dev, s);
+}
+
+// Replay small ticks through cached hipGraphs: ticks of at most max_rows
+// rows, at most max_graphs tick shapes cached (least recently used evicted);
+// max_rows 0 turns replay off and frees the cache.
+int hk_engine_graphs(void* h, int max_rows, int max_graphs) {
+  HK_REQUIRE(h, "hk_engine_graphs: null handle");
+  Engine& e = *static_cast<Engine*>(h);
+  HK_REQUIRE(max_rows >= 0 && max_graphs >= 0, "hk_engine_graphs: negative limit");
+  HK_REQUIRE(max_rows == 0 || max_graphs > 0, "hk_engine_graphs: replay needs a cache");
+  e.graph_rows = std::min(max_rows, e.max_rows);
+  e.graph_cap = max_graphs;
+  if (max_rows == 0 || (int)e.graphs.size() > max_graphs) {
+    HK_CHECK_HIP(hipDeviceSynchronize());
+    for (auto& kv : e.graphs)
+      for (auto& x : kv.second.exec)
+        if (x) HK_CHECK_HIP(hipGraphExecDestroy(x));
+    e.graphs.clear();
   }
+  return HK_OK;
+}
+
+int hk_engine_graph_info(void* h, int64_t* cached, int64_t* captures, int64_t* replays) {
+  HK_REQUIRE(h && cached && captures && replays, "hk_engine_graph_info: null argument");
+  Engine& e = *static_cast<Engine*>(h);
+  *cached = (int64_t)e.graphs.size();
+  *captures = e.graph_captures;
+  *replays = e.graph_replays;
   return HK_OK;
 }
 

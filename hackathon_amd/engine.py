@@ -37,6 +37,8 @@ _lib.register("hk_engine_reset_slots", c_int, [c_void_p, c_void_p, c_int, c_void
 _lib.register("hk_engine_tick", c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p])
 
 _lib.register("hk_engine_check", c_int, [c_void_p, c_void_p])
+_lib.register("hk_engine_graphs", c_int, [c_void_p, c_int, c_int])
+_lib.register("hk_engine_graph_info", c_int, [c_void_p] + [ctypes.POINTER(c_int64)] * 3)
 _lib.register("hk_engine_profile", c_int, [c_void_p, c_int])
 _lib.register("hk_engine_profile_read", c_int, [c_void_p, c_int, ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_double)])
 
@@ -361,6 +363,21 @@ class Engine:
         )
         _lib.check(st, "hk_engine_tick")
         return preds
+
+    def graphs(self, max_rows: int, max_graphs: int = 256):
+        """Replay ticks of at most max_rows rows through cached hipGraphs
+        (one capture per tick shape, at most max_graphs shapes cached); 0
+        turns replay off (the reference's captured step,
+        example_model.py:444-492)."""
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().hk_engine_graphs(self._h, max_rows, max_graphs), "hk_engine_graphs")
+
+    def graph_info(self) -> dict:
+        """{"cached", "captures", "replays"} of the graph cache."""
+        vals = [c_int64() for _ in range(3)]
+        _lib.check(_lib.lib().hk_engine_graph_info(self._h, *[ctypes.byref(v) for v in vals]),
+                   "hk_engine_graph_info")
+        return dict(zip(("cached", "captures", "replays"), (v.value for v in vals)))
 
     def check(self):
         """Wait for the current stream's work (every tick enqueued on it) and

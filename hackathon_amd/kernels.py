@@ -229,3 +229,37 @@ def slstm_step(state, i, f, z, o, mask=None):
     )
     _lib.check(st, "hk_slstm_step")
     return y
+
+
+_LP = {torch.bfloat16: 0, torch.float16: 1}
+
+
+def cast_linear(x, weight, bias=None, workspace=None):
+    """CastLinear.forward (example_model.py:92-95): F.linear(x.to(lp),
+    weight, bias).to(float32) for a weight held in bf16 or fp16.
+
+    x: fp32 [..., K] (cast to the weight's dtype, as CastLinear does);
+    weight: [N, K] bf16/fp16 contiguous; bias: [N] in the weight's dtype or
+    None; workspace: optional zero-filled uint8 CUDA tensor (>= 256 KiB) for
+    split-K. Returns fp32 [..., N]."""
+    assert weight.dtype in _LP, f"weight must be bf16 or fp16, got {weight.dtype}"
+    assert weight.dim() == 2 and weight.is_contiguous(), "weight must be a contiguous [N, K] matrix"
+    N, K = weight.shape
+    assert x.shape[-1] == K, f"x must end in {K}, got {tuple(x.shape)}"
+    dev = weight.device
+    if dev.type != "cuda":
+        raise _lib.HipLibraryError("cast_linear needs GPU tensors")
+    xl = x.reshape(-1, K).to(device=dev, dtype=weight.dtype).contiguous()
+    b = None
+    if bias is not None:
+        assert bias.dtype == weight.dtype and tuple(bias.shape) == (N,), "bias must be [N] in the weight's dtype"
+        b = bias.to(torch.float32).contiguous()
+    out = torch.empty(xl.shape[0], N, dtype=torch.float32, device=dev)
+    ws, ws_bytes = None, 0
+    if workspace is not None:
+        assert workspace.dtype == torch.uint8 and workspace.device == dev
+        ws, ws_bytes = workspace.data_ptr(), workspace.numel()
+    _lib.check(_lib.lib().hk_cast_linear(
+        xl.data_ptr(), weight.data_ptr(), _lib.ptr(b), out.data_ptr(), xl.shape[0], N, K,
+        _LP[weight.dtype], ws, ws_bytes, _lib.current_stream(dev)), "hk_cast_linear")
+    return out.reshape(*x.shape[:-1], N)

@@ -84,6 +84,19 @@ int hk_conv1d_step(float* state, const float* x, const float* weight, const floa
 int hk_block_linear(const float* x, const float* weight, const float* bias, float* out, int batch,
                     int blocks, int block_size, void* stream);
 
+/* CastLinear.forward (example_model.py:92-95) on operands already in the
+ * 16-bit format fmt (0 bf16, 1 fp16): out[m,n] = fp32 of round_fmt(sum_k
+ * x[m,k] w[n,k] + bias[n]) (fp32 accumulation, the bias added in fp32, one
+ * rounding to fmt, as torch's 16-bit linear rounds its result before the
+ * cast back to fp32). x [M,K], w [N,K] (nn.Linear layout), K a multiple of
+ * 64, both 16-byte aligned; bias [N] fp32 holding values representable in
+ * fmt (CastLinear's 16-bit bias), NULL = none; out [M,N] fp32. The engine's
+ * projection GEMM. workspace (NULL = none) lets it split K over several
+ * work-groups: workspace_bytes >= 256 KiB, zero-filled before its first use
+ * (calls leave it zeroed); calls sharing one workspace must not overlap. */
+int hk_cast_linear(const uint16_t* x, const uint16_t* w, const float* bias, float* out, int M,
+                   int N, int K, int fmt, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* RGLRU.forward after its two BlockLinears (model/hawk.py:31-37):
  * i = sigmoid(gate_i), r = sigmoid(gate_r), a_t = a ** (c * r),
  * h <- h * a_t + sqrt(1 - a_t^2) * (i * x); out (NULL = none) = new h on
@@ -210,6 +223,22 @@ int hk_engine_reset_slots(void* handle, const int* slots_host, int n, void* stre
  * tick exceeds max_rows / max_runs. */
 int hk_engine_tick(void* handle, const int* slot_ids_host, const int* run_off_host, int n_runs,
                    const float* features_dev, float* preds_dev, void* stream);
+
+/* hipGraph replay of small ticks. Replaces the reference's captured step
+ * (_capture_step / _replay_graph, example_model.py:444-492), which records
+ * one full-capacity round once and replays it for every round. Here ticks of
+ * at most max_rows rows are captured once per tick shape (the run lengths;
+ * descriptors, features and predictions go through fixed device buffers) and
+ * replayed from a cache of at most max_graphs shapes, least recently used
+ * evicted; hk_engine_tick then enqueues one copy in, one graph launch and
+ * one copy out. Results are bit-identical to the eager tick's. max_rows 0
+ * (the default) enqueues every tick's kernels eagerly and frees the cache.
+ * Not used while hk_engine_profile records. */
+int hk_engine_graphs(void* handle, int max_rows, int max_graphs);
+
+/* Shapes cached, graphs captured and ticks replayed so far. No reference
+ * counterpart (test and measurement support). */
+int hk_engine_graph_info(void* handle, int64_t* cached, int64_t* captures, int64_t* replays);
 
 /* Waits for the work enqueued on `stream` (a tick's stream: every tick joins
  * its side streams back into it, so this covers whole ticks; other work on

@@ -224,3 +224,48 @@ def test_refusal_guards(dev):
     with pytest.raises(AssertionError):
         hk.rglru_step(x, x, x, x, torch.zeros(8, device=dev),
                       mask=torch.ones(4, dtype=torch.int32, device=dev))
+
+
+def _ulp(v, dtype):
+    # spacing of the 16-bit format at |v| (normal range; fp16 subnormal step below)
+    mant = 7 if dtype == torch.bfloat16 else 10
+    e = torch.floor(torch.log2(v.abs().clamp_min(1e-30)))
+    if dtype == torch.float16:
+        e = e.clamp_min(-14)
+    return torch.pow(2.0, e - mant)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(256, 4096, 2048), (37, 2048, 4096), (5, 8448, 2048), (1, 64, 64)])
+def test_cast_linear_matches_castlinear(dev, dtype, M, N, K):
+    """hk_cast_linear (the engine's projection GEMM) against CastLinear's
+    expression F.linear(x.to(lp), W_lp, b_lp).to(float32)
+    (example_model.py:92-95) as a GPU BLAS evaluates it: the sum and the bias
+    accumulated in fp32, one rounding to the 16-bit format. Against the
+    float64 sum rounded once, an element may differ by one rounding step
+    plus the fp32 accumulation error, bounded here by sixteen fp32 rounding
+    steps of the sum of the terms' magnitudes (16 * 2^-24 * sum_k |x_k w_k|,
+    which dominates only for outputs near zero); at least 98% of them must
+    be exact. torch's CPU kernel (which may round the product and the bias sum
+    separately) stays within two steps. With and without a split-K
+    workspace."""
+    from hackathon_amd import kernels as hk
+
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, K, generator=g)
+    w = (torch.rand(N, K, generator=g) * 2 - 1) * K ** -0.5
+    b = (torch.rand(N, generator=g) * 0.1 - 0.05)
+    xl, wl, bl = x.to(dtype), w.to(dtype), b.to(dtype)
+    exact = (xl.double() @ wl.double().T + bl.double()).to(dtype).to(torch.float32)
+    acc = 16 * 2.0 ** -24 * (xl.double().abs() @ wl.double().abs().T + bl.double().abs()).float()
+    cpu = torch.nn.functional.linear(xl, wl, bl).to(torch.float32)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+    for workspace in (None, ws):
+        got = hk.cast_linear(x.to(dev), wl.to(dev), bl.to(dev), workspace=workspace).cpu()
+        d = (got - exact).abs()
+        ulp = _ulp(torch.maximum(got.abs(), exact.abs()), dtype)
+        assert bool((d <= ulp + acc).all()), float((d / (ulp + acc)).max())
+        assert float((d == 0).float().mean()) >= 0.98
+        assert bool(((got - cpu).abs() <= 2 * (_ulp(torch.maximum(got.abs(), cpu.abs()), dtype) + acc)).all())
+    # the workspace is left zeroed (its arrival counters) for the next call
+    assert int(ws[: 1 << 18].sum()) == 0
