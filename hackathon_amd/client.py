@@ -87,6 +87,7 @@ class NnInferenceClient:
         config: ModelConfig = DEFAULT,
         weights: dict | None = None,
         linear_dtype: str | None = None,
+        weights_path: str | None = None,
         max_rows: int = 1024,
         device: str = "cuda:0",
         seed: int = 0,
@@ -96,6 +97,12 @@ class NnInferenceClient:
                 linear_dtype = requested_linear_dtype()
             engine = Engine(config, capacity=num_symbols, max_rows=max(max_rows, num_symbols),
                             linear_dtype=linear_dtype, device=device)
+            if weights is None and weights_path is not None:
+                # the reference's checkpoint, from a local file
+                # (example_model.py:296-302 fetches it over the network)
+                from .weights import load_checkpoint
+
+                weights = load_checkpoint(weights_path, config)
             if weights is None:
                 from .weights import generate
 
@@ -105,9 +112,6 @@ class NnInferenceClient:
         self.capacity = num_symbols
         if num_symbols > engine.capacity:
             raise ValueError("num_symbols exceeds the engine's slot capacity")
-        if engine.max_rows < num_symbols:
-            # One round holds at most one request per symbol; it must fit a tick.
-            raise ValueError("the engine's max_rows must be at least num_symbols")
         self.symbol_to_idx: Dict[str, int] = {}
         self.num_outputs = 4
         self.num_features = engine.cfg.num_features
@@ -184,10 +188,11 @@ class NnInferenceClient:
         if len(unslotted):
             parts.append(np.concatenate([np.arange(base[i], base[i + 1]) for i in unslotted]))
         items = np.flatnonzero(slots >= 0)
-        for k0, k1 in self._round_chunks(counts[items]):
-            c = np.clip(counts[items] - k0, 0, k1 - k0)
+        for k0, k1, part in self._round_chunks(counts[items]):
+            sub = items if part is None else items[part]
+            c = np.clip(counts[sub] - k0, 0, k1 - k0)
             keep = c > 0
-            it, c = items[keep], c[keep]
+            it, c = sub[keep], c[keep]
             runs, req_row, resp = pack_tick(slots[it], c)
             # the chunk's requests (numbered item by item) -> global request index
             sub0 = np.concatenate([[0], np.cumsum(c)[:-1]])
@@ -198,21 +203,34 @@ class NnInferenceClient:
         return order, out[order]
 
     def _round_chunks(self, counts):
-        """Round ranges [k0, k1) whose requests fit one tick each."""
+        """Ticks as (k0, k1, part): rounds [k0, k1) of the symbols `part`
+        (indices into counts; None = all), each within max_rows requests.
+        Whole rounds are grouped while they fit; a single round larger than
+        max_rows is cut into runs of consecutive symbols (dict order), which
+        keeps every symbol's order and the response order (symbols in a
+        round are independent)."""
         if len(counts) == 0:
             return []
         maxlen = int(counts.max())
-        if int(counts.sum()) <= self.engine.max_rows:
-            return [(0, maxlen)]
+        R = self.engine.max_rows
+        if int(counts.sum()) <= R:
+            return [(0, maxlen, None)]
         # requests in round k: symbols with more than k requests
         per_round = np.cumsum(np.bincount(counts, minlength=maxlen + 1)[::-1])[::-1][1:]
         chunks, k0, rows = [], 0, 0
         for k in range(maxlen):
-            if rows + per_round[k] > self.engine.max_rows and k > k0:
-                chunks.append((k0, k))
+            n = int(per_round[k])
+            if rows and rows + n > R:
+                chunks.append((k0, k, None))
                 k0, rows = k, 0
-            rows += int(per_round[k])
-        chunks.append((k0, maxlen))
+            if n > R:
+                active = np.flatnonzero(counts > k)
+                chunks.extend((k, k + 1, active[j:j + R]) for j in range(0, n, R))
+                k0, rows = k + 1, 0
+                continue
+            rows += n
+        if k0 < maxlen:
+            chunks.append((k0, maxlen, None))
         return chunks
 
     def _tick_rows(self, runs, rows, feats):

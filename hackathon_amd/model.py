@@ -46,7 +46,7 @@ import torch
 
 from . import _lib
 from .engine import Engine, Runs
-from .spec import DEFAULT, ModelConfig, param_specs
+from .spec import DEFAULT, ModelConfig
 
 
 class StaleStateError(RuntimeError):
@@ -86,13 +86,6 @@ class EngineState:
             self._model._free(self.slot0, self.batch_size)
 
 
-def _load_weights_only(path) -> dict:
-    sd = torch.load(path, map_location="cpu", weights_only=True)
-    if not isinstance(sd, dict):
-        raise ValueError(f"{path}: expected a state_dict, got {type(sd).__name__}")
-    return sd
-
-
 class MultiTowerModel:
     """model/inference_model.py:103-146 on the HIP engine.
 
@@ -107,6 +100,8 @@ class MultiTowerModel:
                  device: str | torch.device = "cuda:0", max_rows: int | None = None):
         self.config = config
         self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.engine = Engine(config, capacity=capacity, max_rows=max_rows or capacity,
                              linear_dtype=linear_dtype, device=self.device)
         self._free_ranges = [(0, capacity)]  # (slot0, count), disjoint
@@ -120,19 +115,17 @@ class MultiTowerModel:
     def from_checkpoint(cls, path, config: ModelConfig = DEFAULT, **kw):
         """A model whose weights are read from a local state_dict file
         (torch.load with weights_only=True)."""
-        return cls(config, weights=_load_weights_only(path), **kw)
+        from .weights import load_checkpoint
+
+        return cls(config, weights=load_checkpoint(path, config), **kw)
 
     def load_state_dict(self, state_dict: dict, strict: bool = True):
         """Bind a reference state_dict (its parameter names). With strict,
-        missing or unexpected keys raise, as torch's load_state_dict does."""
-        want = {p.name: p.shape for p in param_specs(self.config)}
-        missing = sorted(set(want) - set(state_dict))
-        unexpected = sorted(set(state_dict) - set(want))
-        if strict and (missing or unexpected):
-            raise KeyError(f"state_dict mismatch: missing {missing[:5]}, unexpected {unexpected[:5]}")
-        for k, shape in want.items():
-            if tuple(state_dict[k].shape) != tuple(shape):
-                raise ValueError(f"{k}: shape {tuple(state_dict[k].shape)}, expected {shape}")
+        unexpected keys raise as well as missing ones, as torch's
+        load_state_dict does."""
+        from .weights import check_state_dict
+
+        check_state_dict(self.config, state_dict, strict)
         self.engine.load_weights(state_dict)
 
     # -- state slots ----------------------------------------------------------------
@@ -159,8 +152,10 @@ class MultiTowerModel:
     def init_state(self, batch_size: int, device=None) -> EngineState:
         """MultiTowerModel.init_state (model/inference_model.py:145-146):
         batch_size rows at the reference's initial values."""
-        if device is not None and torch.device(device) != self.device:
-            raise ValueError(f"the state lives on {self.device}")
+        if device is not None:
+            d = torch.device(device)
+            if d.type != self.device.type or (d.index is not None and d.index != self.device.index):
+                raise ValueError(f"the state lives on {self.device}")
         s0 = self._alloc(batch_size)
         self.engine.reset_slots(np.arange(s0, s0 + batch_size, dtype=np.int32))
         return EngineState(self, s0, batch_size)

@@ -54,3 +54,30 @@ def to_lp_bits(x: torch.Tensor, fmt: str) -> torch.Tensor:
     _lib.check(_lib.lib().hk_to_lp_host(x.data_ptr(), out.data_ptr(), x.numel(), LP_FORMATS[fmt]),
                "hk_to_lp_host")
     return out
+
+
+def check_state_dict(cfg: ModelConfig, sd: dict, strict: bool = True) -> None:
+    """Raise unless `sd` holds every parameter of MultiTowerModel(cfg) under
+    the reference's names with the reference's shapes (and, with strict,
+    nothing else), as torch's load_state_dict would."""
+    want = {p.name: p.shape for p in param_specs(cfg)}
+    missing = sorted(set(want) - set(sd))
+    unexpected = sorted(set(sd) - set(want))
+    if missing or (strict and unexpected):
+        raise KeyError(f"state_dict mismatch: missing {missing[:5]} ({len(missing)}), "
+                       f"unexpected {unexpected[:5]} ({len(unexpected)})")
+    for k, shape in want.items():
+        if tuple(sd[k].shape) != tuple(shape):
+            raise ValueError(f"{k}: shape {tuple(sd[k].shape)}, expected {tuple(shape)}")
+
+
+def load_checkpoint(path, cfg: ModelConfig) -> dict[str, torch.Tensor]:
+    """A reference state_dict from a local file, read as the reference client
+    reads its checkpoint (torch.load with weights_only=True,
+    example_model.py:296-302; the download itself needs the network), checked
+    against cfg and converted to CPU fp32."""
+    sd = torch.load(path, map_location="cpu", weights_only=True)
+    if not isinstance(sd, dict):
+        raise ValueError(f"{path}: expected a state_dict, found {type(sd).__name__}")
+    check_state_dict(cfg, sd)
+    return {k: v.detach().to(torch.float32).contiguous() for k, v in sd.items()}

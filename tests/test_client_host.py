@@ -40,11 +40,11 @@ def _client(capacity, max_rows, F=6):
     return c
 
 
-@pytest.mark.parametrize("max_rows", [64, 7, 3])
+@pytest.mark.parametrize("max_rows", [64, 7, 3, 2])
 def test_process_arrays_order_chunks_and_overflow(max_rows):
     rng = np.random.default_rng(max_rows)
     capacity = 5
-    client = _client(capacity, max_rows=max(max_rows, capacity))
+    client = _client(capacity, max_rows=max_rows)  # 2: a round may span several ticks
     seen = []
     for batch in range(4):
         names = [f"S{i}" for i in rng.permutation(8)[:6]]
@@ -99,9 +99,16 @@ def test_round_chunks_cover_rounds_within_max_rows():
     for max_rows in (4, 9, 33):
         client = _client(capacity=64, max_rows=max_rows)
         for _ in range(20):
-            counts = rng.integers(1, 12, size=rng.integers(1, max_rows + 1))
+            counts = rng.integers(1, 12, size=rng.integers(1, 3 * max_rows))
             chunks = client._round_chunks(counts)
-            assert chunks[0][0] == 0 and chunks[-1][1] == counts.max()
-            assert all(a[1] == b[0] for a, b in zip(chunks, chunks[1:]))
-            for k0, k1 in chunks:
-                assert int(np.clip(counts - k0, 0, k1 - k0).sum()) <= max_rows or k1 == k0 + 1
+            # every (request round, symbol) pair exactly once, rounds in order
+            seen = []
+            for k0, k1, part in chunks:
+                idx = np.arange(len(counts)) if part is None else part
+                c = np.clip(counts[idx] - k0, 0, k1 - k0)
+                assert 0 < int(c.sum()) <= max_rows
+                seen.extend((k, int(i)) for i, ci in zip(idx, c) for k in range(k0, k0 + ci))
+            want = [(k, i) for i in range(len(counts)) for k in range(counts[i])]
+            assert sorted(seen) == sorted(want) and len(seen) == len(want)
+            starts = [k0 for k0, _, _ in chunks]
+            assert starts == sorted(starts)

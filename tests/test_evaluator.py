@@ -1,0 +1,97 @@
+"""The evaluator (hackathon_amd.evaluator, the reference's
+local_evaluator.py:19-112) and checkpoint ingest on the CPU: the metric
+against a hand computation, the batching (consecutive rows, grouped by
+symbol in first-appearance order, every response charged its batch's time),
+the capacity rule, and state_dict checks. tests/golden/tiny.parquet is the
+reference's own requests file (100 requests over 34 symbols)."""
+
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from hackathon_amd import spec, weights
+from hackathon_amd.evaluator import LocalEvaluator, calculate_metrics
+
+TINY = Path(__file__).resolve().parent / "golden" / "tiny.parquet"
+
+
+def test_metric_hand_computed():
+    targets = np.array([[0.0, 1.0, 2.0, 3.0], [1.0, 1.0, 1.0, 1.0], [5.0, 5.0, 5.0, 5.0]])
+    preds = {0: [0.5, 1.0, 1.0, 3.0], 2: [5.0, 6.0, 5.0, 2.0]}  # request 1 unanswered
+    lat = {0: 2.0, 2: 4.0}
+    m = calculate_metrics(targets, preds, lat)
+    assert m["total_requests"] == 3 and m["total_responses"] == 2
+    assert m["response_rate"] == pytest.approx(2 / 3) and m["avg_latency_ms"] == 3.0
+    assert m["tower_0"] == (0.5, 0.25)
+    assert m["tower_1"] == (1.0, 0.5)
+    assert m["tower_2"] == (1.0, 0.5)
+    assert m["tower_3"] == (3.0, 1.5)
+    with pytest.raises(ValueError):
+        calculate_metrics(targets, {0: [1.0, 2.0]}, {0: 1.0})
+
+
+def test_tiny_parquet_batching_and_capacity():
+    ev = LocalEvaluator(TINY)
+    assert len(ev.symbols) == 100 and ev.features.shape == (100, 79)
+    assert ev.num_symbols == max(int(s[-3:]) for s in ev.symbols) + 1
+    calls = []
+
+    def fake_process_batch(by_sym):
+        # answers each request with its own first four features
+        calls.append([(s, [r.unique_id for r in reqs]) for s, reqs in by_sym.items()])
+        ids = [r.unique_id for reqs in by_sym.values() for r in reqs]
+        return SimpleNamespace(unique_ids=ids,
+                               predictions=[ev.features[i, :4].tolist() for i in ids])
+
+    m = ev.evaluate_model(fake_process_batch, batch_size=8)
+    assert len(calls) == 13 and m["response_rate"] == 1.0
+    for b, call in enumerate(calls):
+        rows = list(range(8 * b, min(8 * b + 8, 100)))
+        firsts = list(dict.fromkeys(ev.symbols[r] for r in rows))
+        assert [s for s, _ in call] == firsts
+        assert sorted(i for _, ids in call for i in ids) == rows
+    err = np.abs(ev.features[:, :4].astype(np.float64) - ev.targets)
+    for t in range(4):
+        assert m[f"tower_{t}"][0] == pytest.approx(err[:, t].max())
+        assert m[f"tower_{t}"][1] == pytest.approx(err[:, t].mean())
+
+    # the flat-array path answers the same requests with the same metric
+    class FakeClient:
+        def process_arrays(self, symbols, counts, feats):
+            assert len(feats) == sum(counts)
+            return np.arange(len(feats))[::-1], feats[::-1, :4].astype(np.float64)
+
+    m2 = ev.evaluate_arrays(FakeClient(), batch_size=8)
+    for t in range(4):
+        assert m2[f"tower_{t}"] == pytest.approx(m[f"tower_{t}"])
+
+
+def test_checkpoint_ingest_weights_only(tmp_path):
+    cfg = spec.SMALL
+    sd = weights.generate(cfg, 0)
+    path = tmp_path / "state_dict.pt"
+    torch.save(sd, path)
+    got = weights.load_checkpoint(path, cfg)
+    assert set(got) == set(sd) and all(torch.equal(got[k], sd[k]) for k in sd)
+    bad = dict(sd)
+    bad.pop("output_proj.bias")
+    torch.save(bad, tmp_path / "missing.pt")
+    with pytest.raises(KeyError):
+        weights.load_checkpoint(tmp_path / "missing.pt", cfg)
+    bad = dict(sd)
+    bad["towers.0.input_up.weight"] = torch.zeros(3, 3)
+    torch.save(bad, tmp_path / "shape.pt")
+    with pytest.raises(ValueError):
+        weights.load_checkpoint(tmp_path / "shape.pt", cfg)
+    extra = dict(sd)
+    extra["something.else"] = torch.zeros(1)
+    weights.check_state_dict(cfg, extra, strict=False)
+    with pytest.raises(KeyError):
+        weights.check_state_dict(cfg, extra, strict=True)
+    # a pickled object that is not a plain tensor dict is refused by the loader
+    torch.save({"w": SimpleNamespace(a=1)}, tmp_path / "obj.pt", _use_new_zipfile_serialization=True)
+    with pytest.raises(Exception):
+        weights.load_checkpoint(tmp_path / "obj.pt", cfg)
