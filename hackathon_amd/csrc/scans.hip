@@ -314,6 +314,11 @@ __global__ __launch_bounds__(256) void slstm_round_kernel(
 constexpr int kPersistRuns = 16;   // runs per chunk = one MFMA n-tile
 constexpr int kValuRuns = 4;       // chunks up to this size use the VALU product
 constexpr int kPersistThreads = 512;
+// LDS a persistent work-group asks for at least, so that it has its CU to
+// itself: other streams' kernels sharing those CUs slow the recurrence's
+// step chain about as much as they gain (C4 tick 9.40-9.45 ms against
+// 9.42-9.50 with the CUs shared, interleaved runs on two boxes).
+constexpr size_t kPersistLdsFloor = 140 * 1024;
 // Bounded wait: each poll re-reads a wave's words (a memory round trip of a
 // microsecond or more), so this bounds a wait to well under a few seconds,
 // far above a legitimate step even when other streams' kernels delay some
@@ -909,11 +914,14 @@ int launch_persist(const SlstmPersistArgs& a, size_t smem, hipStream_t s) {
   return HK_OK;
 }
 
-// LDS bytes of a persistent launch over n_runs runs and n_rounds steps.
+// LDS bytes a persistent launch over n_runs runs and n_rounds steps uses.
 size_t persist_smem(int hs, int n_runs, int n_rounds) {
   return (size_t)(kPersistRuns * (hs + 8) + 2 * kPersistRuns * 64) * sizeof(float) +
          (size_t)persist_meta_ints(n_runs, n_rounds) * sizeof(int);
 }
+
+// LDS bytes it asks for (see kPersistLdsFloor).
+size_t persist_smem_launch(size_t used) { return std::max(used, kPersistLdsFloor); }
 
 template <int HS>
 int persist_pair_fits(size_t smem, int heads, bool* ok) {
@@ -930,7 +938,7 @@ int slstm_persist_pair_fits(int hidden, int heads, int max_runs, int max_rounds,
   *ok = false;
   if (!slstm_persist_supported(hidden, heads)) return HK_OK;
   const int hs = hidden / heads;
-  const size_t smem = persist_smem(hs, max_runs, max_rounds);
+  const size_t smem = persist_smem_launch(persist_smem(hs, max_runs, max_rounds));
   switch (hs) {
     case 32: return persist_pair_fits<32>(smem, heads, ok);
     case 64: return persist_pair_fits<64>(smem, heads, ok);
@@ -960,6 +968,7 @@ int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* 
     HK_REQUIRE(n_rounds <= 512, "slstm_persist: tracing supports at most 512 steps");
     smem += (size_t)n_rounds * 8 * sizeof(uint64_t);
   }
+  smem = persist_smem_launch(smem);
   switch (hs) {
     case 32: return launch_persist<32>(a, smem, s);
     case 64: return launch_persist<64>(a, smem, s);
