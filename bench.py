@@ -475,9 +475,11 @@ def tick_projections(cfg, run_off):
 
 
 def gemm_replay(torch, dev, shapes, reps=3):
-    """The given CastLinear GEMMs through hk_cast_linear (bf16) on one
-    stream, each with weights of its own (so weights stream from HBM as in
-    the tick: 3.7 GB at the default dims), inputs resident. Returns the
+    """The given CastLinear GEMMs through hk_cast_linear_packed (bf16, the
+    engine's projection kernel, weights packed by hk_pack_cast_weight as the
+    engine packs its slots) on one stream, each with weights of its own (so
+    weights stream from HBM as in the tick: 3.7 GB at the default dims),
+    inputs resident. Returns the
     average launch duration over `reps` back-to-back passes of the whole
     sequence (one HIP event pair per pass, so launch gaps are not added),
     per-launch durations from a pass with an event pair around every launch
@@ -495,13 +497,20 @@ def gemm_replay(torch, dev, shapes, reps=3):
     x = (torch.randn(Mmax, Kmax, device=dev, generator=g) * 0.5).to(torch.bfloat16)
     out = torch.empty(Mmax * Nmax, dtype=torch.float32, device=dev)
     bias = torch.zeros(Nmax, dtype=torch.float32, device=dev)
-    weights = [((torch.rand(n, k, device=dev, generator=g) - 0.5) * k ** -0.5).to(torch.bfloat16)
-               for _, n, k in shapes]
+    weights = []
+    for _, n, k in shapes:
+        w = ((torch.rand(n, k, device=dev, generator=g) - 0.5) * k ** -0.5).to(torch.bfloat16)
+        p = torch.empty_like(w)
+        if lib.hk_pack_cast_weight(w.data_ptr(), p.data_ptr(), n, k, stream) != 0:
+            raise RuntimeError(lib.hk_last_error().decode())
+        weights.append(p)
+        del w
     cur = torch.cuda.current_stream(dev)
 
     def launch(m, n, k, w):
-        st = lib.hk_cast_linear(x.data_ptr(), w.data_ptr(), bias.data_ptr(), out.data_ptr(),
-                                m, n, k, 0, ws.data_ptr(), ws.numel(), stream)
+        st = lib.hk_cast_linear_packed(x.data_ptr(), w.data_ptr(), bias.data_ptr(),
+                                       out.data_ptr(), m, n, k, 0, ws.data_ptr(), ws.numel(),
+                                       stream)
         if st != 0:
             raise RuntimeError(lib.hk_last_error().decode())
 
@@ -548,7 +557,7 @@ def gemm_roofline(avg_s, bytes_, flops):
 def bench_gemm(args) -> int:
     """The dominant kernel alone: one C4 tick's 250 CastLinear projection
     GEMMs (the first timed tick's shapes, 1024 symbols, 256 Zipf(1.1)
-    requests) replayed through hk_cast_linear on one stream, weights from
+    requests) replayed through hk_cast_linear_packed on one stream, weights from
     HBM. The command the committed rocprofv3 summary of the GEMM runs."""
     import torch
 
@@ -1064,7 +1073,7 @@ def main() -> int:
 
     # The roofline of the dominant kernel (the CastLinear projection GEMM:
     # the largest share of kernel time in the tick's trace): the first timed
-    # tick's 250 GEMMs replayed alone through hk_cast_linear on one stream,
+    # tick's 250 GEMMs replayed alone through hk_cast_linear_packed on one stream,
     # weights from HBM, per-launch HIP events. In the tick the same launches
     # share the CUs with three other streams.
     first = packed[W]
@@ -1134,7 +1143,8 @@ def main() -> int:
                     "stream wait per call included",
         },
         "roofline": {
-            "kernel": "gemm_kernel<0, 64, 3> (bf16 CastLinear projection GEMM, 64x64 tiles)",
+            "kernel": "gemm_wp_kernel (bf16 CastLinear projection GEMM, packed weights; "
+                      "tiles 64x128, 64x64, 32x64, 32x32 by shape)",
             "bound": "hbm",
             "achieved": grf["achieved_GBs"],
             "peak": HBM_PEAK_GBS,
@@ -1148,7 +1158,8 @@ def main() -> int:
             "avg_us": grf["avg_us"],
             "algorithmic_bytes_per_launch": grf["algorithmic_bytes_per_launch"],
             "method": ("the first timed tick's 250 CastLinear GEMMs replayed alone through "
-                       "hk_cast_linear on one stream, weights from HBM; average launch duration "
+                       "hk_cast_linear_packed on one stream, weights from HBM; average launch "
+                       "duration "
                        "= HIP-event time of three back-to-back passes / 750 (bench.py --workload "
                        "gemm runs the same replay; profiles/ holds its rocprofv3 kernel-trace "
                        "and counter summaries); algorithmic bytes = bf16 W + bf16 A + fp32 out "

@@ -563,6 +563,50 @@ int hk_cast_linear(const uint16_t* x, const uint16_t* w, const float* bias, floa
   return hk::gemm(g, ws, (hipStream_t)stream);
 }
 
+int hk_pack_cast_weight(const uint16_t* w, uint16_t* packed, int N, int K, void* stream) {
+  return hk::pack_lp_weight(w, packed, N, K, (hipStream_t)stream);
+}
+
+int hk_cast_linear_packed(const uint16_t* x, const uint16_t* w_packed, const float* bias,
+                          float* out, int M, int N, int K, int fmt, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
+  constexpr int64_t kCastArrivals = 1 << 16;
+  HK_REQUIRE(x && w_packed && out, "hk_cast_linear_packed: null operand");
+  HK_REQUIRE(M >= 0 && hk::packable(N, K),
+             "hk_cast_linear_packed: bad shape M=%d N=%d K=%d (N a multiple of 32, K of 64)", M,
+             N, K);
+  HK_REQUIRE(fmt == hk::kLpBF16 || fmt == hk::kLpF16, "hk_cast_linear_packed: format %d", fmt);
+  HK_REQUIRE(hk::aligned16(x) && hk::aligned16(w_packed),
+             "hk_cast_linear_packed: operands must be 16-byte aligned");
+  HK_REQUIRE(K % 8 == 0, "hk_cast_linear_packed: K=%d", K);
+  HK_REQUIRE(workspace == nullptr || workspace_bytes >= kCastArrivals * 4,
+             "hk_cast_linear_packed: a workspace needs at least %lld bytes",
+             (long long)kCastArrivals * 4);
+  if (M == 0) return HK_OK;
+  hk::GemmArgs g;
+  g.type = fmt == hk::kLpF16 ? hk::GemmType::kF16 : hk::GemmType::kBF16;
+  g.A = x;
+  g.lda = K;
+  g.W = w_packed;
+  g.w_packed = true;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.ep.bias = bias;
+  g.ep.round_lp = true;
+  g.ep.lp_fmt = fmt;
+  g.ep.out = out;
+  g.ep.ldo = N;
+  hk::GemmWorkspace ws;
+  if (workspace != nullptr) {
+    ws.arrivals = static_cast<int*>(workspace);
+    ws.arrival_elems = kCastArrivals;
+    ws.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCastArrivals * 4);
+    ws.partial_elems = (workspace_bytes - kCastArrivals * 4) / 4;
+  }
+  return hk::gemm(g, ws, (hipStream_t)stream);
+}
+
 int hk_rglru_step(float* h, const float* x, const float* gate_i, const float* gate_r,
                   const float* a, float c, const uint8_t* mask, float* out, int batch, int width,
                   void* stream) {

@@ -62,13 +62,12 @@ __device__ __forceinline__ float gelu_erf(float x) {
 }
 
 // Round-to-nearest-even fp32 -> bf16 bits (no NaN inputs on this path, but a
-// NaN stays a NaN: the quiet bit is forced).
+// NaN stays a NaN: the quiet bit is forced). Written as selects, not early
+// returns, so a wave converts without branching.
 __host__ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
-  uint32_t lsb = (u >> 16) & 1u;
-  u += 0x7fffu + lsb;
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : r);
 }
 
 __host__ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
@@ -84,30 +83,31 @@ __host__ __device__ __forceinline__ float round_bf16(float f) {
 // round-half-even bias, the carry stepping into the exponent. Subnormal
 // results: adding 0.5 (whose ulp is 2^-24, the fp16 subnormal step) makes
 // the fp32 adder round |f| to a multiple of 2^-24; the low bits of the sum
-// are that multiple.
+// are that multiple. Every case is computed and the result selected (no
+// branches): NaN -> quiet NaN, |f| >= 65520 (rounds past 65504) or infinity
+// -> infinity, |f| >= 2^-14 -> normal, else subnormal or zero.
 __host__ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t sign = (u >> 16) & 0x8000u;
   const uint32_t a = u & 0x7fffffffu;
-  if (a >= 0x7f800000u) return sign | 0x7c00u | (a > 0x7f800000u ? 0x200u : 0u);
-  if (a >= 0x477ff000u) return sign | 0x7c00u;  // >= 65520 rounds past 65504
-  if (a >= 0x38800000u) {                       // >= 2^-14: normal fp16
-    const uint32_t r = a - 0x38000000u;         // rebias the exponent (127 -> 15)
-    return sign | (uint16_t)((r + 0xfffu + ((r >> 13) & 1u)) >> 13);
-  }
-  const float t = __builtin_bit_cast(float, a) + 0.5f;
-  return sign | (uint16_t)(__builtin_bit_cast(uint32_t, t) - 0x3f000000u);
+  const uint32_t r = a - 0x38000000u;  // rebias the exponent (127 -> 15)
+  const uint32_t normal = (r + 0xfffu + ((r >> 13) & 1u)) >> 13;
+  const uint32_t sub =
+      __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, a) + 0.5f) - 0x3f000000u;
+  uint32_t v = a >= 0x38800000u ? normal : sub;
+  v = a >= 0x477ff000u ? 0x7c00u : v;
+  v = a > 0x7f800000u ? 0x7e00u : v;
+  return (uint16_t)(sign | v);
 }
 
 __host__ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
   const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
-  if (e == 0) {  // zero / subnormal: m * 2^-24, exact in fp32
-    const float v = (float)m * 5.9604644775390625e-08f;
-    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) | sign);
-  }
-  if (e == 31) return __builtin_bit_cast(float, sign | 0x7f800000u | (m << 13));
-  return __builtin_bit_cast(float, sign | ((e + 112u) << 23) | (m << 13));
+  // zero / subnormal: m * 2^-24, exact in fp32; infinity / NaN; normal
+  const uint32_t sub = __builtin_bit_cast(uint32_t, (float)m * 5.9604644775390625e-08f);
+  uint32_t v = e == 31u ? 0x7f800000u | (m << 13) : ((e + 112u) << 23) | (m << 13);
+  v = e == 0u ? sub : v;
+  return __builtin_bit_cast(float, sign | v);
 }
 
 // The 16-bit compute formats of CastLinear (example_model.py:150-155).
@@ -118,6 +118,15 @@ __host__ __device__ __forceinline__ uint16_t f32_to_lp_bits(float f, int fmt) {
 }
 __host__ __device__ __forceinline__ float round_lp(float f, int fmt) {
   return fmt == kLpF16 ? f16_bits_to_f32(f32_to_f16_bits(f)) : round_bf16(f);
+}
+// The same with the format fixed at compile time.
+template <int FMT>
+__host__ __device__ __forceinline__ uint16_t f32_to_lp_bits_t(float f) {
+  return FMT == kLpF16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f);
+}
+template <int FMT>
+__host__ __device__ __forceinline__ float round_lp_t(float f) {
+  return FMT == kLpF16 ? f16_bits_to_f32(f32_to_f16_bits(f)) : round_bf16(f);
 }
 
 // Global-memory loads through explicit address-space-1 pointers. Pointers

@@ -98,11 +98,13 @@ struct SlotDef {
   int64_t numel;
   bool lp;          // a CastLinear weight: 16-bit storage in reduced-precision mode
   bool lp_bias;     // a CastLinear bias: rounded to 16 bits in reduced-precision mode
+  int k = 0;        // a CastLinear weight's input width (its N is numel / k)
 };
 
 struct Slot {
   SlotDef def{};
   void* ptr = nullptr;   // device storage (16-bit when def.lp && lowp, else fp32)
+  bool packed = false;   // 16-bit weight held in the pack_lp_weight layout
   bool bound = false;
 };
 
@@ -121,9 +123,9 @@ std::vector<SlotDef> block_slots(const Dims& d, int tower) {
   std::vector<SlotDef> v = {
       {"norm1.weight", d.H, false, false},
       {"norm2.weight", d.H, false, false},
-      {"mlp.fc1.weight", (int64_t)d.P * d.H, true, false},
+      {"mlp.fc1.weight", (int64_t)d.P * d.H, true, false, d.H},
       {"mlp.fc1.bias", d.P, false, true},
-      {"mlp.fc2.weight", (int64_t)d.H * d.P, true, false},
+      {"mlp.fc2.weight", (int64_t)d.H * d.P, true, false, d.P},
       {"mlp.fc2.bias", d.H, false, true},
   };
   switch (tower) {
@@ -138,7 +140,7 @@ std::vector<SlotDef> block_slots(const Dims& d, int tower) {
       v.push_back({"slstm.group_norm.weight", d.H, false, false});
       v.push_back({"slstm.group_norm.bias", d.H, false, false});
       v.push_back({"mlstm.norm.weight", d.H, false, false});
-      v.push_back({"mlstm.{x_proj,gate_proj}.weight", 2 * I * d.H, true, false});
+      v.push_back({"mlstm.{x_proj,gate_proj}.weight", 2 * I * d.H, true, false, d.H});
       v.push_back({"mlstm.{q,k,v}_proj.weight", 3 * I * 4, false, false});
       v.push_back({"mlstm.conv (4 taps x I)", 4 * I, false, false});
       v.push_back({"mlstm.conv1d.conv.bias", I, false, false});
@@ -146,14 +148,14 @@ std::vector<SlotDef> block_slots(const Dims& d, int tower) {
       v.push_back({"mlstm.mlstm_cell.{igate,fgate}_proj.bias", 2LL * d.nh, false, false});
       v.push_back({"mlstm.mlstm_cell.outnorm.weight", I, false, false});
       v.push_back({"mlstm.mlstm_cell.outnorm.bias", I, false, false});
-      v.push_back({"mlstm.proj_down.weight", (int64_t)d.H * I, true, false});
+      v.push_back({"mlstm.proj_down.weight", (int64_t)d.H * I, true, false, (int)I});
       v.push_back({"mlstm.learnable_skip", I, false, false});
       v.push_back({"final_norm.weight", d.H, false, false});
       break;
     }
     case kMamba2: {
       const int64_t C = d.Im + 2LL * d.bc;
-      v.push_back({"{input,b,c,z}_proj.weight", (C + d.Im) * d.H, true, false});
+      v.push_back({"{input,b,c,z}_proj.weight", (C + d.Im) * d.H, true, false, d.H});
       v.push_back({"dt_proj.weight", (int64_t)d.nhm * d.H, false, false});
       v.push_back({"dt_proj.bias", d.nhm, false, false});
       v.push_back({"{input,b,c}_conv (4 taps x C)", 4 * C, false, false});
@@ -161,23 +163,23 @@ std::vector<SlotDef> block_slots(const Dims& d, int tower) {
       v.push_back({"a", d.nhm, false, false});
       v.push_back({"d", d.nhm, false, false});
       v.push_back({"norm.weight", d.Im, false, false});
-      v.push_back({"out_proj.weight", (int64_t)d.H * d.Im, true, false});
+      v.push_back({"out_proj.weight", (int64_t)d.H * d.Im, true, false, d.Im});
       break;
     }
     case kRetNet: {
-      v.push_back({"{q,k,v,g}_proj.weight", 4LL * d.H * d.H, true, false});
-      v.push_back({"out_proj.weight", (int64_t)d.H * d.H, true, false});
+      v.push_back({"{q,k,v,g}_proj.weight", 4LL * d.H * d.H, true, false, d.H});
+      v.push_back({"out_proj.weight", (int64_t)d.H * d.H, true, false, d.H});
       v.push_back({"decay", d.nh, false, false});
       v.push_back({"angle", d.hs_r, false, false});
       break;
     }
     case kHawk: {
-      v.push_back({"{gate,recurrent}_proj.weight", 2LL * d.H * d.H, true, false});
+      v.push_back({"{gate,recurrent}_proj.weight", 2LL * d.H * d.H, true, false, d.H});
       v.push_back({"conv (4 taps x H)", 4LL * d.H, false, false});
       v.push_back({"conv.conv.bias", d.H, false, false});
       v.push_back({"rglru.{input,recurrence}_gate.weight", 2LL * d.H * d.bs_h, false, false});
       v.push_back({"rglru.a", d.H, false, false});
-      v.push_back({"out_proj.weight", (int64_t)d.H * d.H, true, false});
+      v.push_back({"out_proj.weight", (int64_t)d.H * d.H, true, false, d.H});
       break;
     }
   }
@@ -185,9 +187,9 @@ std::vector<SlotDef> block_slots(const Dims& d, int tower) {
 }
 
 std::vector<SlotDef> tower_slots(const Dims& d) {
-  return {{"input_up.weight (K padded)", (int64_t)d.P * d.Fpad, true, false},
+  return {{"input_up.weight (K padded)", (int64_t)d.P * d.Fpad, true, false, d.Fpad},
           {"input_up.bias", d.P, false, true},
-          {"input_down.weight", (int64_t)d.H * d.P, true, false},
+          {"input_down.weight", (int64_t)d.H * d.P, true, false, d.P},
           {"input_down.bias", d.H, false, true}};
 }
 
@@ -554,6 +556,7 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
   g.lda = ldx;
   g.W = lin.w->ptr;
   g.ldw = K;
+  g.w_packed = lp && lin.w->packed;
   g.M = M;
   g.N = N;
   g.K = K;
@@ -1190,7 +1193,13 @@ int hk_engine_create(const int* cfg, int n_cfg, void** out) {
   }
   for (auto& def : hk::global_slots(d)) e->gslots.push_back(hk::Slot{def});
   auto alloc_slot = [&](hk::Slot& s) -> bool {
-    const size_t bytes = (size_t)s.def.numel * ((s.def.lp && e->lowp) ? 2 : 4);
+    const bool lp = s.def.lp && e->lowp;
+    const size_t bytes = (size_t)s.def.numel * (lp ? 2 : 4);
+    // CastLinear weights of a packable shape are stored packed for the
+    // matrix cores (every engine shape is; the checks keep odd widths on the
+    // row-major path).
+    s.packed = lp && s.def.k > 0 && s.def.numel % s.def.k == 0 &&
+               hk::packable((int)(s.def.numel / s.def.k), s.def.k);
     s.ptr = e->alloc_bytes(bytes);
     return s.ptr != nullptr;
   };
@@ -1289,8 +1298,11 @@ int hk_engine_load_param(void* h, int tower, int layer, int slot, const float* h
     float* tmp = nullptr;
     HK_CHECK_HIP(hipMalloc(&tmp, (size_t)numel * 4));
     hipError_t err = hipMemcpy(tmp, host, (size_t)numel * 4, hipMemcpyHostToDevice);
-    int st = err == hipSuccess ? hk::to_lp(tmp, static_cast<uint16_t*>(s->ptr), numel, e.lp_fmt, nullptr)
-                               : HK_ERR_HIP;
+    uint16_t* dst = static_cast<uint16_t*>(s->ptr);
+    int st = err != hipSuccess ? HK_ERR_HIP
+             : s->packed       ? hk::pack_f32_to_lp(tmp, dst, (int)(numel / s->def.k), s->def.k,
+                                                    e.lp_fmt, nullptr)
+                               : hk::to_lp(tmp, dst, numel, e.lp_fmt, nullptr);
     if (st == HK_OK) err = hipDeviceSynchronize();
     (void)hipFree(tmp);
     if (err != hipSuccess) {
@@ -1331,10 +1343,20 @@ int hk_engine_load_param_noalloc(void* h, int tower, int layer, int slot, const 
              e.device, dev);
   if (s->def.lp && e.lowp) {
     uint16_t* dst = static_cast<uint16_t*>(s->ptr);
-    for (int64_t off = 0; off < numel; off += hk::kScratchFloats) {
-      const int64_t n = std::min(hk::kScratchFloats, numel - off);
+    // A packed slot moves in whole 32-row blocks: rows r .. r + n of W fill
+    // packed elements r*K .. (r + n)*K, so each chunk packs on its own.
+    const int64_t K = s->def.k;
+    const int64_t step = s->packed ? (hk::kScratchFloats / K) / 32 * 32 * K : hk::kScratchFloats;
+    HK_REQUIRE(step > 0, "hk_engine_load_param_noalloc: %s rows do not fit the staging array",
+               s->def.name);
+    for (int64_t off = 0; off < numel; off += step) {
+      const int64_t n = std::min(step, numel - off);
       HK_CHECK_HIP(hipMemcpy(e.scratch, host + off, (size_t)n * 4, hipMemcpyHostToDevice));
-      HK_TRY(hk::to_lp(e.scratch, dst + off, n, e.lp_fmt, nullptr));
+      if (s->packed) {
+        HK_TRY(hk::pack_f32_to_lp(e.scratch, dst + off, (int)(n / K), (int)K, e.lp_fmt, nullptr));
+      } else {
+        HK_TRY(hk::to_lp(e.scratch, dst + off, n, e.lp_fmt, nullptr));
+      }
       HK_CHECK_HIP(hipStreamSynchronize(nullptr));  // the next chunk overwrites the array
     }
   } else if (s->def.lp_bias && e.lowp) {

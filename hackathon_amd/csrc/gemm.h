@@ -45,6 +45,9 @@ struct GemmArgs {
   const void* A2 = nullptr;
   int a2_from = 0;
   int a_period = 0;
+  // 16-bit W held in the fragment-packed layout of pack_lp_weight (ldw is
+  // then unused; N and K must be multiples of 32 and 64).
+  bool w_packed = false;
   GemmEpilogue ep;
 };
 
@@ -60,5 +63,18 @@ struct GemmWorkspace {
 
 // K must be a multiple of 64 (bf16, fp16) or 16 (fp32); lda/ldw multiples of 8 / 4.
 int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int splits_hint = 0);
+
+// Packed layout of a 16-bit weight W[N][K] (row-major, ldw = K) for the
+// matrix cores: 16-bit element (n, k) goes to
+//   ((((n / 32) * (K / 32) + k / 32) * 2 + (n % 32) / 16) * 64 + lane) * 8 + k % 8,
+//   lane = n % 16 + 16 * ((k % 32) / 8),
+// i.e. for each 32-column block, each 32-deep k block is two 1 KB MFMA B
+// fragments (16 columns each) in lane order, and the 64-deep slab a wave
+// multiplies is 4 KB contiguous. N must be a multiple of 32, K of 64.
+bool packable(int N, int K);
+int pack_lp_weight(const uint16_t* src, uint16_t* dst, int N, int K, hipStream_t stream);
+// fp32 rows [rows][K] (rows a multiple of 32) -> rounded to format fmt and
+// packed (the packed rows r .. r + rows of a larger W start at r*K).
+int pack_f32_to_lp(const float* src, uint16_t* dst, int rows, int K, int fmt, hipStream_t stream);
 
 }  // namespace hk

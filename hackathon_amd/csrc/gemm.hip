@@ -1,6 +1,11 @@
-// Projection GEMM kernel (see gemm.h).
+// Projection GEMM kernels (see gemm.h). Two kernels:
+// - gemm_wp_kernel, for the engine's 16-bit CastLinear projections, whose
+//   weights are stored packed in MFMA fragment order (described at the
+//   kernel);
+// - gemm_kernel, below, for fp32 products (the fp32 mode's linears and the
+//   BlockLinear batches) and 16-bit weights in row-major layout.
 //
-// 64x64 output tile per 256-thread work-group, 4 wave64s in a 2x2 layout,
+// gemm_kernel: 64x64 output tile per 256-thread work-group, 4 wave64s in a 2x2 layout,
 // each wave owning a 32x32 sub-tile = 2x2 MFMA 16x16 fragments. K advances in
 // 128-byte slabs (64 bf16/fp16 or 32 fp32 per row) that travel global -> LDS
 // directly (global_load_lds_dwordx4) through a ring of kStages LDS stages,
@@ -413,7 +418,498 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
   }
 }
 
+// lgkmcnt(0) tying every register of r (in groups of 8 or 4) to the wait.
+template <int N>
+__device__ __forceinline__ void ds_wait_all(u32x4 (&r)[N]) {
+  static_assert(N % 4 == 0, "groups of four");
+#pragma unroll
+  for (int i = 0; i + 8 <= N; i += 8)
+    __asm__ volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(r[i]), "+v"(r[i + 1]), "+v"(r[i + 2]), "+v"(r[i + 3]), "+v"(r[i + 4]),
+                       "+v"(r[i + 5]), "+v"(r[i + 6]), "+v"(r[i + 7])
+                     :
+                     : "memory");
+  if constexpr (N % 8 == 4)
+    __asm__ volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(r[N - 4]), "+v"(r[N - 3]), "+v"(r[N - 2]), "+v"(r[N - 1])
+                     :
+                     : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Packed-weight tile for the 16-bit projections (W in the pack_lp_weight
+// layout). NW waves per work-group, each owning 32 output columns (two MFMA
+// B fragments) and every one of the tile's 16*MF rows.
+//
+// W is the operand each element of which feeds exactly one wave, and packed
+// it is 4 KB contiguous per wave and slab: it travels global -> VGPR with
+// fully coalesced 1 KB loads and never touches LDS. A (row-major) is shared
+// by all waves and travels global -> LDS (global_load_lds_dwordx4, 8 rows x
+// 128 bytes per 1 KB transfer) through a ring of R slabs, XOR-swizzled as in
+// the 64x64 kernel; each wave reads its A fragments from there. (An A
+// fragment is 16 rows x 64 bytes, so loading it straight from row-major
+// memory touches 16 rows per instruction and runs several times slower.)
+// R - 1 slabs of A and W loads stay in flight behind the slab being
+// multiplied; every slab, including padding slabs past the range, issues
+// the same loads, so each ring slot is written the same way in every
+// iteration.
+template <GemmType T, int MF, int NW, int R>
+__global__ __launch_bounds__(64 * NW) void gemm_wp_kernel(GemmArgs g, float* partial,
+                                                          int* arrivals, int splits, int tiles_m,
+                                                          int tiles_n) {
+  static_assert(T != GemmType::kF32, "16-bit operands only");
+  constexpr int BMT = 16 * MF;          // tile rows
+  constexpr int BNT = 32 * NW;          // tile columns
+  constexpr int ASLAB = BMT * 128;      // one A slab in LDS
+  constexpr int TPW = 2 * MF / NW;      // A transfers (1 KB) per wave per slab
+  constexpr int G = TPW + 4;            // vector-memory instructions per wave per slab
+  static_assert(TPW >= 1 && TPW * NW == 2 * MF, "A transfers must split evenly over waves");
+  static_assert(R >= 2 && (R - 2) * G < 64, "ring depth");
+  static_assert(R * ASLAB <= 96 * 1024, "LDS ring");
+  typedef uint16_t E;
+  __shared__ __align__(16) unsigned char ring[R * ASLAB];
+
+  const int nwg = gridDim.x;
+  int bid = blockIdx.x;
+  const int full = (nwg / 8) * 8;
+  if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
+  const int tm = bid % tiles_m;
+  const int rest = bid / tiles_m;
+  const int tn = rest % tiles_n;
+  const int split = rest / tiles_n;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int fr = lane & 15;
+  const int fq = lane >> 4;
+  const int m0 = tm * BMT;
+  const int nw0 = tn * BNT + 32 * wave;  // this wave's first column
+  const bool cols_live = nw0 < g.N;
+  const E* const A = static_cast<const E*>(g.A);
+  const E* const W = static_cast<const E*>(g.W);
+  const int kb32 = g.K / 32;
+
+  // A transfers: wave w issues t = w*TPW .. w*TPW + TPW - 1, transfer t
+  // covering slab rows 8t .. 8t + 7; lane l lands at byte 16 l: row
+  // 8t + l / 8, physical chunk l % 8 holding logical chunk
+  // (l % 8) ^ ((row >> 1) & 7). Rows past M read row 0.
+  const E* a_src[TPW];
+  int a_off[TPW];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const int t = wave * TPW + u;
+    const int row = 8 * t + lane / 8;
+    const int lc = (lane % 8) ^ ((row >> 1) & 7);
+    const int ar = m0 + row;
+    a_src[u] = A + (int64_t)(ar < g.M ? ar : 0) * g.lda + lc * 8;
+    a_off[u] = t * 1024;
+  }
+  // W: this wave's 32-column block (block 0 for a wave past N: its loads
+  // stay in range, its products are never stored).
+  const E* const w_src = W + (int64_t)(cols_live ? nw0 / 32 : 0) * kb32 * 1024 + lane * 8;
+
+  const int ktiles = g.K / 64;
+  const int per = (ktiles + splits - 1) / splits;
+  const int kt0 = split * per;
+  const int nslab = max(min(ktiles, kt0 + per) - kt0, 0);
+
+  // A fragment rows of this lane within a slab, and their swizzle keys.
+  uint32_t arow[MF];
+  int akey[MF];
+#pragma unroll
+  for (int i = 0; i < MF; ++i) {
+    const int ra = 16 * i + fr;
+    arow[i] = ra * 128;
+    akey[i] = (ra >> 1) & 7;
+  }
+
+  float bias_v[2] = {0.0f, 0.0f};
+  if (g.ep.bias && cols_live) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) bias_v[c] = g.ep.bias[nw0 + 16 * c + fr];
+  }
+
+  floatx4 acc[MF][2];
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) acc[i][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  u32x4 wreg[R][4];  // [ring slot][k step * 2 + column fragment]
+  auto issue = [&](int i, int r, u32x4 (&dst)[4]) {
+    const int ks = kt0 + (i < nslab ? i : 0);
+    unsigned char* const st = ring + r * ASLAB;
+#pragma unroll
+    for (int u = 0; u < TPW; ++u)
+      __builtin_amdgcn_global_load_lds((gptr_t)(a_src[u] + (int64_t)ks * 64), (lptr_t)(st + a_off[u]),
+                                       16, 0, 0);
+    const E* const wp = w_src + (int64_t)ks * 2048;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = gload16(wp + q * 512);
+  };
+
+  const int npad = (nslab + R - 1) / R * R;
+#pragma unroll
+  for (int r = 0; r < R - 1; ++r) issue(r, r, wreg[r]);
+
+  for (int ib = 0; ib < npad; ib += R) {
+#pragma unroll
+    for (int jj = 0; jj < R; ++jj) {
+      const int i = ib + jj;
+      // Slab i's loads are complete once only the R - 2 later slabs' are
+      // outstanding; the barrier then shows every wave's A transfers and
+      // retires all reads of ring slot (jj - 1) mod R, the next target.
+      wait_vmcnt<(R - 2) * G>();
+      __asm__ volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      __asm__ volatile("" ::: "memory");
+      issue(i + R - 1, (jj + R - 1) % R, wreg[(jj + R - 1) % R]);
+      if (cols_live && i < nslab) {
+        const uint32_t st = lds_addr(ring) + (uint32_t)jj * ASLAB;
+        u32x4 af[2 * MF];  // [k step * MF + row fragment]
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int m = 0; m < MF; ++m)
+            af[h * MF + m] = ds_read16(st + arow[m] + (((h * 4 + fq) ^ akey[m]) << 4));
+        ds_wait_all(af);
+        const u32x4(&b)[4] = wreg[jj];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int m = 0; m < MF; ++m)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+              if constexpr (T == GemmType::kBF16) {
+                acc[m][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, af[h * MF + m]), __builtin_bit_cast(bf16x8, b[2 * h + c]),
+                    acc[m][c], 0, 0, 0);
+              } else {
+                acc[m][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(halfx8, af[h * MF + m]), __builtin_bit_cast(halfx8, b[2 * h + c]),
+                    acc[m][c], 0, 0, 0);
+              }
+            }
+      }
+    }
+  }
+  // The padding slabs' loads are still in flight: all of them land before
+  // the work-group goes on.
+  wait_vmcnt<0>();
+
+  // Fragment (m, c): lane holds rows 16 m + 4 fq + e, column 16 c + fr.
+  if (splits > 1) {
+    // (The host keeps splits * M * N within the int range.)
+    const int MN = g.M * g.N;
+    int off[MF][2][4];
+#pragma unroll
+    for (int m = 0; m < MF; ++m)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int n = nw0 + 16 * c + fr;
+          const int r = m0 + 16 * m + 4 * fq + e;
+          off[m][c][e] = (cols_live && r < g.M) ? r * g.N + n : -1;
+        }
+#pragma unroll
+    for (int m = 0; m < MF; ++m)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (off[m][c][e] >= 0)
+            __hip_atomic_store(partial + split * MN + off[m][c][e], acc[m][c][e], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    // Every partial store of this lane acknowledged at the agent-coherent
+    // level, then every wave's, before the tile counter sees this split.
+    wait_vmcnt<0>();
+    __shared__ int last_split;
+    __syncthreads();
+    int* const arrival = arrivals + (int64_t)tn * tiles_m + tm;
+    if (tid == 0)
+      last_split = __hip_atomic_fetch_add(arrival, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    __syncthreads();
+    if (!last_split) return;
+    if (tid == 0) __hip_atomic_store(arrival, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Sum in split order; this split's own part comes from its registers.
+    floatx4 sum[MF][2];
+#pragma unroll
+    for (int m = 0; m < MF; ++m)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) sum[m][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sp = 0; sp < splits; ++sp) {
+      float t[MF][2][4];
+#pragma unroll
+      for (int m = 0; m < MF; ++m)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            t[m][c][e] = (sp != split && off[m][c][e] >= 0)
+                             ? __hip_atomic_load(partial + sp * MN + off[m][c][e], __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)
+                             : acc[m][c][e];
+#pragma unroll
+      for (int m = 0; m < MF; ++m)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum[m][c][e] += t[m][c][e];
+    }
+#pragma unroll
+    for (int m = 0; m < MF; ++m)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) acc[m][c] = sum[m][c];
+  }
+  if (!cols_live) return;
+
+  // Epilogue: bias, rounding to the operand format, relu, residual, stores.
+  // Each option is one uniform branch around a loop over all of the lane's
+  // values, so the per-value code is straight-line; a tile whose rows all
+  // lie inside the output stores without bounds checks. The residual may be
+  // the output itself (x += f(x)): every residual read comes before any
+  // store.
+  constexpr int FMT = T == GemmType::kF16 ? kLpF16 : kLpBF16;
+  typedef __attribute__((address_space(1))) float gf32;
+  typedef __attribute__((address_space(1))) uint16_t gu16;
+  const GemmEpilogue& ep = g.ep;
+  float v[MF][2][4];
+#pragma unroll
+  for (int m = 0; m < MF; ++m)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[m][c][e] = acc[m][c][e] + bias_v[c];
+  if (ep.round_lp) {
+#pragma unroll
+    for (int m = 0; m < MF; ++m)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[m][c][e] = round_lp_t<FMT>(v[m][c][e]);
+  }
+  if (ep.act == 1) {
+#pragma unroll
+    for (int m = 0; m < MF; ++m)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[m][c][e] = fmaxf(v[m][c][e], 0.0f);
+  }
+  const int r0 = m0 + 4 * fq;  // element (m, c, e): row r0 + 16 m + e, column c0 + 16 c
+  const int c0 = nw0 + fr;
+  if (m0 + BMT <= g.M) {
+    if (ep.residual) {
+      float res[MF][2][4];
+#pragma unroll
+      for (int m = 0; m < MF; ++m)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            res[m][c][e] = *(const gf32*)(ep.residual + (int64_t)(r0 + 16 * m + e) * ep.ldr + c0 + 16 * c);
+#pragma unroll
+      for (int m = 0; m < MF; ++m)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[m][c][e] += res[m][c][e];
+    }
+    if (ep.out) {
+#pragma unroll
+      for (int m = 0; m < MF; ++m)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            *(gf32*)(ep.out + (int64_t)(r0 + 16 * m + e) * ep.ldo + c0 + 16 * c) = v[m][c][e];
+    }
+    if (ep.out_lp) {
+#pragma unroll
+      for (int m = 0; m < MF; ++m)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            *(gu16*)(ep.out_lp + (int64_t)(r0 + 16 * m + e) * ep.ldl + c0 + 16 * c) =
+                f32_to_lp_bits_t<FMT>(v[m][c][e]);
+    }
+    return;
+  }
+  // The tile's last rows run past M: every access checks its row.
+  if (ep.residual) {
+#pragma unroll
+    for (int m = 0; m < MF; ++m)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = r0 + 16 * m + e;
+          if (r < g.M) v[m][c][e] += ep.residual[(int64_t)r * ep.ldr + c0 + 16 * c];
+        }
+  }
+#pragma unroll
+  for (int m = 0; m < MF; ++m)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = r0 + 16 * m + e;
+        if (r < g.M) {
+          if (ep.out) ep.out[(int64_t)r * ep.ldo + c0 + 16 * c] = v[m][c][e];
+          if (ep.out_lp) ep.out_lp[(int64_t)r * ep.ldl + c0 + 16 * c] = f32_to_lp_bits_t<FMT>(v[m][c][e]);
+        }
+      }
+}
+
+// Row-major 16-bit W[N][K] -> the packed layout (one thread per 16-byte
+// chunk of the destination: lane l of fragment f reads 8 consecutive k of
+// one row).
+__global__ void pack_lp_weight_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                      int N, int K) {
+  const int64_t chunks = (int64_t)N * K / 8;
+  const int kb32 = K / 32;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < chunks;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(q % 64);
+    const int64_t f = q / 64;             // fragment: ((nb * kb32 + kb) * 2 + hf)
+    const int hf = (int)(f % 2);
+    const int64_t blk = f / 2;
+    const int kb = (int)(blk % kb32);
+    const int nb = (int)(blk / kb32);
+    const int n = nb * 32 + hf * 16 + lane % 16;
+    const int k = kb * 32 + 8 * (lane / 16);
+    const u32x4 v = gload16(src + (int64_t)n * K + k);
+    *reinterpret_cast<u32x4*>(dst + q * 8) = v;
+  }
+}
+
+// The same from fp32 rows, rounding each value to the 16-bit format on the
+// way (the engine's weight binding).
+__global__ void pack_f32_to_lp_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                                      int rows, int K, int fmt) {
+  const int64_t chunks = (int64_t)rows * K / 8;
+  const int kb32 = K / 32;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < chunks;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(q % 64);
+    const int64_t f = q / 64;
+    const int hf = (int)(f % 2);
+    const int64_t blk = f / 2;
+    const int kb = (int)(blk % kb32);
+    const int nb = (int)(blk / kb32);
+    const int n = nb * 32 + hf * 16 + lane % 16;
+    const int k = kb * 32 + 8 * (lane / 16);
+    const float* p = src + (int64_t)n * K + k;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)f32_to_lp_bits(p[2 * j], fmt) | ((uint32_t)f32_to_lp_bits(p[2 * j + 1], fmt) << 16);
+    *reinterpret_cast<u32x4*>(dst + q * 8) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+template <GemmType T, int MF, int NW, int R>
+void launch_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int splits,
+               int tiles_m, int tiles_n) {
+  hipLaunchKernelGGL((gemm_wp_kernel<T, MF, NW, R>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+                     dim3(64 * NW), 0, stream, g, ws.partial, ws.arrivals, splits, tiles_m,
+                     tiles_n);
+}
+
+// The packed-weight kernel for one GEMM (batch 1, W packed).
+int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int splits_hint) {
+  HK_REQUIRE(g.type != GemmType::kF32 && g.batch == 1 && g.A2 == nullptr && g.a_period == 0,
+             "gemm: a packed weight needs a 16-bit single GEMM");
+  HK_REQUIRE(packable(g.N, g.K), "gemm: packed weight shape N=%d K=%d", g.N, g.K);
+  const int fmt = g.type == GemmType::kF16 ? kLpF16 : kLpBF16;
+  HK_REQUIRE(!(g.ep.round_lp || g.ep.out_lp) || g.ep.lp_fmt == fmt,
+             "gemm: the packed kernel rounds to its operand format");
+  // Tile: the largest of 64x128, 64x64, 32x64, 32x32 (rows x columns) that
+  // still gives at least 160 work-groups (most of the 256 CUs) without
+  // splitting K; failing that the smallest, with K split to fill the device.
+  // Measured on the ensemble's shapes (M 77-256, N 2048-8448, K 128-4096):
+  // taller tiles or split K lose to more, smaller work-groups, because each
+  // CU's concurrent L2 misses, not its MFMA or LDS rate, bound these GEMMs.
+  static const int kTiles[4][2] = {{4, 4}, {4, 2}, {2, 2}, {2, 1}};  // (MF, NW)
+  int pick = 3;
+  for (int c = 0; c < 4; ++c) {
+    const int64_t t = (int64_t)((g.M + 16 * kTiles[c][0] - 1) / (16 * kTiles[c][0])) *
+                      ((g.N + 32 * kTiles[c][1] - 1) / (32 * kTiles[c][1]));
+    if (t >= 160) {
+      pick = c;
+      break;
+    }
+  }
+  const int mf = kTiles[pick][0];
+  const int nw = kTiles[pick][1];
+  constexpr int R = 4;
+  const int tiles_m = (g.M + 16 * mf - 1) / (16 * mf);
+  const int tiles_n = (g.N + 32 * nw - 1) / (32 * nw);
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
+  const int ktiles = g.K / 64;
+  int splits = splits_hint;
+  if (splits <= 0) {
+    splits = tiles >= 160 ? 1 : (int)((256 + tiles - 1) / tiles);
+    splits = std::min(splits, std::max(1, ktiles / 4));
+    splits = std::min(splits, 16);
+  }
+  splits = std::max(1, std::min(splits, ktiles));
+  while (splits > 1 && (int64_t)splits * g.M * g.N > ws.partial_elems) --splits;
+  if (tiles > ws.arrival_elems || ws.arrivals == nullptr) splits = 1;
+  const int per = (ktiles + splits - 1) / splits;
+  splits = (ktiles + per - 1) / per;
+  HK_REQUIRE(tiles * splits < (1LL << 31), "gemm: grid too large");
+  const bool f16 = g.type == GemmType::kF16;
+#define HK_WP_CASE(MF_, NW_, R_)                                                             \
+  if (mf == MF_ && nw == NW_ && R == R_) {                                                  \
+    if (f16)                                                                                \
+      launch_wp<GemmType::kF16, MF_, NW_, R_>(g, ws, stream, splits, tiles_m, tiles_n);     \
+    else                                                                                    \
+      launch_wp<GemmType::kBF16, MF_, NW_, R_>(g, ws, stream, splits, tiles_m, tiles_n);    \
+    HK_LAUNCH_CHECK();                                                                      \
+    return HK_OK;                                                                           \
+  }
+  HK_WP_CASE(4, 4, 4)
+  HK_WP_CASE(4, 2, 4)
+  HK_WP_CASE(2, 2, 4)
+  HK_WP_CASE(2, 1, 4)
+#undef HK_WP_CASE
+  HK_REQUIRE(false, "gemm: no packed kernel for MF=%d NW=%d R=%d", mf, nw, R);
+  return HK_ERR_ARG;
+}
+
 }  // namespace
+
+bool packable(int N, int K) { return N > 0 && K > 0 && N % 32 == 0 && K % 64 == 0; }
+
+int pack_lp_weight(const uint16_t* src, uint16_t* dst, int N, int K, hipStream_t stream) {
+  HK_REQUIRE(src && dst, "pack_lp_weight: null operand");
+  HK_REQUIRE(packable(N, K), "pack_lp_weight: N=%d K=%d (N a multiple of 32, K of 64)", N, K);
+  HK_REQUIRE(((uintptr_t)src & 15u) == 0 && ((uintptr_t)dst & 15u) == 0,
+             "pack_lp_weight: operands must be 16-byte aligned");
+  const int64_t chunks = (int64_t)N * K / 8;
+  const unsigned blocks = (unsigned)std::min<int64_t>((chunks + 255) / 256, 4096);
+  hipLaunchKernelGGL(pack_lp_weight_kernel, dim3(blocks), dim3(256), 0, stream, src, dst, N, K);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
+int pack_f32_to_lp(const float* src, uint16_t* dst, int rows, int K, int fmt, hipStream_t stream) {
+  HK_REQUIRE(src && dst, "pack_f32_to_lp: null operand");
+  HK_REQUIRE(rows > 0 && rows % 32 == 0 && K > 0 && K % 64 == 0,
+             "pack_f32_to_lp: rows=%d K=%d (rows a multiple of 32, K of 64)", rows, K);
+  HK_REQUIRE(((uintptr_t)dst & 15u) == 0, "pack_f32_to_lp: destination must be 16-byte aligned");
+  const int64_t chunks = (int64_t)rows * K / 8;
+  const unsigned blocks = (unsigned)std::min<int64_t>((chunks + 255) / 256, 4096);
+  hipLaunchKernelGGL(pack_f32_to_lp_kernel, dim3(blocks), dim3(256), 0, stream, src, dst, rows, K,
+                     fmt);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
 
 int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int splits_hint) {
   HK_REQUIRE(g.A && g.W && (g.ep.out || g.ep.out_lp), "gemm: null operand");
@@ -431,6 +927,7 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
                  g.w_bstride % align == 0,
              "gemm: leading dimensions must keep 16-byte alignment");
   if (g.M == 0) return HK_OK;
+  if (g.w_packed) return gemm_wp(g, ws, stream, splits_hint);
   const int tiles_m = (g.M + BM - 1) / BM;
   const int tiles_n = (g.N + BN - 1) / BN;
   const int64_t tiles = (int64_t)tiles_m * tiles_n * g.batch;

@@ -234,14 +234,33 @@ def slstm_step(state, i, f, z, o, mask=None):
 _LP = {torch.bfloat16: 0, torch.float16: 1}
 
 
-def cast_linear(x, weight, bias=None, workspace=None):
+def pack_cast_weight(weight):
+    """A CastLinear weight [N, K] (bf16/fp16, N a multiple of 32, K of 64)
+    rearranged into the matrix-core layout the engine's projection GEMM
+    streams (hk_pack_cast_weight). The result has the same dtype and shape;
+    only cast_linear(..., packed=True) reads it."""
+    assert weight.dtype in _LP, f"weight must be bf16 or fp16, got {weight.dtype}"
+    assert weight.dim() == 2 and weight.is_contiguous(), "weight must be a contiguous [N, K] matrix"
+    N, K = weight.shape
+    assert N % 32 == 0 and K % 64 == 0, f"packing needs N % 32 == 0 and K % 64 == 0, got {N} x {K}"
+    if weight.device.type != "cuda":
+        raise _lib.HipLibraryError("pack_cast_weight needs a GPU tensor")
+    out = torch.empty_like(weight)
+    _lib.check(_lib.lib().hk_pack_cast_weight(weight.data_ptr(), out.data_ptr(), N, K,
+                                              _lib.current_stream(weight.device)),
+               "hk_pack_cast_weight")
+    return out
+
+
+def cast_linear(x, weight, bias=None, workspace=None, packed=False):
     """CastLinear.forward (example_model.py:92-95): F.linear(x.to(lp),
     weight, bias).to(float32) for a weight held in bf16 or fp16.
 
     x: fp32 [..., K] (cast to the weight's dtype, as CastLinear does);
-    weight: [N, K] bf16/fp16 contiguous; bias: [N] in the weight's dtype or
-    None; workspace: optional zero-filled uint8 CUDA tensor (>= 256 KiB) for
-    split-K. Returns fp32 [..., N]."""
+    weight: [N, K] bf16/fp16 contiguous (with packed=True, the output of
+    pack_cast_weight: the engine's kernel); bias: [N] in the weight's dtype
+    or None; workspace: optional zero-filled uint8 CUDA tensor (>= 256 KiB)
+    for split-K. Returns fp32 [..., N]."""
     assert weight.dtype in _LP, f"weight must be bf16 or fp16, got {weight.dtype}"
     assert weight.dim() == 2 and weight.is_contiguous(), "weight must be a contiguous [N, K] matrix"
     N, K = weight.shape
@@ -259,7 +278,8 @@ def cast_linear(x, weight, bias=None, workspace=None):
     if workspace is not None:
         assert workspace.dtype == torch.uint8 and workspace.device == dev
         ws, ws_bytes = workspace.data_ptr(), workspace.numel()
-    _lib.check(_lib.lib().hk_cast_linear(
+    fn = "hk_cast_linear_packed" if packed else "hk_cast_linear"
+    _lib.check(getattr(_lib.lib(), fn)(
         xl.data_ptr(), weight.data_ptr(), _lib.ptr(b), out.data_ptr(), xl.shape[0], N, K,
-        _LP[weight.dtype], ws, ws_bytes, _lib.current_stream(dev)), "hk_cast_linear")
+        _LP[weight.dtype], ws, ws_bytes, _lib.current_stream(dev)), fn)
     return out.reshape(*x.shape[:-1], N)

@@ -97,6 +97,24 @@ int hk_block_linear(const float* x, const float* weight, const float* bias, floa
 int hk_cast_linear(const uint16_t* x, const uint16_t* w, const float* bias, float* out, int M,
                    int N, int K, int fmt, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* A CastLinear weight (example_model.py:82-95, the 16-bit W of
+ * convert_linears :109-148) rearranged once, at load time, into the layout
+ * the engine's projection GEMM streams: w [N,K] 16-bit row-major -> packed
+ * [N*K] (N a multiple of 32, K of 64, both 16-byte aligned). For each block
+ * of 32 output columns and 32-deep block of K, two 1 KB matrix-core operand
+ * fragments of 16 columns in lane order (element (n, k) at
+ * ((((n/32)*(K/32) + k/32)*2 + (n%32)/16)*64 + n%16 + 16*((k%32)/8))*8 + k%8).
+ * Stream-ordered on `stream`. */
+int hk_pack_cast_weight(const uint16_t* w, uint16_t* packed, int N, int K, void* stream);
+
+/* hk_cast_linear with the weight in the hk_pack_cast_weight layout: the
+ * kernel the engine runs for every CastLinear projection (the weight slots
+ * are packed at binding). Same operands, result and workspace rules as
+ * hk_cast_linear; N a multiple of 32. */
+int hk_cast_linear_packed(const uint16_t* x, const uint16_t* w_packed, const float* bias,
+                          float* out, int M, int N, int K, int fmt, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
 /* RGLRU.forward after its two BlockLinears (model/hawk.py:31-37):
  * i = sigmoid(gate_i), r = sigmoid(gate_r), a_t = a ** (c * r),
  * h <- h * a_t + sqrt(1 - a_t^2) * (i * x); out (NULL = none) = new h on

@@ -269,3 +269,55 @@ def test_cast_linear_matches_castlinear(dev, dtype, M, N, K):
         assert bool(((got - cpu).abs() <= 2 * (_ulp(torch.maximum(got.abs(), cpu.abs()), dtype) + acc)).all())
     # the workspace is left zeroed (its arrival counters) for the next call
     assert int(ws[: 1 << 18].sum()) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(256, 8192, 2048), (256, 4096, 2048), (256, 2048, 2048),
+                                   (179, 8448, 2048), (77, 2048, 4096), (37, 2048, 4096),
+                                   (5, 8448, 2048), (1, 64, 64), (100, 320, 640), (300, 1024, 192)])
+def test_cast_linear_packed_matches_castlinear(dev, dtype, M, N, K):
+    """The engine's projection kernel (hk_cast_linear_packed, the weight
+    rearranged by hk_pack_cast_weight) against CastLinear's expression at the
+    bar of test_cast_linear_matches_castlinear. The shapes cover every tile
+    of the kernel (64x128, 64x64, 32x64, 32x32; rows past M, split K when the
+    tiles cannot fill the device) and the tick's projections; the packed
+    result also equals the row-major kernel's within the same bound."""
+    from hackathon_amd import kernels as hk
+
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g)
+    w = (torch.rand(N, K, generator=g) * 2 - 1) * K ** -0.5
+    b = (torch.rand(N, generator=g) * 0.1 - 0.05)
+    xl, wl, bl = x.to(dtype), w.to(dtype), b.to(dtype)
+    exact = (xl.double() @ wl.double().T + bl.double()).to(dtype).to(torch.float32)
+    acc = 16 * 2.0 ** -24 * (xl.double().abs() @ wl.double().abs().T + bl.double().abs()).float()
+    wd = wl.to(dev)
+    packed = hk.pack_cast_weight(wd)
+    assert not torch.equal(packed, wd) or N * K <= 64 * 64
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+    for workspace in (None, ws):
+        got = hk.cast_linear(x.to(dev), packed, bl.to(dev), workspace=workspace, packed=True).cpu()
+        d = (got - exact).abs()
+        ulp = _ulp(torch.maximum(got.abs(), exact.abs()), dtype)
+        assert bool((d <= ulp + acc).all()), float((d / (ulp + acc)).max())
+        assert float((d == 0).float().mean()) >= 0.98
+        rm = hk.cast_linear(x.to(dev), wd, bl.to(dev), workspace=workspace).cpu()
+        assert bool(((got - rm).abs() <= 2 * (_ulp(torch.maximum(got.abs(), rm.abs()), dtype) + acc)).all())
+    assert int(ws[: 1 << 18].sum()) == 0
+
+
+def test_pack_cast_weight_layout(dev):
+    """hk_pack_cast_weight moves element (n, k) of W to
+    ((((n/32)*(K/32) + k/32)*2 + (n%32)/16)*64 + n%16 + 16*((k%32)/8))*8 + k%8:
+    a permutation, checked element by element against that formula."""
+    from hackathon_amd import kernels as hk
+
+    N, K = 96, 192
+    w = torch.arange(N * K, dtype=torch.int32).remainder(65521).to(torch.int16).view(torch.bfloat16)
+    w = w.reshape(N, K).contiguous()
+    p = hk.pack_cast_weight(w.to(dev)).cpu().view(torch.int16).reshape(-1)
+    n = torch.arange(N).view(N, 1).expand(N, K)
+    k = torch.arange(K).view(1, K).expand(N, K)
+    lane = n % 16 + 16 * ((k % 32) // 8)
+    idx = ((((n // 32) * (K // 32) + k // 32) * 2 + (n % 32) // 16) * 64 + lane) * 8 + k % 8
+    assert torch.equal(p[idx.reshape(-1)], w.view(torch.int16).reshape(-1))
