@@ -80,6 +80,9 @@ def matrix_scan_bytes(ticks, first, depth, tile_bytes, entry_bytes, row_bytes):
 
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 GEMM_COUNTERS = os.path.join(PROFILES, "gemm_cast_linear_tick_replay_hbm_counters.txt")
+# The packed projection kernel's tile rule inside an engine tick (gemm.h
+# kMinTilesShared); 0 selects the rule for a GEMM alone on the device.
+TICK_MIN_WORK_GROUPS = 112
 
 
 def counter_traffic(path, algorithmic_per_dispatch):
@@ -474,7 +477,7 @@ def tick_projections(cfg, run_off):
     return out
 
 
-def gemm_replay(torch, dev, shapes, reps=3):
+def gemm_replay(torch, dev, shapes, reps=3, min_work_groups=0):
     """The given CastLinear GEMMs through hk_cast_linear_packed (bf16, the
     engine's projection kernel, weights packed by hk_pack_cast_weight as the
     engine packs its slots) on one stream, each with weights of its own (so
@@ -509,8 +512,8 @@ def gemm_replay(torch, dev, shapes, reps=3):
 
     def launch(m, n, k, w):
         st = lib.hk_cast_linear_packed(x.data_ptr(), w.data_ptr(), bias.data_ptr(),
-                                       out.data_ptr(), m, n, k, 0, ws.data_ptr(), ws.numel(),
-                                       stream)
+                                       out.data_ptr(), m, n, k, 0, min_work_groups,
+                                       ws.data_ptr(), ws.numel(), stream)
         if st != 0:
             raise RuntimeError(lib.hk_last_error().decode())
 
@@ -1080,6 +1083,10 @@ def main() -> int:
     shapes = tick_projections(cfg, first.run_off)
     g_avg, _, g_bytes, g_flops = gemm_replay(torch, dev, shapes)
     grf = gemm_roofline(g_avg, g_bytes, g_flops)
+    # The same launches under the tile rule the engine uses inside a tick
+    # (at least 112 work-groups: three other streams share the device).
+    t_avg, _, _, _ = gemm_replay(torch, dev, shapes, min_work_groups=TICK_MIN_WORK_GROUPS)
+    trf = gemm_roofline(t_avg, g_bytes, g_flops)
 
     # The serving path on the same engine: NnInferenceClient.process_batch
     # on dicts of request objects (the reference's interface), wall clock
@@ -1164,6 +1171,11 @@ def main() -> int:
                        "gemm runs the same replay; profiles/ holds its rocprofv3 kernel-trace "
                        "and counter summaries); algorithmic bytes = bf16 W + bf16 A + fp32 out "
                        "+ bias"),
+            "tick_tile_rule": {"min_work_groups": TICK_MIN_WORK_GROUPS, "avg_us": trf["avg_us"],
+                               "achieved": trf["achieved_GBs"], "frac": trf["hbm_frac"],
+                               "note": "the same replay with the tile rule the engine uses "
+                                       "inside a tick (larger tiles: the tick is faster, the "
+                                       "lone GEMM slower)"},
             "secondary": {"mlstm_scan_isolated": isolated_mlstm_scan(torch, dev)},
         },
         "kernels": kernels,

@@ -50,7 +50,7 @@ _SIGNATURES = {
     "hk_pack_tick": (c_int, [c_void_p] * 2 + [c_int] + [c_void_p] * 6),
     "hk_cast_linear": (c_int, [c_void_p] * 4 + [c_int] * 4 + [c_void_p, c_int64, c_void_p]),
     "hk_pack_cast_weight": (c_int, [c_void_p] * 2 + [c_int] * 2 + [c_void_p]),
-    "hk_cast_linear_packed": (c_int, [c_void_p] * 4 + [c_int] * 4 + [c_void_p, c_int64, c_void_p]),
+    "hk_cast_linear_packed": (c_int, [c_void_p] * 4 + [c_int] * 5 + [c_void_p, c_int64, c_void_p]),
 }
 
 _lib = None

@@ -568,8 +568,8 @@ int hk_pack_cast_weight(const uint16_t* w, uint16_t* packed, int N, int K, void*
 }
 
 int hk_cast_linear_packed(const uint16_t* x, const uint16_t* w_packed, const float* bias,
-                          float* out, int M, int N, int K, int fmt, void* workspace,
-                          int64_t workspace_bytes, void* stream) {
+                          float* out, int M, int N, int K, int fmt, int min_work_groups,
+                          void* workspace, int64_t workspace_bytes, void* stream) {
   constexpr int64_t kCastArrivals = 1 << 16;
   HK_REQUIRE(x && w_packed && out, "hk_cast_linear_packed: null operand");
   HK_REQUIRE(M >= 0 && hk::packable(N, K),
@@ -578,7 +578,7 @@ int hk_cast_linear_packed(const uint16_t* x, const uint16_t* w_packed, const flo
   HK_REQUIRE(fmt == hk::kLpBF16 || fmt == hk::kLpF16, "hk_cast_linear_packed: format %d", fmt);
   HK_REQUIRE(hk::aligned16(x) && hk::aligned16(w_packed),
              "hk_cast_linear_packed: operands must be 16-byte aligned");
-  HK_REQUIRE(K % 8 == 0, "hk_cast_linear_packed: K=%d", K);
+  HK_REQUIRE(min_work_groups >= 0, "hk_cast_linear_packed: min_work_groups=%d", min_work_groups);
   HK_REQUIRE(workspace == nullptr || workspace_bytes >= kCastArrivals * 4,
              "hk_cast_linear_packed: a workspace needs at least %lld bytes",
              (long long)kCastArrivals * 4);
@@ -589,6 +589,7 @@ int hk_cast_linear_packed(const uint16_t* x, const uint16_t* w_packed, const flo
   g.lda = K;
   g.W = w_packed;
   g.w_packed = true;
+  g.min_tiles = min_work_groups;
   g.M = M;
   g.N = N;
   g.K = K;

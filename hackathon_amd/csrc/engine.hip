@@ -557,6 +557,11 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
   g.W = lin.w->ptr;
   g.ldw = K;
   g.w_packed = lp && lin.w->packed;
+  // A tick's four streams share the device: above 64 rows the larger tiles
+  // of the shared rule measure faster in the tick (C4: 9.21-9.24 against
+  // 9.34-9.37 ms); at 64 rows (the B=64 latency tick) the lone rule's
+  // smaller tiles do (p50 5.09 against 5.17 ms).
+  g.min_tiles = M > 64 ? kMinTilesShared : kMinTilesAlone;
   g.M = M;
   g.N = N;
   g.K = K;

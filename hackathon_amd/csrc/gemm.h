@@ -15,6 +15,15 @@ namespace hk {
 
 enum class GemmType { kBF16 = 0, kF32 = 1, kF16 = 2 };
 
+// Work-group counts of the packed kernel's tile rule (measured on the
+// ensemble's projection shapes): alone on the device, 160 (most of the 256
+// CUs; CastLinear replay 14.8 us per launch against 16.6 at 112); inside a
+// four-stream tick, 112 for GEMMs of more than 64 rows (larger tiles re-read
+// less and crowd the other streams less: C4 tick 9.21-9.24 ms against
+// 9.34-9.37 at 160).
+constexpr int kMinTilesAlone = 160;
+constexpr int kMinTilesShared = 112;
+
 struct GemmEpilogue {
   const float* bias = nullptr;      // [N] (per batch: + b*c_bstride)
   const float* residual = nullptr;  // [M, ldr] added last
@@ -48,6 +57,11 @@ struct GemmArgs {
   // 16-bit W held in the fragment-packed layout of pack_lp_weight (ldw is
   // then unused; N and K must be multiples of 32 and 64).
   bool w_packed = false;
+  // Packed kernel's tile rule: the largest tile that still gives at least
+  // this many work-groups without splitting K (0: kMinTilesAlone, for a GEMM
+  // that has the device to itself; the engine's ticks, where three other
+  // streams share the device, pass kMinTilesShared).
+  int min_tiles = 0;
   GemmEpilogue ep;
 };
 

@@ -829,17 +829,18 @@ int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int 
   HK_REQUIRE(!(g.ep.round_lp || g.ep.out_lp) || g.ep.lp_fmt == fmt,
              "gemm: the packed kernel rounds to its operand format");
   // Tile: the largest of 64x128, 64x64, 32x64, 32x32 (rows x columns) that
-  // still gives at least 160 work-groups (most of the 256 CUs) without
-  // splitting K; failing that the smallest, with K split to fill the device.
-  // Measured on the ensemble's shapes (M 77-256, N 2048-8448, K 128-4096):
-  // taller tiles or split K lose to more, smaller work-groups, because each
-  // CU's concurrent L2 misses, not its MFMA or LDS rate, bound these GEMMs.
+  // still gives at least min_tiles work-groups without splitting K; failing
+  // that the smallest, with K split to fill the device. Measured on the
+  // ensemble's shapes (M 77-256, N 2048-8448, K 128-4096): taller tiles or
+  // split K lose to more, smaller work-groups, because each CU's concurrent
+  // L2 misses, not its MFMA or LDS rate, bound these GEMMs.
+  const int min_tiles = g.min_tiles > 0 ? g.min_tiles : kMinTilesAlone;
   static const int kTiles[4][2] = {{4, 4}, {4, 2}, {2, 2}, {2, 1}};  // (MF, NW)
   int pick = 3;
   for (int c = 0; c < 4; ++c) {
     const int64_t t = (int64_t)((g.M + 16 * kTiles[c][0] - 1) / (16 * kTiles[c][0])) *
                       ((g.N + 32 * kTiles[c][1] - 1) / (32 * kTiles[c][1]));
-    if (t >= 160) {
+    if (t >= min_tiles) {
       pick = c;
       break;
     }
@@ -853,7 +854,7 @@ int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int 
   const int ktiles = g.K / 64;
   int splits = splits_hint;
   if (splits <= 0) {
-    splits = tiles >= 160 ? 1 : (int)((256 + tiles - 1) / tiles);
+    splits = tiles >= min_tiles ? 1 : (int)((256 + tiles - 1) / tiles);
     splits = std::min(splits, std::max(1, ktiles / 4));
     splits = std::min(splits, 16);
   }

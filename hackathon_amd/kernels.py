@@ -252,7 +252,7 @@ def pack_cast_weight(weight):
     return out
 
 
-def cast_linear(x, weight, bias=None, workspace=None, packed=False):
+def cast_linear(x, weight, bias=None, workspace=None, packed=False, min_work_groups=0):
     """CastLinear.forward (example_model.py:92-95): F.linear(x.to(lp),
     weight, bias).to(float32) for a weight held in bf16 or fp16.
 
@@ -260,7 +260,8 @@ def cast_linear(x, weight, bias=None, workspace=None, packed=False):
     weight: [N, K] bf16/fp16 contiguous (with packed=True, the output of
     pack_cast_weight: the engine's kernel); bias: [N] in the weight's dtype
     or None; workspace: optional zero-filled uint8 CUDA tensor (>= 256 KiB)
-    for split-K. Returns fp32 [..., N]."""
+    for split-K; min_work_groups: the packed kernel's tile rule (0: the
+    device to itself). Returns fp32 [..., N]."""
     assert weight.dtype in _LP, f"weight must be bf16 or fp16, got {weight.dtype}"
     assert weight.dim() == 2 and weight.is_contiguous(), "weight must be a contiguous [N, K] matrix"
     N, K = weight.shape
@@ -278,8 +279,15 @@ def cast_linear(x, weight, bias=None, workspace=None, packed=False):
     if workspace is not None:
         assert workspace.dtype == torch.uint8 and workspace.device == dev
         ws, ws_bytes = workspace.data_ptr(), workspace.numel()
-    fn = "hk_cast_linear_packed" if packed else "hk_cast_linear"
-    _lib.check(getattr(_lib.lib(), fn)(
-        xl.data_ptr(), weight.data_ptr(), _lib.ptr(b), out.data_ptr(), xl.shape[0], N, K,
-        _LP[weight.dtype], ws, ws_bytes, _lib.current_stream(dev)), fn)
+    lib = _lib.lib()
+    if packed:
+        st = lib.hk_cast_linear_packed(xl.data_ptr(), weight.data_ptr(), _lib.ptr(b), out.data_ptr(),
+                                       xl.shape[0], N, K, _LP[weight.dtype], int(min_work_groups),
+                                       ws, ws_bytes, _lib.current_stream(dev))
+        _lib.check(st, "hk_cast_linear_packed")
+    else:
+        st = lib.hk_cast_linear(xl.data_ptr(), weight.data_ptr(), _lib.ptr(b), out.data_ptr(),
+                                xl.shape[0], N, K, _LP[weight.dtype], ws, ws_bytes,
+                                _lib.current_stream(dev))
+        _lib.check(st, "hk_cast_linear")
     return out.reshape(*x.shape[:-1], N)

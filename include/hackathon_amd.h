@@ -110,10 +110,14 @@ int hk_pack_cast_weight(const uint16_t* w, uint16_t* packed, int N, int K, void*
 /* hk_cast_linear with the weight in the hk_pack_cast_weight layout: the
  * kernel the engine runs for every CastLinear projection (the weight slots
  * are packed at binding). Same operands, result and workspace rules as
- * hk_cast_linear; N a multiple of 32. */
+ * hk_cast_linear; N a multiple of 32. min_work_groups selects the tile: the
+ * largest that still gives that many work-groups without splitting K (0:
+ * 160, for a GEMM that has the device to itself; the engine's four-stream
+ * ticks use 112 above 64 rows). The result does not depend on it beyond fp32 summation
+ * order. */
 int hk_cast_linear_packed(const uint16_t* x, const uint16_t* w_packed, const float* bias,
-                          float* out, int M, int N, int K, int fmt, void* workspace,
-                          int64_t workspace_bytes, void* stream);
+                          float* out, int M, int N, int K, int fmt, int min_work_groups,
+                          void* workspace, int64_t workspace_bytes, void* stream);
 
 /* RGLRU.forward after its two BlockLinears (model/hawk.py:31-37):
  * i = sigmoid(gate_i), r = sigmoid(gate_r), a_t = a ** (c * r),

@@ -280,8 +280,10 @@ def test_cast_linear_packed_matches_castlinear(dev, dtype, M, N, K):
     rearranged by hk_pack_cast_weight) against CastLinear's expression at the
     bar of test_cast_linear_matches_castlinear. The shapes cover every tile
     of the kernel (64x128, 64x64, 32x64, 32x32; rows past M, split K when the
-    tiles cannot fill the device) and the tick's projections; the packed
-    result also equals the row-major kernel's within the same bound."""
+    tiles cannot fill the device) and the tick's projections, under the tile
+    rule of a lone GEMM, of the engine's ticks (112 work-groups) and one no
+    shape meets (always the smallest tile, K split); the packed result also
+    equals the row-major kernel's within the same bound."""
     from hackathon_amd import kernels as hk
 
     g = torch.Generator().manual_seed(M + N + K)
@@ -295,8 +297,9 @@ def test_cast_linear_packed_matches_castlinear(dev, dtype, M, N, K):
     packed = hk.pack_cast_weight(wd)
     assert not torch.equal(packed, wd) or N * K <= 64 * 64
     ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
-    for workspace in (None, ws):
-        got = hk.cast_linear(x.to(dev), packed, bl.to(dev), workspace=workspace, packed=True).cpu()
+    for workspace, mwg in ((None, 0), (ws, 0), (ws, 112), (ws, 1 << 20)):
+        got = hk.cast_linear(x.to(dev), packed, bl.to(dev), workspace=workspace, packed=True,
+                             min_work_groups=mwg).cpu()
         d = (got - exact).abs()
         ulp = _ulp(torch.maximum(got.abs(), exact.abs()), dtype)
         assert bool((d <= ulp + acc).all()), float((d / (ulp + acc)).max())
