@@ -784,10 +784,9 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   m.row_parts = row_parts(r, d.hs_m);
   m.out_part_stride = (int64_t)n * I;
   HK_TRY(timed_mat_scan(e, 0, m, s));
-  HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(mlstm_post(w.NUM, m.row_parts, m.out_part_stride, w.DEN, d.nh, F32(e, kXLSTM, l, X_L_GN_W), F32(e, kXLSTM, l, X_L_GN_B),
                     F32(e, kXLSTM, l, X_L_SKIP), w.XMC, w.XMG + I, 2 * I, n, I, d.nh, w.HS.f,
-                    w.HS.l, e.lp_fmt, s));
+                    w.HS.l, e.lp_fmt, log_commit_of(m), s));
   HK_TRY(linear(e, w, w.HS, I, {S(e, kXLSTM, l, X_L_DOWN_W), nullptr}, n, H, I, 0, w.X1, H, w.X2,
                 H, nullptr, 0, s));
   // final_norm and the Block's residual (x = final_norm(x2) + x) are applied
@@ -828,9 +827,9 @@ int run_mamba2(Engine& e, int l, const Runs& r, hipStream_t s) {
   // tower's stream is not the one that ends the tick)
   m.out_part_stride = (int64_t)n * I;
   HK_TRY(timed_mat_scan(e, 1, m, s));
-  HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(mamba2_post(w.YS, m.row_parts, m.out_part_stride, w.MXC, C, w.PROJ + C, W, F32(e, kMamba2, l, M_D),
-                     F32(e, kMamba2, l, M_NORM), n, I, d.hm, w.YN.f, w.YN.l, e.lp_fmt, s));
+                     F32(e, kMamba2, l, M_NORM), n, I, d.hm, w.YN.f, w.YN.l, e.lp_fmt,
+                     log_commit_of(m), s));
   HK_TRY(linear(e, w, w.YN, I, {S(e, kMamba2, l, M_OUT_W), nullptr}, n, H, I, 0, w.X.f, H, w.X.f,
                 H, nullptr, 0, s));
   return HK_OK;
@@ -864,9 +863,8 @@ int run_retnet(Engine& e, int l, const Runs& r, hipStream_t s) {
   m.row_parts = row_parts(r, d.hs_r);
   m.out_part_stride = (int64_t)n * H;
   HK_TRY(timed_mat_scan(e, 2, m, s));
-  HK_TRY(launch_mat_log_commit(m, s));
   HK_TRY(retnet_post(w.O, m.row_parts, m.out_part_stride, w.QKVG + 3 * H, 4 * H, n, H, d.hs_r,
-                     w.YO.f, w.YO.l, e.lp_fmt, s));
+                     w.YO.f, w.YO.l, e.lp_fmt, log_commit_of(m), s));
   HK_TRY(linear(e, w, w.YO, H, {S(e, kRetNet, l, R_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f,
                 H, nullptr, 0, s));
   return HK_OK;

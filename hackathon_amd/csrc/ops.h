@@ -6,6 +6,7 @@
 #pragma once
 
 #include "common.h"
+#include "scan_mat.h"
 
 namespace hk {
 
@@ -34,7 +35,7 @@ int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, u
 int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const float* x,
                 int64_t ldx, const float* z, int64_t ldz, const float* d, const float* w,
                 int n_rows, int inner, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
-                hipStream_t s);
+                const LogCommit& lc, hipStream_t s);
 
 // dt = softplus(dt_raw); decay = exp(a[head] * dt) (model/mamba2.py:92-97).
 int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float* dt,
@@ -44,7 +45,7 @@ int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float*
 // (eps 1e-6, no affine), times silu(g). o is the sum of n_parts planes.
 int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g, int64_t ldg,
                 int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
-                hipStream_t s);
+                const LogCommit& lc, hipStream_t s);
 
 // sLSTM block tail + mLSTM block norm (model/xlstm.py:422-424, :308):
 // x1 = GroupNorm(groups)(y) + skip; xn = LayerNorm(x1) * w_ln.
@@ -70,7 +71,7 @@ int layernorm_rows(const float* x, const float* w, const float* residual, int n_
 int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* den, int den_ld,
                const float* gn_w, const float* gn_b, const float* skip_w, const float* x_conv,
                const float* x_gate, int64_t ld_gate, int n_rows, int inner, int heads,
-               float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s);
+               float* out, uint16_t* out_lp, int lp_fmt, const LogCommit& lc, hipStream_t s);
 
 // preds[r, col] = x[r] . w + b (shared output_proj, model/inference_model.py:142).
 int output_proj(const float* x, const float* w, const float* b, int n_rows, int hidden,

@@ -180,7 +180,12 @@ __global__ __launch_bounds__(256) void mamba2_post_kernel(
     const float* __restrict__ ssm_out, int n_parts, int64_t part_stride,
     const float* __restrict__ x, int64_t ldx, const float* __restrict__ z, int64_t ldz,
     const float* __restrict__ d, const float* __restrict__ w, int inner, int head_size,
-    float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt) {
+    float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt, int n_rows, LogCommit lc) {
+  if ((int)blockIdx.x >= n_rows) {  // the scan's log-header update (LogCommit)
+    const int i = ((int)blockIdx.x - n_rows) * (int)blockDim.x + (int)threadIdx.x;
+    if (i < lc.jobs()) log_commit_one(lc, i);
+    return;
+  }
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const float* xr = x + row * ldx;
@@ -228,7 +233,12 @@ constexpr int kHeadPostMax = 16;
 __global__ void retnet_post_kernel(const float* __restrict__ o, int n_parts, int64_t part_stride,
                                    const float* __restrict__ g, int64_t ldg, int hidden,
                                    int head_size, float* __restrict__ out,
-                                   uint16_t* __restrict__ out_lp, int lp_fmt) {
+                                   uint16_t* __restrict__ out_lp, int lp_fmt, int n_rows, LogCommit lc) {
+  if ((int)blockIdx.x >= n_rows) {  // the scan's log-header update (LogCommit)
+    const int i = ((int)blockIdx.x - n_rows) * (int)blockDim.x + (int)threadIdx.x;
+    if (i < lc.jobs()) log_commit_one(lc, i);
+    return;
+  }
   const int64_t row = blockIdx.x;
   const int head = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -314,7 +324,12 @@ __global__ void mlstm_post_kernel(const float* __restrict__ num, int n_parts, in
                                   const float* __restrict__ skip_w,
                                   const float* __restrict__ x_conv,
                                   const float* __restrict__ x_gate, int64_t ld_gate, int inner,
-                                  int hs, float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt) {
+                                  int hs, float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt, int n_rows, LogCommit lc) {
+  if ((int)blockIdx.x >= n_rows) {  // the scan's log-header update (LogCommit)
+    const int i = ((int)blockIdx.x - n_rows) * (int)blockDim.x + (int)threadIdx.x;
+    if (i < lc.jobs()) log_commit_one(lc, i);
+    return;
+  }
   const int64_t row = blockIdx.x;
   const int head = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -578,15 +593,21 @@ int stage_features(const float* feat, int n_rows, int f, int kpad, float* out, u
   return HK_OK;
 }
 
+// Rows plus the work-groups of a LogCommit job of `threads`-thread groups.
+unsigned rows_and_commit(int n_rows, const LogCommit& lc, int threads) {
+  return (unsigned)(n_rows + (lc.jobs() + threads - 1) / threads);
+}
+
 int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const float* x,
                 int64_t ldx, const float* z, int64_t ldz, const float* d, const float* w,
                 int n_rows, int inner, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
-                hipStream_t s) {
-  if (n_rows == 0) return HK_OK;
+                const LogCommit& lc, hipStream_t s) {
+  if (n_rows == 0 && lc.jobs() == 0) return HK_OK;
   HK_REQUIRE(inner <= 256 * kMambaPostMax && n_parts >= 1,
              "mamba2_post: inner %d above %d or no planes", inner, 256 * kMambaPostMax);
-  hipLaunchKernelGGL(mamba2_post_kernel, dim3(n_rows), dim3(256), 0, s, ssm_out, n_parts,
-                     part_stride, x, ldx, z, ldz, d, w, inner, head_size, out, out_lp, lp_fmt);
+  hipLaunchKernelGGL(mamba2_post_kernel, dim3(rows_and_commit(n_rows, lc, 256)), dim3(256), 0, s,
+                     ssm_out, n_parts, part_stride, x, ldx, z, ldz, d, w, inner, head_size, out,
+                     out_lp, lp_fmt, n_rows, lc);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
@@ -602,14 +623,15 @@ int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float*
 
 int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g, int64_t ldg,
                 int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
-                hipStream_t s) {
-  if (n_rows == 0) return HK_OK;
+                const LogCommit& lc, hipStream_t s) {
+  if (n_rows == 0 && lc.jobs() == 0) return HK_OK;
   const int heads = hidden / head_size;
   HK_REQUIRE(heads * head_size == hidden && heads <= 16 && head_size <= 64 * kHeadPostMax &&
                  n_parts >= 1,
              "retnet_post: %d heads of %d unsupported", heads, head_size);
-  hipLaunchKernelGGL(retnet_post_kernel, dim3(n_rows), dim3(64 * heads), 0, s, o, n_parts,
-                     part_stride, g, ldg, hidden, head_size, out, out_lp, lp_fmt);
+  hipLaunchKernelGGL(retnet_post_kernel, dim3(rows_and_commit(n_rows, lc, 64 * heads)),
+                     dim3(64 * heads), 0, s, o, n_parts, part_stride, g, ldg, hidden, head_size,
+                     out, out_lp, lp_fmt, n_rows, lc);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
@@ -641,16 +663,16 @@ int layernorm_rows(const float* x, const float* w, const float* residual, int n_
 int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* den, int den_ld,
                const float* gn_w, const float* gn_b, const float* skip_w, const float* x_conv,
                const float* x_gate, int64_t ld_gate, int n_rows, int inner, int heads,
-               float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s) {
-  if (n_rows == 0) return HK_OK;
+               float* out, uint16_t* out_lp, int lp_fmt, const LogCommit& lc, hipStream_t s) {
+  if (n_rows == 0 && lc.jobs() == 0) return HK_OK;
   HK_REQUIRE(heads >= 1 && heads <= 16 && inner % heads == 0 &&
                  inner / heads <= 64 * kHeadPostMax && n_parts >= 1,
              "mlstm_post: %d heads of %d unsupported", heads, inner / std::max(heads, 1));
   const int hs = inner / heads;
 #define HK_POST(U, F)                                                                     \
-  hipLaunchKernelGGL((mlstm_post_kernel<U, F>), dim3(n_rows), dim3(64 * heads), 0, s, num, \
-                     n_parts, part_stride, den, den_ld, gn_w, gn_b, skip_w, x_conv, x_gate,  \
-                     ld_gate, inner, hs, out, out_lp, lp_fmt)
+  hipLaunchKernelGGL((mlstm_post_kernel<U, F>), dim3(rows_and_commit(n_rows, lc, 64 * heads)), \
+                     dim3(64 * heads), 0, s, num, n_parts, part_stride, den, den_ld, gn_w, gn_b, \
+                     skip_w, x_conv, x_gate, ld_gate, inner, hs, out, out_lp, lp_fmt, n_rows, lc)
   if (hs == 512) {
     HK_POST(8, true);
   } else if (hs == 256) {

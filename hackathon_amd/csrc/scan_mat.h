@@ -15,6 +15,9 @@
 
 namespace hk {
 
+constexpr int kLogHdr = 16;  // floats per (slot, head) log header
+constexpr int kLogCapMax = 8;
+
 struct Operand {
   const float* ptr = nullptr;  // nullptr => the value 1.0 (scale only)
   int64_t row_stride = 0;      // elements between request rows
@@ -62,11 +65,53 @@ struct MatScanDesc {
   int log_cap = 0;
 };
 
-constexpr int kLogHdr = 16;  // floats per (slot, head) log header
-constexpr int kLogCapMax = 8;
+// The log-header update of one scan launch (deferred write-back), as a job
+// that runs after the scan: job i advances the header of (run i / heads,
+// head i % heads). A run that fit the log appends its steps (entry n + t
+// gets the product of the run's alphas after step t; F and the older
+// coefficients are scaled by the product of all of them); any other run's
+// tile was written back, so its log is emptied. The scan kernel reads the
+// header only, so the update waits for the whole launch; the tower's post
+// kernel (which also follows the scan and does not read the header) runs
+// it in extra work-groups, which saves a launch per layer.
+struct LogCommit {
+  const int* slot_ids = nullptr;
+  const int* run_off = nullptr;
+  int n_runs = 0, heads = 0;
+  Operand alpha;
+  float* log_hdr = nullptr;
+  int log_cap = 0;  // 0: no log, no jobs
+  __host__ __device__ int jobs() const { return log_cap > 0 ? n_runs * heads : 0; }
+};
+
+__device__ __forceinline__ void log_commit_one(const LogCommit& c, int i) {
+  const int run = i / c.heads;
+  const int head = i - run * c.heads;
+  const int slot = c.slot_ids[run];
+  const int r0 = c.run_off[run];
+  const int len = c.run_off[run + 1] - r0;
+  float* h = c.log_hdr + ((int64_t)slot * c.heads + head) * kLogHdr;
+  const int n = (int)h[0];
+  if (n + len <= c.log_cap) {
+    float p = 1.0f;  // product of the alphas after step t
+    for (int t = len - 1; t >= 0; --t) {
+      h[2 + n + t] = p;
+      p *= c.alpha.ptr[(int64_t)(r0 + t) * c.alpha.row_stride + (int64_t)head * c.alpha.head_stride];
+    }
+    for (int j = 0; j < n; ++j) h[2 + j] *= p;
+    h[1] *= p;
+    h[0] = (float)(n + len);
+  } else {
+    h[0] = 0.0f;
+    h[1] = 1.0f;
+  }
+}
+
+// The job of a scan described by d (no jobs without a log or runs).
+LogCommit log_commit_of(const MatScanDesc& d);
 
 int launch_mat_scan(const MatScanDesc& d, hipStream_t stream);
-// The log header update of a scan launch (deferred write-back); run after it.
+// The LogCommit job of a scan launch as a launch of its own; run after it.
 int launch_mat_log_commit(const MatScanDesc& d, hipStream_t stream);
 // Materialises slots [slot0, slot0 + n) into B and empties their logs.
 int mat_log_flush(const MatScanDesc& d, int slot0, int n, hipStream_t stream);

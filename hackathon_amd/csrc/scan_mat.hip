@@ -350,29 +350,9 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
 // by the product of the run's later alphas, and scales the older entries
 // and F by the product of all of them; any other run left B materialised,
 // so its log empties (n = 0, F = 1).
-__global__ void mat_log_commit_kernel(MatScanDesc d) {
+__global__ void mat_log_commit_kernel(LogCommit c) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= d.n_runs * d.heads) return;
-  const int run = i / d.heads;
-  const int head = i - run * d.heads;
-  const int slot = d.slot_ids[run];
-  const int r0 = d.run_off[run];
-  const int len = d.run_off[run + 1] - r0;
-  float* h = d.log_hdr + ((int64_t)slot * d.heads + head) * kLogHdr;
-  const int n = (int)h[0];
-  if (n + len <= d.log_cap) {
-    float p = 1.0f;  // product of the alphas after step t
-    for (int t = len - 1; t >= 0; --t) {
-      h[2 + n + t] = p;
-      p *= d.alpha.ptr[(int64_t)(r0 + t) * d.alpha.row_stride + (int64_t)head * d.alpha.head_stride];
-    }
-    for (int j = 0; j < n; ++j) h[2 + j] *= p;
-    h[1] *= p;
-    h[0] = (float)(n + len);
-  } else {
-    h[0] = 0.0f;
-    h[1] = 1.0f;
-  }
+  if (i < c.jobs()) log_commit_one(c, i);
 }
 
 // B <- F B + sum_j b_j (a_j g_j) for slots slot0 + blockIdx.z, one row per
@@ -411,11 +391,24 @@ __global__ void mat_log_clear_kernel(float* hdr, int heads, const int* slots, in
 
 }  // namespace
 
+LogCommit log_commit_of(const MatScanDesc& d) {
+  LogCommit c;
+  if (d.log_cap == 0 || d.n_runs == 0 || d.per_row) return c;
+  c.slot_ids = d.slot_ids;
+  c.run_off = d.run_off;
+  c.n_runs = d.n_runs;
+  c.heads = d.heads;
+  c.alpha = d.alpha;
+  c.log_hdr = d.log_hdr;
+  c.log_cap = d.log_cap;
+  return c;
+}
+
 int launch_mat_log_commit(const MatScanDesc& d, hipStream_t stream) {
   if (d.log_cap == 0 || d.n_runs == 0) return HK_OK;
   HK_REQUIRE(!d.per_row && d.slot_ids && d.run_off && d.log_hdr, "mat_log_commit: need runs");
-  const int total = d.n_runs * d.heads;
-  hipLaunchKernelGGL(mat_log_commit_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, d);
+  const LogCommit c = log_commit_of(d);
+  hipLaunchKernelGGL(mat_log_commit_kernel, dim3((c.jobs() + 255) / 256), dim3(256), 0, stream, c);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
