@@ -511,6 +511,7 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
           v[u] = reinterpret_cast<const float4*>(a.h_state + (int64_t)l_slot[c0 + j] * H +
                                                  head * hs)[i - j * vph];
         }
+        if (tr && c0 == 0) ltr[t * 8 + 1] = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
         for (int u = 0; u < kV; ++u) {
           const int i = u * NT + tid;
