@@ -90,16 +90,32 @@ __device__ __forceinline__ void log_commit_one(const LogCommit& c, int i) {
   const int slot = c.slot_ids[run];
   const int r0 = c.run_off[run];
   const int len = c.run_off[run + 1] - r0;
+  // The header and the run's first kLogCapMax alphas are loaded together,
+  // before any store (a store ahead of a load of another array would keep
+  // the loads in order, one memory round trip per step).
   float* h = c.log_hdr + ((int64_t)slot * c.heads + head) * kLogHdr;
-  const int n = (int)h[0];
+  float hv[2 + kLogCapMax];
+#pragma unroll
+  for (int j = 0; j < 2 + kLogCapMax; ++j) hv[j] = h[j];
+  const float* ap =
+      c.alpha.ptr + (int64_t)r0 * c.alpha.row_stride + (int64_t)head * c.alpha.head_stride;
+  float a[kLogCapMax];
+#pragma unroll
+  for (int t = 0; t < kLogCapMax; ++t) a[t] = t < len ? ap[(int64_t)t * c.alpha.row_stride] : 1.0f;
+  const int n = (int)hv[0];
   if (n + len <= c.log_cap) {
     float p = 1.0f;  // product of the alphas after step t
-    for (int t = len - 1; t >= 0; --t) {
-      h[2 + n + t] = p;
-      p *= c.alpha.ptr[(int64_t)(r0 + t) * c.alpha.row_stride + (int64_t)head * c.alpha.head_stride];
+#pragma unroll
+    for (int t = kLogCapMax - 1; t >= 0; --t) {
+      if (t < len) {
+        h[2 + n + t] = p;
+        p *= a[t];
+      }
     }
-    for (int j = 0; j < n; ++j) h[2 + j] *= p;
-    h[1] *= p;
+#pragma unroll
+    for (int j = 0; j < kLogCapMax; ++j)
+      if (j < n) h[2 + j] = hv[2 + j] * p;
+    h[1] = hv[1] * p;
     h[0] = (float)(n + len);
   } else {
     h[0] = 0.0f;
