@@ -276,7 +276,8 @@ struct Engine {
   Act FE;
   // Tick descriptors, one device block (layout of stage_ints()): slot ids,
   // run offsets and active-run counts of the whole tick, run offsets of the
-  // second xLSTM group (relative to its first row) and per-group counts.
+  // second xLSTM group (relative to its first row), per-group counts, and
+  // each row's position in its run and slot.
   int* d_desc = nullptr;
   int* d_slots = nullptr;
   int* d_off = nullptr;
@@ -284,6 +285,8 @@ struct Engine {
   int* d_off2 = nullptr;     // [max_runs + 1]
   int* d_act1 = nullptr;     // [max_rows]
   int* d_act2 = nullptr;     // [max_rows]
+  int* d_pos = nullptr;      // [max_rows]: position of each row in its run
+  int* d_rslot = nullptr;    // [max_rows]: slot of each row's run
   unsigned long long* d_xch = nullptr;   // [max_rows][H]: sLSTM h exchange words
   unsigned long long* d_xch2 = nullptr;  // the same for the second xLSTM group
   // Exchange tags: eager launches count up from 1 per buffer below
@@ -296,7 +299,7 @@ struct Engine {
   uint64_t* d_trace = nullptr;  // HK_TRACE_SLSTM: per-step stamps of layer 0's sLSTM
   int* h_stage = nullptr;    // pinned [2][stage_ints()]
   int* h_err = nullptr;      // pinned [1]: d_err read back by hk_engine_check
-  int stage_ints() const { return 3 * max_runs + 2 + 3 * max_rows; }
+  int stage_ints() const { return 3 * max_runs + 2 + 5 * max_rows; }
   hipEvent_t stage_done[2] = {nullptr, nullptr};
   int stage_idx = 0;
   // The towers are independent and run concurrently, forked from and joined
@@ -488,6 +491,8 @@ int build_workspace(Engine& e) {
   e.d_off2 = e.d_act + e.max_rows;
   e.d_act1 = e.d_off2 + e.max_runs + 1;
   e.d_act2 = e.d_act1 + e.max_rows;
+  e.d_pos = e.d_act2 + e.max_rows;
+  e.d_rslot = e.d_pos + e.max_rows;
   HK_CHECK_HIP(hipMemset(e.d_err, 0, 4));
   if (std::getenv("HK_TRACE_SLSTM")) {
     e.d_trace = static_cast<uint64_t*>(e.alloc_bytes((size_t)e.max_rows * 8 * 8));
@@ -747,20 +752,25 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   // mLSTM block (model/xlstm.py:298-325).
   HK_TRY(linear(e, w, w.XN2, H, {S(e, kXLSTM, l, X_L_XG_W), nullptr}, n, 2 * I, H, 0, nullptr, 0,
                 w.XMG, 2 * I, nullptr, 0, s));
-  HK_TRY(conv_scan(r, w.XMG, 2 * I, I, st[XS_L_CONV], le[XS_L_CONV], F32(e, kXLSTM, l, X_L_CONV_W),
-                   F32(e, kXLSTM, l, X_L_CONV_B), 1, w.XMC, I, s));
   const float* wqkv = F32(e, kXLSTM, l, X_L_QKV_W);
   const float k_div = (float)std::sqrt((double)d.hs_m);
   const int n_if = 2 * d.nh;
   const int segs = if_segments(I);
+  ConvCommit conv_commit;
   if (mlstm_qkv_if_supported(I, n_if, segs)) {
-    // q, k, v and the gate pre-activations in one launch (segment partials)
-    HK_TRY(mlstm_qkv_if(w.XMC, w.XMG, 2 * I, wqkv, wqkv + (int64_t)I * 4, wqkv + (int64_t)2 * I * 4,
+    // the conv, q, k, v and the gate pre-activations in one launch (segment
+    // partials); mlstm_post writes the conv state the runs leave
+    const ConvIn conv{st[XS_L_CONV], le[XS_L_CONV], F32(e, kXLSTM, l, X_L_CONV_W),
+                      F32(e, kXLSTM, l, X_L_CONV_B), r.row_pos, r.row_slot, w.XMC};
+    HK_TRY(mlstm_qkv_if(conv, w.XMG, 2 * I, wqkv, wqkv + (int64_t)I * 4, wqkv + (int64_t)2 * I * 4,
                         n, I, k_div, F32(e, kXLSTM, l, X_L_IF_W), F32(e, kXLSTM, l, X_L_IF_B), n_if,
                         w.QKV, w.KS, w.IF, segs, s));
+    conv_commit = ConvCommit{st[XS_L_CONV], le[XS_L_CONV], r.row_pos, r.row_slot, w.XMG, 2 * I};
     HK_TRY(mlstm_gates(r, w.IF, segs, (int64_t)n * n_if, d.nh, w.QKV, I, w.KS, st[XS_L_N],
                        st[XS_L_M], w.IG, w.FG, w.DEN, s));
   } else {
+    HK_TRY(conv_scan(r, w.XMG, 2 * I, I, st[XS_L_CONV], le[XS_L_CONV],
+                     F32(e, kXLSTM, l, X_L_CONV_W), F32(e, kXLSTM, l, X_L_CONV_B), 1, w.XMC, I, s));
     HK_TRY(mlstm_qkv(w.XMC, w.XMG, 2 * I, wqkv, wqkv + (int64_t)I * 4, wqkv + (int64_t)2 * I * 4,
                      n, I, 4, k_div, w.QKV, w.KS, s));
     HK_TRY(linear(e, w, Act{w.QKV, nullptr}, 3 * I,
@@ -786,7 +796,7 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   HK_TRY(timed_mat_scan(e, 0, m, s));
   HK_TRY(mlstm_post(w.NUM, m.row_parts, m.out_part_stride, w.DEN, d.nh, F32(e, kXLSTM, l, X_L_GN_W), F32(e, kXLSTM, l, X_L_GN_B),
                     F32(e, kXLSTM, l, X_L_SKIP), w.XMC, w.XMG + I, 2 * I, n, I, d.nh, w.HS.f,
-                    w.HS.l, e.lp_fmt, log_commit_of(m), s));
+                    w.HS.l, e.lp_fmt, log_commit_of(m), conv_commit, s));
   HK_TRY(linear(e, w, w.HS, I, {S(e, kXLSTM, l, X_L_DOWN_W), nullptr}, n, H, I, 0, w.X1, H, w.X2,
                 H, nullptr, 0, s));
   // final_norm and the Block's residual (x = final_norm(x2) + x) are applied
@@ -1025,7 +1035,7 @@ struct TickShape {
 int enqueue_tick(Engine& e, const TickShape& sh, const float* features_dev, float* preds_dev,
                  hipStream_t s) {
   Group all;
-  all.r = Runs{e.d_slots, e.d_off, sh.n_runs, sh.n_rows, sh.steps};
+  all.r = Runs{e.d_slots, e.d_off, sh.n_runs, sh.n_rows, sh.steps, e.d_pos, e.d_rslot};
   all.act_dev = e.d_act;
   all.act = sh.act;
   HK_TRY(stage_features(features_dev, sh.n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, e.lp_fmt, s));
@@ -1033,11 +1043,11 @@ int enqueue_tick(Engine& e, const TickShape& sh, const float* features_dev, floa
   for (int i = 0; i < Engine::kSide; ++i) HK_CHECK_HIP(hipStreamWaitEvent(e.side[i], e.fork_ev, 0));
   if (sh.split < sh.n_runs) {
     Group g1, g2;
-    g1.r = Runs{e.d_slots, e.d_off, sh.split, sh.row_split, sh.steps};
+    g1.r = Runs{e.d_slots, e.d_off, sh.split, sh.row_split, sh.steps, e.d_pos, e.d_rslot};
     g1.act_dev = e.d_act1;
     g1.act = sh.act1;
     g2.r = Runs{e.d_slots + sh.split, e.d_off2, sh.n_runs - sh.split, sh.n_rows - sh.row_split,
-                sh.steps2};
+                sh.steps2, e.d_pos + sh.row_split, e.d_rslot + sh.row_split};
     g2.act_dev = e.d_act2;
     g2.act = sh.act2;
     g2.row0 = sh.row_split;
@@ -1589,7 +1599,14 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   int* h_off2 = h_act + e.max_rows;
   int* h_act1 = h_off2 + e.max_runs + 1;
   int* h_act2 = h_act1 + e.max_rows;
+  int* h_pos = h_act2 + e.max_rows;
+  int* h_rslot = h_pos + e.max_rows;
   std::memcpy(h_slots, slot_ids_host, (size_t)n_runs * 4);
+  for (int i = 0; i < n_runs; ++i)
+    for (int r = run_off_host[i]; r < run_off_host[i + 1]; ++r) {
+      h_pos[r] = r - run_off_host[i];
+      h_rslot[r] = slot_ids_host[i];
+    }
   std::memcpy(h_off, run_off_host, (size_t)(n_runs + 1) * 4);
   {
     int c = n_runs;

@@ -16,6 +16,34 @@ struct Runs {
   int n_runs = 0;
   int n_rows = 0;
   int max_len = 0;                // steps of the longest run (host)
+  const int* row_pos = nullptr;   // device [n_rows]: position of each row in its run
+  const int* row_slot = nullptr;  // device [n_rows]: slot of each row's run
+};
+
+// A width-4 causal conv (model/modules.py:23-49) computed by the kernel
+// that consumes it: row r at position p of its run reads the inputs of
+// positions p-3 .. p, those before the run from the slot's conv state
+// (3 rows of `channels`, oldest first); out = silu(conv).
+struct ConvIn {
+  const float* state = nullptr;  // [slot][3][channels]
+  int64_t slot_stride = 0;
+  const float* w = nullptr;       // [4][channels] (tap 0 multiplies the oldest input)
+  const float* b = nullptr;       // [channels]
+  const int* row_pos = nullptr;
+  const int* row_slot = nullptr;
+  float* out = nullptr;           // [n_rows][channels], for later readers
+};
+
+// The conv state a run leaves (its last 3 inputs, behind the old state's
+// newest ones when the run is shorter than 3), written by a kernel that runs
+// after every reader of the old state: the last row of each run writes it.
+struct ConvCommit {
+  float* state = nullptr;  // null: nothing to write
+  int64_t slot_stride = 0;
+  const int* row_pos = nullptr;
+  const int* row_slot = nullptr;
+  const float* x = nullptr;  // the conv's inputs [n_rows][ldx]
+  int64_t ldx = 0;
 };
 
 // ---- row kernels (rowops.hip) ---------------------------------------------
@@ -68,10 +96,13 @@ int layernorm_rows(const float* x, const float* w, const float* residual, int n_
 // mLSTM cell/block tail (model/xlstm.py:236-241, :321-322):
 // out = GroupNorm(num / den) ; h = (out + skip * x_conv) * silu(x_gate).
 // num is the sum of n_parts planes part_stride floats apart.
+// Extra work: the scan's log-header update (lc) and the conv state of the
+// block's conv (cc, over `inner` channels).
 int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* den, int den_ld,
                const float* gn_w, const float* gn_b, const float* skip_w, const float* x_conv,
                const float* x_gate, int64_t ld_gate, int n_rows, int inner, int heads,
-               float* out, uint16_t* out_lp, int lp_fmt, const LogCommit& lc, hipStream_t s);
+               float* out, uint16_t* out_lp, int lp_fmt, const LogCommit& lc,
+               const ConvCommit& cc, hipStream_t s);
 
 // preds[r, col] = x[r] . w + b (shared output_proj, model/inference_model.py:142).
 int output_proj(const float* x, const float* w, const float* b, int n_rows, int hidden,
@@ -83,13 +114,14 @@ int mlstm_qkv(const float* x_conv, const float* x_m, int64_t ld_xm, const float*
               const float* wk, const float* wv, int n_rows, int inner, int blk, float k_div,
               float* qkv, float* ks, hipStream_t s);
 
-// mlstm_qkv with blk 4 fused with the cell's input / forget gate projections
-// (model/xlstm.py:29-30, :52-54): w_if [n_out][3*inner] (igate rows, then
-// fgate rows), b_if [n_out]. The pre-activations land as `segs` partial
-// planes if_part [segs][n_rows][n_out], to be added in plane order (plane 0
-// holds the bias).
+// mlstm_qkv with blk 4 fused with the block's conv (x_conv = conv over the
+// first `inner` columns of x_m, written to conv.out) and the cell's input /
+// forget gate projections (model/xlstm.py:29-30, :52-54): w_if
+// [n_out][3*inner] (igate rows, then fgate rows), b_if [n_out]. The
+// pre-activations land as `segs` partial planes if_part [segs][n_rows][n_out],
+// to be added in plane order (plane 0 holds the bias).
 bool mlstm_qkv_if_supported(int inner, int n_out, int segs);
-int mlstm_qkv_if(const float* x_conv, const float* x_m, int64_t ld_xm, const float* wq,
+int mlstm_qkv_if(const ConvIn& conv, const float* x_m, int64_t ld_xm, const float* wq,
                  const float* wk, const float* wv, int n_rows, int inner, float k_div,
                  const float* w_if, const float* b_if, int n_out, float* qkv, float* ks,
                  float* if_part, int segs, hipStream_t s);

@@ -324,7 +324,8 @@ __global__ void mlstm_post_kernel(const float* __restrict__ num, int n_parts, in
                                   const float* __restrict__ skip_w,
                                   const float* __restrict__ x_conv,
                                   const float* __restrict__ x_gate, int64_t ld_gate, int inner,
-                                  int hs, float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt, int n_rows, LogCommit lc) {
+                                  int hs, float* __restrict__ out, uint16_t* __restrict__ out_lp, int lp_fmt, int n_rows, LogCommit lc,
+                                  ConvCommit cc) {
   if ((int)blockIdx.x >= n_rows) {  // the scan's log-header update (LogCommit)
     const int i = ((int)blockIdx.x - n_rows) * (int)blockDim.x + (int)threadIdx.x;
     if (i < lc.jobs()) log_commit_one(lc, i);
@@ -333,6 +334,29 @@ __global__ void mlstm_post_kernel(const float* __restrict__ num, int n_parts, in
   const int64_t row = blockIdx.x;
   const int head = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  // The last row of each run leaves the conv state: the inputs of positions
+  // p-2 .. p (p its position), those before the run from the old state
+  // (read here, before any write; every reader of it ran before this kernel).
+  if (cc.state != nullptr && (row + 1 == n_rows || cc.row_pos[row + 1] == 0)) {
+    const int p = cc.row_pos[row];
+    float* st = cc.state + (int64_t)cc.row_slot[row] * cc.slot_stride;
+    float nv[3][U];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = head * hs + lane + 64 * u;
+        nv[k][u] = 0.0f;
+        if (FULL || lane + 64 * u < hs)
+          nv[k][u] = p - 2 + k >= 0 ? cc.x[(row - (2 - k)) * cc.ldx + c]
+                                    : st[(int64_t)(1 + p + k) * inner + c];
+      }
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (FULL || lane + 64 * u < hs) st[(int64_t)k * inner + head * hs + lane + 64 * u] = nv[k][u];
+  }
   const int64_t base = row * inner + (int64_t)head * hs;
   const float* gate = x_gate + row * ld_gate + (int64_t)head * hs;
   float hv[U], gw[U], gb[U], sk[U], xc[U], xg[U];
@@ -421,16 +445,18 @@ __global__ void mlstm_qkv_kernel(const float* __restrict__ x_conv, const float* 
 }
 
 // mLSTM q/k/v BlockLinear with 4x4 blocks (model/xlstm.py:191-193,
-// :220-222) fused with the input / forget gate projections of the cell,
-// [igate; fgate](cat(q, k, v)) (model/xlstm.py:29-30, :52-54), for one
-// (row, column segment) per work-group: each thread computes whole 4-column
-// blocks of q, k and v with 16-byte loads, stores them, and accumulates
-// their NOUT gate-row products; the work-group's NOUT sums (in a fixed
-// order) are segment seg's partial pre-activations, plane seg of if_part
-// [segs][n_rows][NOUT]; plane 0 also carries the bias.
+// :220-222) fused with the block's causal conv (model/xlstm.py:217-218) and
+// the input / forget gate projections of the cell, [igate; fgate](cat(q, k,
+// v)) (model/xlstm.py:29-30, :52-54), for R rows x one column segment per
+// work-group: each thread computes whole 4-column blocks of the conv output
+// (from x_m's rows and, before a run, the slot's conv state; stored for the
+// block's tail), of q, k and v with 16-byte loads, stores them, and
+// accumulates their NOUT gate-row products; the work-group's NOUT sums (in
+// a fixed order) are segment seg's partial pre-activations, plane seg of
+// if_part [segs][n_rows][NOUT]; plane 0 also carries the bias.
 template <int NOUT, int R>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void mlstm_qkv_if_kernel(
-    const float* __restrict__ x_conv, const float* __restrict__ x_m, int64_t ld_xm,
+    ConvIn conv, const float* __restrict__ x_m, int64_t ld_xm,
     const float* __restrict__ wq, const float* __restrict__ wk, const float* __restrict__ wv,
     int n_rows, int inner, float k_div, const float* __restrict__ w_if,
     const float* __restrict__ b_if, float* __restrict__ qkv, float* __restrict__ ks,
@@ -442,21 +468,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   const int tid = threadIdx.x;
   const int per = (inner >> 2) / gridDim.x;  // 4-column blocks per segment
   const int64_t wl = (int64_t)3 * inner;
-  int rows[R];
+  int rows[R], pos[R];
+  const float* cst[R];  // the conv state of the row's slot
 #pragma unroll
-  for (int r = 0; r < R; ++r) rows[r] = min(rbase + r, n_rows - 1);
+  for (int r = 0; r < R; ++r) {
+    rows[r] = min(rbase + r, n_rows - 1);
+    pos[r] = conv.row_pos[rows[r]];
+    cst[r] = conv.state + (int64_t)conv.row_slot[rows[r]] * conv.slot_stride;
+  }
   auto dot4 = [](float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; };
+  // One channel of the conv, in conv_scan's order of operations.
+  auto conv1 = [](float b, float w0, float w1, float w2, float w3, float s0, float s1, float s2,
+                  float x) {
+    float v = b + w0 * s0;
+    v += w1 * s1;
+    v += w2 * s2;
+    v += w3 * x;
+    return silu(v);
+  };
   float acc[R * NOUT];
 #pragma unroll
   for (int i = 0; i < R * NOUT; ++i) acc[i] = 0.0f;
   for (int nb = seg * per + tid; nb < (seg + 1) * per; nb += 256) {
     // The block's weights are loaded once for all R rows; every operand is
     // loaded before any is used (one L2 round trip per block).
-    float4 xc[R], xm[R];
+    // xs[r][k]: the input k positions before row r's (k = 1..3; index
+    // k - 1), from x_m inside the run, else from the conv state.
+    float4 xc[R], xm[R], xs[R][3];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      xc[r] = reinterpret_cast<const float4*>(x_conv + (int64_t)rows[r] * inner)[nb];
       xm[r] = reinterpret_cast<const float4*>(x_m + (int64_t)rows[r] * ld_xm)[nb];
+#pragma unroll
+      for (int k = 1; k <= 3; ++k) {
+        const float* src = pos[r] >= k ? x_m + (int64_t)(rows[r] - k) * ld_xm
+                                       : cst[r] + (int64_t)(3 + pos[r] - k) * inner;
+        xs[r][k - 1] = reinterpret_cast<const float4*>(src)[nb];
+      }
+    }
+    const float4 cw0 = reinterpret_cast<const float4*>(conv.w)[nb];
+    const float4 cw1 = reinterpret_cast<const float4*>(conv.w + inner)[nb];
+    const float4 cw2 = reinterpret_cast<const float4*>(conv.w + 2 * (int64_t)inner)[nb];
+    const float4 cw3 = reinterpret_cast<const float4*>(conv.w + 3 * (int64_t)inner)[nb];
+    const float4 cb = reinterpret_cast<const float4*>(conv.b)[nb];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float4 s0 = xs[r][2], s1 = xs[r][1], s2 = xs[r][0], x0 = xm[r];
+      xc[r] = make_float4(conv1(cb.x, cw0.x, cw1.x, cw2.x, cw3.x, s0.x, s1.x, s2.x, x0.x),
+                          conv1(cb.y, cw0.y, cw1.y, cw2.y, cw3.y, s0.y, s1.y, s2.y, x0.y),
+                          conv1(cb.z, cw0.z, cw1.z, cw2.z, cw3.z, s0.z, s1.z, s2.z, x0.z),
+                          conv1(cb.w, cw0.w, cw1.w, cw2.w, cw3.w, s0.w, s1.w, s2.w, x0.w));
+      if (rbase + r < n_rows)
+        reinterpret_cast<float4*>(conv.out + (int64_t)rows[r] * inner)[nb] = xc[r];
     }
     // W[nb][o][h]: block nb's 4x4 weights, row o = output column 4nb + o
     float4 bq[4], bk[4], bv[4];
@@ -663,16 +725,20 @@ int layernorm_rows(const float* x, const float* w, const float* residual, int n_
 int mlstm_post(const float* num, int n_parts, int64_t part_stride, const float* den, int den_ld,
                const float* gn_w, const float* gn_b, const float* skip_w, const float* x_conv,
                const float* x_gate, int64_t ld_gate, int n_rows, int inner, int heads,
-               float* out, uint16_t* out_lp, int lp_fmt, const LogCommit& lc, hipStream_t s) {
+               float* out, uint16_t* out_lp, int lp_fmt, const LogCommit& lc,
+               const ConvCommit& cc, hipStream_t s) {
   if (n_rows == 0 && lc.jobs() == 0) return HK_OK;
   HK_REQUIRE(heads >= 1 && heads <= 16 && inner % heads == 0 &&
                  inner / heads <= 64 * kHeadPostMax && n_parts >= 1,
              "mlstm_post: %d heads of %d unsupported", heads, inner / std::max(heads, 1));
+  HK_REQUIRE(!cc.state || (cc.row_pos && cc.row_slot && cc.x),
+             "mlstm_post: conv state update without row descriptors or inputs");
   const int hs = inner / heads;
 #define HK_POST(U, F)                                                                     \
   hipLaunchKernelGGL((mlstm_post_kernel<U, F>), dim3(rows_and_commit(n_rows, lc, 64 * heads)), \
                      dim3(64 * heads), 0, s, num, n_parts, part_stride, den, den_ld, gn_w, gn_b, \
-                     skip_w, x_conv, x_gate, ld_gate, inner, hs, out, out_lp, lp_fmt, n_rows, lc)
+                     skip_w, x_conv, x_gate, ld_gate, inner, hs, out, out_lp, lp_fmt, n_rows, lc, \
+                     cc)
   if (hs == 512) {
     HK_POST(8, true);
   } else if (hs == 256) {
@@ -708,22 +774,25 @@ int mlstm_qkv(const float* x_conv, const float* x_m, int64_t ld_xm, const float*
   return HK_OK;
 }
 
-int mlstm_qkv_if(const float* x_conv, const float* x_m, int64_t ld_xm, const float* wq,
+int mlstm_qkv_if(const ConvIn& conv, const float* x_m, int64_t ld_xm, const float* wq,
                  const float* wk, const float* wv, int n_rows, int inner, float k_div,
                  const float* w_if, const float* b_if, int n_out, float* qkv, float* ks,
                  float* if_part, int segs, hipStream_t s) {
   if (n_rows == 0) return HK_OK;
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  HK_REQUIRE(mlstm_qkv_if_supported(inner, n_out, segs) && ld_xm % 4 == 0 && al16(x_conv) &&
-                 al16(x_m) && al16(wq) && al16(wk) && al16(wv) && al16(w_if) && al16(qkv) &&
-                 al16(ks),
+  HK_REQUIRE(conv.state && conv.w && conv.b && conv.row_pos && conv.row_slot && conv.out,
+             "mlstm_qkv_if: null conv operand");
+  HK_REQUIRE(mlstm_qkv_if_supported(inner, n_out, segs) && ld_xm % 4 == 0 &&
+                 conv.slot_stride % 4 == 0 && al16(conv.state) && al16(conv.w) && al16(conv.b) &&
+                 al16(conv.out) && al16(x_m) && al16(wq) && al16(wk) && al16(wv) && al16(w_if) &&
+                 al16(qkv) && al16(ks),
              "mlstm_qkv_if: inner %d, %d gate rows, %d segments or alignment unsupported", inner,
              n_out, segs);
   // R rows per work-group share each block's weight loads (R * n_out <= 64).
   const dim3 block(256);
 #define HK_QKV_IF(NOUT, R)                                                                      \
   hipLaunchKernelGGL((mlstm_qkv_if_kernel<NOUT, R>), dim3(segs, (n_rows + (R)-1) / (R)), block, \
-                     0, s, x_conv, x_m, ld_xm, wq, wk, wv, n_rows, inner, k_div, w_if, b_if, qkv, \
+                     0, s, conv, x_m, ld_xm, wq, wk, wv, n_rows, inner, k_div, w_if, b_if, qkv, \
                      ks, if_part)
   switch (n_out) {
     case 4: HK_QKV_IF(4, 4); break;
