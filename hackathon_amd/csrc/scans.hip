@@ -165,15 +165,24 @@ __global__ __launch_bounds__(256) void rglru_scan_kernel(
     }
   };
   auto step = [&](const Rows& v, int rb) {
+    // Each product and sum rounded on its own, as the reference's tensor
+    // ops do (model/hawk.py:35-37): no multiply-add is fused here, so the
+    // result does not depend on how the compiler lays out the chunk.
+#pragma clang fp contract(off)
+    // The gates of the chunk's rows in the run only (the bound is uniform
+    // over the work-group, so rows past the run cost a branch, not the math).
     float at[kRgChunk], ut[kRgChunk], og[kRgChunk];
 #pragma unroll
     for (int k = 0; k < kRgChunk; ++k) {
-      const float it = sigmoid(v.i[k]);
-      const float rt = sigmoid(v.r[k]);
-      at[k] = powf(base, c_exp * rt);
-      const float mult = sqrtf(1.0f - at[k] * at[k]);
-      ut[k] = mult * (it * v.x[k]);
-      og[k] = gelu_erf(v.g[k]);
+      at[k] = ut[k] = og[k] = 0.0f;
+      if (rb + k < r1) {
+        const float it = sigmoid(v.i[k]);
+        const float rt = sigmoid(v.r[k]);
+        at[k] = powf(base, c_exp * rt);
+        const float mult = sqrtf(1.0f - at[k] * at[k]);
+        ut[k] = mult * (it * v.x[k]);
+        og[k] = gelu_erf(v.g[k]);
+      }
     }
 #pragma unroll
     for (int k = 0; k < kRgChunk; ++k) {
