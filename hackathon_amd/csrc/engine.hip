@@ -873,8 +873,11 @@ int run_retnet(Engine& e, int l, const Runs& r, hipStream_t s) {
   m.row_parts = row_parts(r, d.hs_r);
   m.out_part_stride = (int64_t)n * H;
   HK_TRY(timed_mat_scan(e, 2, m, s));
+  // the slots' offsets and scales advance after every reader (retnet_prep)
+  const RetnetAdvance adv{r.slot_ids, r.run_off, r.n_runs, d.nh, F32(e, kRetNet, l, R_DECAY),
+                          reinterpret_cast<int*>(st[RS_OFF]), st[RS_SCALE]};
   HK_TRY(retnet_post(w.O, m.row_parts, m.out_part_stride, w.QKVG + 3 * H, 4 * H, n, H, d.hs_r,
-                     w.YO.f, w.YO.l, e.lp_fmt, log_commit_of(m), s));
+                     w.YO.f, w.YO.l, e.lp_fmt, log_commit_of(m), adv, s));
   HK_TRY(linear(e, w, w.YO, H, {S(e, kRetNet, l, R_OUT_W), nullptr}, n, H, H, 0, w.X.f, H, w.X.f,
                 H, nullptr, 0, s));
   return HK_OK;

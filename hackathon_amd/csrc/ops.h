@@ -69,11 +69,41 @@ int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const fl
 int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float* dt,
               float* decay, hipStream_t s);
 
+// The RetNet position bookkeeping a tick leaves per (slot, head)
+// (model/retnet.py:264-269): offsets += run length, and the scale advanced
+// s' = s*gamma + 1 once per step; one job per (run, head), run after every
+// reader of the old values.
+struct RetnetAdvance {
+  const int* slot_ids = nullptr;
+  const int* run_off = nullptr;
+  int n_runs = 0, heads = 0;
+  const float* decay = nullptr;  // [heads]
+  int* offsets = nullptr;        // [slot]; null: no jobs
+  float* scales = nullptr;       // [slot][heads]
+  __host__ __device__ int jobs() const { return offsets ? n_runs * heads : 0; }
+};
+
+// Job i of a RetnetAdvance: (run i / heads, head i % heads). The scale steps
+// through the run with the expression retnet_prep steps it with per row.
+__device__ __forceinline__ void retnet_advance_one(const RetnetAdvance& a, int i) {
+  const int run = i / a.heads;
+  const int head = i - run * a.heads;
+  const int slot = a.slot_ids[run];
+  const int len = a.run_off[run + 1] - a.run_off[run];
+  float sc = a.scales[(int64_t)slot * a.heads + head];
+  const float gam = a.decay[head];
+  for (int t = 0; t < len; ++t) sc = sc * gam + 1.0f;
+  a.scales[(int64_t)slot * a.heads + head] = sc;
+  if (head == 0) a.offsets[slot] += len;
+}
+
 // RetNet tail before out_proj (model/retnet.py:168-169): per-head RMSNorm
 // (eps 1e-6, no affine), times silu(g). o is the sum of n_parts planes.
+// Extra work: the scan's log-header update (lc) and the tick's position
+// bookkeeping (adv).
 int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g, int64_t ldg,
                 int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
-                const LogCommit& lc, hipStream_t s);
+                const LogCommit& lc, const RetnetAdvance& adv, hipStream_t s);
 
 // sLSTM block tail + mLSTM block norm (model/xlstm.py:422-424, :308):
 // x1 = GroupNorm(groups)(y) + skip; xn = LayerNorm(x1) * w_ln.
@@ -142,7 +172,10 @@ int conv_scan(const Runs& r, const float* in, int64_t ld_in, int channels, float
               int64_t slot_stride, const float* w, const float* bias, int act_silu, float* out,
               int64_t ldo, hipStream_t s);
 
-// RetNet rotary + scale recurrence (model/retnet.py:239-269, :340).
+// RetNet rotary + scale recurrence (model/retnet.py:239-269, :340) for
+// each row, from the offsets and scales the slot held before the tick (the
+// bookkeeping that advances them is RetnetAdvance). Needs r.row_pos and
+// r.row_slot.
 int retnet_prep(const Runs& r, const float* qkvg, int64_t ld, int hidden, int heads,
                 float k_scaling, const float* angle, const float* decay, int* offsets,
                 float* scales, float* k_rope, float* q_scaled, hipStream_t s);

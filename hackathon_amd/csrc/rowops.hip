@@ -233,10 +233,14 @@ constexpr int kHeadPostMax = 16;
 __global__ void retnet_post_kernel(const float* __restrict__ o, int n_parts, int64_t part_stride,
                                    const float* __restrict__ g, int64_t ldg, int hidden,
                                    int head_size, float* __restrict__ out,
-                                   uint16_t* __restrict__ out_lp, int lp_fmt, int n_rows, LogCommit lc) {
-  if ((int)blockIdx.x >= n_rows) {  // the scan's log-header update (LogCommit)
+                                   uint16_t* __restrict__ out_lp, int lp_fmt, int n_rows, LogCommit lc,
+                                   RetnetAdvance adv) {
+  if ((int)blockIdx.x >= n_rows) {  // the scan's log-header update, then the position bookkeeping
     const int i = ((int)blockIdx.x - n_rows) * (int)blockDim.x + (int)threadIdx.x;
-    if (i < lc.jobs()) log_commit_one(lc, i);
+    if (i < lc.jobs())
+      log_commit_one(lc, i);
+    else if (i - lc.jobs() < adv.jobs())
+      retnet_advance_one(adv, i - lc.jobs());
     return;
   }
   const int64_t row = blockIdx.x;
@@ -685,15 +689,19 @@ int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float*
 
 int retnet_post(const float* o, int n_parts, int64_t part_stride, const float* g, int64_t ldg,
                 int n_rows, int hidden, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
-                const LogCommit& lc, hipStream_t s) {
-  if (n_rows == 0 && lc.jobs() == 0) return HK_OK;
+                const LogCommit& lc, const RetnetAdvance& adv, hipStream_t s) {
+  if (n_rows == 0 && lc.jobs() == 0 && adv.jobs() == 0) return HK_OK;
   const int heads = hidden / head_size;
   HK_REQUIRE(heads * head_size == hidden && heads <= 16 && head_size <= 64 * kHeadPostMax &&
                  n_parts >= 1,
              "retnet_post: %d heads of %d unsupported", heads, head_size);
-  hipLaunchKernelGGL(retnet_post_kernel, dim3(rows_and_commit(n_rows, lc, 64 * heads)),
-                     dim3(64 * heads), 0, s, o, n_parts, part_stride, g, ldg, hidden, head_size,
-                     out, out_lp, lp_fmt, n_rows, lc);
+  HK_REQUIRE(adv.jobs() == 0 || (adv.slot_ids && adv.run_off && adv.decay && adv.scales),
+             "retnet_post: incomplete position bookkeeping");
+  const int threads = 64 * heads;
+  const unsigned grid =
+      (unsigned)(n_rows + (lc.jobs() + adv.jobs() + threads - 1) / threads);
+  hipLaunchKernelGGL(retnet_post_kernel, dim3(grid), dim3(threads), 0, s, o, n_parts, part_stride,
+                     g, ldg, hidden, head_size, out, out_lp, lp_fmt, n_rows, lc, adv);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }

@@ -68,30 +68,21 @@ __global__ __launch_bounds__(256) void conv_scan_kernel(
 // from the slot's stored scale through the row's position in its run, the
 // same operations in the same order as a sequential pass.
 __global__ __launch_bounds__(256) void retnet_prep_kernel(
-    const int* __restrict__ slot_ids, const int* __restrict__ run_off, int n_runs,
+    const int* __restrict__ row_pos, const int* __restrict__ row_slot,
     const float* __restrict__ qkvg, int64_t ld, int hidden, int head_size, float k_scaling,
     const float* __restrict__ angle, const float* __restrict__ decay,
     const int* __restrict__ offsets, const float* __restrict__ scales, float* __restrict__ k_rope,
     float* __restrict__ q_scaled) {
   const int r = blockIdx.x;
   const int c = blockIdx.y * 256 + threadIdx.x;
-  int lo = 0, hi = n_runs - 1;  // the run holding row r: run_off[lo] <= r < run_off[lo + 1]
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (run_off[mid] <= r) {
-      lo = mid;
-    } else {
-      hi = mid - 1;
-    }
-  }
   if (c >= hidden) return;
   const int heads = hidden / head_size;
   const int head = c / head_size;
   const int j = c % head_size;
   const int partner = (j & 1) ? c - 1 : c + 1;
   const float sign = (j & 1) ? 1.0f : -1.0f;  // rotate_every_two: (-x1, x0)
-  const int slot = slot_ids[lo];
-  const int t = r - run_off[lo];
+  const int slot = row_slot[r];
+  const int t = row_pos[r];
   const float gam = decay[head];
   float sc = scales[(int64_t)slot * heads + head];
   for (int i = 0; i <= t; ++i) sc = sc * gam + 1.0f;
@@ -110,24 +101,6 @@ __global__ __launch_bounds__(256) void retnet_prep_kernel(
   q_scaled[(int64_t)r * hidden + c] = qr * sf;
 }
 
-// After retnet_prep: offsets += run length; scales advanced through the run
-// (s' = s*gamma + 1 per step). Thread per (run, head).
-__global__ void retnet_advance_kernel(const int* __restrict__ slot_ids,
-                                      const int* __restrict__ run_off, int n_runs, int heads,
-                                      const float* __restrict__ decay, int* __restrict__ offsets,
-                                      float* __restrict__ scales) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n_runs * heads) return;
-  const int run = i / heads;
-  const int head = i % heads;
-  const int slot = slot_ids[run];
-  const int len = run_off[run + 1] - run_off[run];
-  float sc = scales[(int64_t)slot * heads + head];
-  const float gam = decay[head];
-  for (int t = 0; t < len; ++t) sc = sc * gam + 1.0f;
-  scales[(int64_t)slot * heads + head] = sc;
-  if (head == 0) offsets[slot] += len;
-}
 
 // grid (runs, ceil(hidden/256)); thread per channel. Only h' = h*a_t + u_t
 // is sequential: a run's rows go through in chunks of kRgChunk, the next
@@ -809,6 +782,7 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
 
   for (int tb = 0; tb < len; tb += 2 * B) {
     block(rq[0], rk[0], rg[0], tb, 0);
+    if (tb + B >= len) break;  // the second block would hold no step of the run
     fill(rq[0], rk[0], rg[0], tb + 2 * B);
     block(rq[1], rk[1], rg[1], tb + B, 1);
     fill(rq[1], rk[1], rg[1], tb + 3 * B);
@@ -846,14 +820,11 @@ int retnet_prep(const Runs& r, const float* qkvg, int64_t ld, int hidden, int he
   if (r.n_runs == 0) return HK_OK;
   HK_REQUIRE(hidden % heads == 0 && (hidden / heads) % 2 == 0, "retnet_prep: bad head size");
   HK_REQUIRE(r.n_rows > 0, "retnet_prep: bad row count %d", r.n_rows);
+  HK_REQUIRE(r.row_pos && r.row_slot, "retnet_prep: needs the rows' run positions and slots");
   dim3 grid(r.n_rows, (hidden + 255) / 256);
-  hipLaunchKernelGGL(retnet_prep_kernel, grid, dim3(256), 0, s, r.slot_ids, r.run_off, r.n_runs,
-                     qkvg, ld, hidden, hidden / heads, k_scaling, angle, decay, offsets, scales,
-                     k_rope, q_scaled);
-  HK_LAUNCH_CHECK();
-  const int n = r.n_runs * heads;
-  hipLaunchKernelGGL(retnet_advance_kernel, dim3((n + 255) / 256), dim3(256), 0, s, r.slot_ids,
-                     r.run_off, r.n_runs, heads, decay, offsets, scales);
+  hipLaunchKernelGGL(retnet_prep_kernel, grid, dim3(256), 0, s, r.row_pos, r.row_slot, qkvg, ld,
+                     hidden, hidden / heads, k_scaling, angle, decay, offsets, scales, k_rope,
+                     q_scaled);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
