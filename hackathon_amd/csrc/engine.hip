@@ -233,7 +233,7 @@ struct TowerWS {
         *IG = nullptr, *FG = nullptr, *DEN = nullptr, *NUM = nullptr, *X2 = nullptr;
   Act XN2, HS;
   // Mamba2
-  float *PROJ = nullptr, *DTR = nullptr, *DTS = nullptr, *DEC = nullptr, *MXC = nullptr,
+  float *PROJ = nullptr, *DTS = nullptr, *DEC = nullptr, *MXC = nullptr,
         *YS = nullptr;
   Act YN;
   // RetNet
@@ -435,13 +435,12 @@ int build_workspace(Engine& e) {
       case kMamba2: {
         const int64_t C = d.Im + 2LL * d.bc;
         w.PROJ = e.alloc_f(R * (C + d.Im));
-        w.DTR = e.alloc_f(R * d.nhm);
         w.DTS = e.alloc_f(R * d.nhm);
         w.DEC = e.alloc_f(R * d.nhm);
         w.MXC = e.alloc_f(R * C);
         w.YS = e.alloc_f(R * d.Im * kMaxRowParts);
         w.YN = e.alloc_act(R * d.Im, false);
-        if (!w.PROJ || !w.DTR || !w.DTS || !w.DEC || !w.MXC || !w.YS ||
+        if (!w.PROJ || !w.DTS || !w.DEC || !w.MXC || !w.YS ||
             any_null(w.YN, false, e.lowp))
           return HK_ERR_HIP;
         max_n = std::max<int64_t>(max_n, C + d.Im);
@@ -552,7 +551,7 @@ struct Lin {
 // y = x . W^T (+ b); CastLinear semantics when W is a reduced-precision slot.
 int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int M, int N, int K,
            int act, const float* residual, int64_t ldr, float* out, int64_t ldo, uint16_t* out_lp,
-           int64_t ldl, hipStream_t s) {
+           int64_t ldl, hipStream_t s, const float* dt_a = nullptr, float* dt_decay = nullptr) {
   GemmArgs g;
   const bool lp = lin.w->def.lp && e.lowp;
   g.type = !lp ? GemmType::kF32 : e.lp_fmt == kLpF16 ? GemmType::kF16 : GemmType::kBF16;
@@ -580,6 +579,9 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
   g.ep.ldo = ldo;
   g.ep.out_lp = out_lp;
   g.ep.ldl = ldl;
+  g.ep.dt_a = dt_a;
+  g.ep.dt_decay = dt_decay;
+  g.ep.ldd = N;
   return timed(e, 4, s, [&] { return gemm(g, w.gemm_ws, s); });
 }
 
@@ -816,9 +818,10 @@ int run_mamba2(Engine& e, int l, const Runs& r, hipStream_t s) {
   // model/mamba2.py:77-97
   HK_TRY(linear(e, w, w.A, H, {S(e, kMamba2, l, M_PROJ_W), nullptr}, n, W, H, 0, nullptr, 0,
                 w.PROJ, W, nullptr, 0, s));
+  // dt = softplus(dt_proj(x)) and decay = exp(A dt) in the GEMM's epilogue
   HK_TRY(linear(e, w, Act{w.A.f, nullptr}, H, {S(e, kMamba2, l, M_DT_W), S(e, kMamba2, l, M_DT_B)},
-                n, d.nhm, H, 0, nullptr, 0, w.DTR, d.nhm, nullptr, 0, s));
-  HK_TRY(mamba2_dt(w.DTR, F32(e, kMamba2, l, M_A), n, d.nhm, w.DTS, w.DEC, s));
+                n, d.nhm, H, 0, nullptr, 0, w.DTS, d.nhm, nullptr, 0, s,
+                F32(e, kMamba2, l, M_A), w.DEC));
   HK_TRY(conv_scan(r, w.PROJ, W, C, st[MS_CONV], le[MS_CONV], F32(e, kMamba2, l, M_CONV_W),
                    F32(e, kMamba2, l, M_CONV_B), 1, w.MXC, C, s));
   MatScanDesc m = mat_state_desc(e, kMamba2, l);

@@ -35,6 +35,12 @@ struct GemmEpilogue {
   int lp_fmt = kLpBF16;             // LpFmt of round_lp and out_lp
   bool round_lp = false;            // round (acc + bias) to lp_fmt first
   int act = 0;                      // 0 none, 1 relu (after rounding)
+  // Mamba2's dt (model/mamba2.py:92-97), fp32 products only: with dt_a set
+  // the result is dt = softplus(acc + bias) (in out), and
+  // dt_decay[m, n] = exp(dt_a[n] * dt).
+  const float* dt_a = nullptr;
+  float* dt_decay = nullptr;
+  int64_t ldd = 0;
 };
 
 struct GemmArgs {

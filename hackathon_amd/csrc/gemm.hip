@@ -399,6 +399,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
         if (ep.round_lp) v = round_lp(v, ep.lp_fmt);
         if (ep.act == 1) v = fmaxf(v, 0.0f);
         outv[i][j][e] = v + res[i][j][e];
+        if (ep.dt_a) outv[i][j][e] = softplus(outv[i][j][e]);
       }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -413,6 +414,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
         if (m >= g.M) continue;
         if (ep.out) ep.out[(int64_t)m * ep.ldo + nc] = outv[i][j][e];
         if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_lp_bits(outv[i][j][e], ep.lp_fmt);
+        if (ep.dt_decay) ep.dt_decay[(int64_t)m * ep.ldd + nc] = expf(ep.dt_a[n] * outv[i][j][e]);
       }
     }
   }
@@ -824,6 +826,7 @@ void launch_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, i
 int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int splits_hint) {
   HK_REQUIRE(g.type != GemmType::kF32 && g.batch == 1 && g.A2 == nullptr && g.a_period == 0,
              "gemm: a packed weight needs a 16-bit single GEMM");
+  HK_REQUIRE(g.ep.dt_a == nullptr, "gemm: the dt epilogue is for fp32 products");
   HK_REQUIRE(packable(g.N, g.K), "gemm: packed weight shape N=%d K=%d", g.N, g.K);
   const int fmt = g.type == GemmType::kF16 ? kLpF16 : kLpBF16;
   HK_REQUIRE(!(g.ep.round_lp || g.ep.out_lp) || g.ep.lp_fmt == fmt,

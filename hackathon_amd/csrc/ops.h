@@ -65,10 +65,6 @@ int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const fl
                 int n_rows, int inner, int head_size, float* out, uint16_t* out_lp, int lp_fmt,
                 const LogCommit& lc, hipStream_t s);
 
-// dt = softplus(dt_raw); decay = exp(a[head] * dt) (model/mamba2.py:92-97).
-int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float* dt,
-              float* decay, hipStream_t s);
-
 // The RetNet position bookkeeping a tick leaves per (slot, head)
 // (model/retnet.py:264-269): offsets += run length, and the scale advanced
 // s' = s*gamma + 1 once per step; one job per (run, head), run after every

@@ -215,18 +215,6 @@ __global__ __launch_bounds__(256) void mamba2_post_kernel(
   }
 }
 
-__global__ void mamba2_dt_kernel(const float* __restrict__ dt_raw, const float* __restrict__ a,
-                                 int n_rows, int heads, float* __restrict__ dt,
-                                 float* __restrict__ decay) {
-  const int64_t total = (int64_t)n_rows * heads;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const float v = softplus(dt_raw[i]);
-    dt[i] = v;
-    decay[i] = expf(a[i % heads] * v);
-  }
-}
-
 // One wave per head.
 // A head's values held in registers (head_size <= 64 * kHeadPostMax).
 constexpr int kHeadPostMax = 16;
@@ -674,15 +662,6 @@ int mamba2_post(const float* ssm_out, int n_parts, int64_t part_stride, const fl
   hipLaunchKernelGGL(mamba2_post_kernel, dim3(rows_and_commit(n_rows, lc, 256)), dim3(256), 0, s,
                      ssm_out, n_parts, part_stride, x, ldx, z, ldz, d, w, inner, head_size, out,
                      out_lp, lp_fmt, n_rows, lc);
-  HK_LAUNCH_CHECK();
-  return HK_OK;
-}
-
-int mamba2_dt(const float* dt_raw, const float* a, int n_rows, int heads, float* dt,
-              float* decay, hipStream_t s) {
-  if (n_rows == 0) return HK_OK;
-  hipLaunchKernelGGL(mamba2_dt_kernel, dim3(grid_for((int64_t)n_rows * heads)), dim3(256), 0, s,
-                     dt_raw, a, n_rows, heads, dt, decay);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }

@@ -52,9 +52,11 @@ __global__ __launch_bounds__(256) void conv_scan_kernel(
   };
   load(xa, r0);
   for (int rb = r0; rb < r1; rb += 2 * kConvChunk) {
-    load(xb, rb + kConvChunk);
+    // (most runs fit one chunk: no prefetch of chunks past the run)
+    if (rb + kConvChunk < r1) load(xb, rb + kConvChunk);
     step(xa, rb);
-    load(xa, rb + 2 * kConvChunk);
+    if (rb + kConvChunk >= r1) break;
+    if (rb + 2 * kConvChunk < r1) load(xa, rb + 2 * kConvChunk);
     step(xb, rb + kConvChunk);
   }
   st[c] = s0;
