@@ -66,6 +66,12 @@ struct Tr<GemmType::kF32> {
 typedef const __attribute__((address_space(1))) void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 
+// Raw buffer resource word 3 (gfx9: 32-bit data format, no stride, no
+// swizzle), and the cache-policy operand of a buffer access that is coherent
+// across the device's XCDs (sc1, as agent-scope atomics compile to).
+constexpr int kBufWord3 = 0x00020000;
+constexpr int kCoherentSc1 = 16;
+
 // LDS address (byte offset) of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -602,28 +608,24 @@ __global__ __launch_bounds__(64 * NW) void gemm_wp_kernel(GemmArgs g, float* par
 
   // Fragment (m, c): lane holds rows 16 m + 4 fq + e, column 16 c + fr.
   if (splits > 1) {
-    // (The host keeps splits * M * N within the int range.)
-    const int MN = g.M * g.N;
-    int off[MF][2][4];
+    // Partials in fragment order, [tile][split][wave][fragment][lane] of
+    // float4 (tile = tn * tiles_m + tm): a lane's four values of a fragment
+    // are one 16-byte agent-coherent (sc1) store and load, and a wave's
+    // access is 1 KB contiguous. Waves past N store and read nothing.
+    constexpr int TILE = BMT * BNT;  // floats per tile and split
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        partial + ((int64_t)tn * tiles_m + tm) * splits * TILE, 0, splits * TILE * 4,
+        kBufWord3);
+    const int lane_b = (wave * MF * 2 * 64 + lane) * 16;
+    if (cols_live) {
 #pragma unroll
-    for (int m = 0; m < MF; ++m)
+      for (int m = 0; m < MF; ++m)
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int n = nw0 + 16 * c + fr;
-          const int r = m0 + 16 * m + 4 * fq + e;
-          off[m][c][e] = (cols_live && r < g.M) ? r * g.N + n : -1;
-        }
-#pragma unroll
-    for (int m = 0; m < MF; ++m)
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (off[m][c][e] >= 0)
-            __hip_atomic_store(partial + split * MN + off[m][c][e], acc[m][c][e], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        for (int c = 0; c < 2; ++c)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[m][c]), prs,
+                                                 lane_b + (m * 2 + c) * 1024, split * TILE * 4,
+                                                 kCoherentSc1);
+    }
     // Every partial store of this lane acknowledged at the agent-coherent
     // level, then every wave's, before the tile counter sees this split.
     wait_vmcnt<0>();
@@ -636,6 +638,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_wp_kernel(GemmArgs g, float* par
     __syncthreads();
     if (!last_split) return;
     if (tid == 0) __hip_atomic_store(arrival, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!cols_live) return;
     // Sum in split order; this split's own part comes from its registers.
     floatx4 sum[MF][2];
 #pragma unroll
@@ -643,17 +646,21 @@ __global__ __launch_bounds__(64 * NW) void gemm_wp_kernel(GemmArgs g, float* par
 #pragma unroll
       for (int c = 0; c < 2; ++c) sum[m][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int sp = 0; sp < splits; ++sp) {
-      float t[MF][2][4];
+      floatx4 t[MF][2];
+      if (sp != split) {
 #pragma unroll
-      for (int m = 0; m < MF; ++m)
+        for (int m = 0; m < MF; ++m)
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+          for (int c = 0; c < 2; ++c)
+            t[m][c] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(prs, lane_b + (m * 2 + c) * 1024,
+                                                               sp * TILE * 4, kCoherentSc1));
+      } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            t[m][c][e] = (sp != split && off[m][c][e] >= 0)
-                             ? __hip_atomic_load(partial + sp * MN + off[m][c][e], __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT)
-                             : acc[m][c][e];
+        for (int m = 0; m < MF; ++m)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) t[m][c] = acc[m][c];
+      }
 #pragma unroll
       for (int m = 0; m < MF; ++m)
 #pragma unroll
@@ -836,17 +843,30 @@ int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int 
   // that the smallest, with K split to fill the device. Measured on the
   // ensemble's shapes (M 77-256, N 2048-8448, K 128-4096): taller tiles or
   // split K lose to more, smaller work-groups, because each CU's concurrent
-  // L2 misses, not its MFMA or LDS rate, bound these GEMMs.
+  // L2 misses, not its MFMA or LDS rate, bound these GEMMs. The one
+  // exception is a long K (4096): one tile size up with K split in two
+  // gains (alone on the device 256x2048x4096 15.5 against 16.9 us,
+  // 179x2048x4096 15.6 / 16.5, 77x2048x4096 11.5 / 15.6; in the C4 tick
+  // 8.95-8.97 against 9.04-9.06 ms). Every K = 2048 shape loses with any
+  // split, and 128x128 tiles lose everywhere.
   const int min_tiles = g.min_tiles > 0 ? g.min_tiles : kMinTilesAlone;
   static const int kTiles[4][2] = {{4, 4}, {4, 2}, {2, 2}, {2, 1}};  // (MF, NW)
+  auto tiles_of = [&](int c) {
+    return (int64_t)((g.M + 16 * kTiles[c][0] - 1) / (16 * kTiles[c][0])) *
+           ((g.N + 32 * kTiles[c][1] - 1) / (32 * kTiles[c][1]));
+  };
   int pick = 3;
-  for (int c = 0; c < 4; ++c) {
-    const int64_t t = (int64_t)((g.M + 16 * kTiles[c][0] - 1) / (16 * kTiles[c][0])) *
-                      ((g.N + 32 * kTiles[c][1] - 1) / (32 * kTiles[c][1]));
-    if (t >= min_tiles) {
+  bool fits = false;
+  for (int c = 0; c < 4 && !fits; ++c) {
+    if (tiles_of(c) >= min_tiles) {
       pick = c;
-      break;
+      fits = true;
     }
+  }
+  int long_k_splits = 0;
+  if (fits && pick > 0 && g.K >= 4096 && 2 * tiles_of(pick - 1) >= min_tiles) {
+    --pick;
+    long_k_splits = 2;
   }
   const int mf = kTiles[pick][0];
   const int nw = kTiles[pick][1];
@@ -856,17 +876,22 @@ int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int 
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
   const int ktiles = g.K / 64;
   int splits = splits_hint;
-  if (splits <= 0) {
+  if (splits <= 0 && long_k_splits > 0) {
+    splits = long_k_splits;
+  } else if (splits <= 0) {
     splits = tiles >= min_tiles ? 1 : (int)((256 + tiles - 1) / tiles);
     splits = std::min(splits, std::max(1, ktiles / 4));
     splits = std::min(splits, 16);
   }
   splits = std::max(1, std::min(splits, ktiles));
-  while (splits > 1 && (int64_t)splits * g.M * g.N > ws.partial_elems) --splits;
+  // (partials are whole tiles: 16*mf x 32*nw floats per tile and split)
+  while (splits > 1 && (int64_t)splits * tiles * (16 * mf) * (32 * nw) > ws.partial_elems) --splits;
   if (tiles > ws.arrival_elems || ws.arrivals == nullptr) splits = 1;
   const int per = (ktiles + splits - 1) / splits;
   splits = (ktiles + per - 1) / per;
   HK_REQUIRE(tiles * splits < (1LL << 31), "gemm: grid too large");
+  HK_REQUIRE(splits == 1 || (int64_t)splits * (16 * mf) * (32 * nw) * 4 < (1LL << 31),
+             "gemm: split tile too large");
   const bool f16 = g.type == GemmType::kF16;
 #define HK_WP_CASE(MF_, NW_, R_)                                                             \
   if (mf == MF_ && nw == NW_ && R == R_) {                                                  \
