@@ -280,13 +280,19 @@ __global__ __launch_bounds__(256) void slstm_round_kernel(
 // Persistent sLSTM recurrence for a whole tick: one launch per layer instead
 // of one launch per step. Work-group g (512 threads, 8 waves) owns 16 units
 // of one head: 64 gate rows (unit*4 + gate) x hs inputs of the recurrent
-// weights, held in VGPRs for every step as fp32 MFMA A fragments (wave =
+// weights, held in VGPRs for every step as MFMA A fragments (wave =
 // (16-row tile, k half)). Step t, per chunk of up to 16 active runs: stage
-// h_{t-1} of the chunk's runs in LDS; G[64 rows x runs] = W . H, on
-// v_mfma_f32_16x16x4_f32 when the chunk has more than kValuRuns runs, else
-// as VALU dot products over the same register-resident weights (past the
-// first steps of a skewed tick only a few long runs remain); add the two k
-// halves through LDS; then the cell update, one (run, unit) per thread.
+// h_{t-1} of the chunk's runs in LDS; G[64 rows x runs] = W . H; add the two
+// k halves through LDS; then the cell update, one (run, unit) per thread.
+// The product, for head sizes 64-512: split f16 on v_mfma_f32_16x16x32_f16,
+// W*S and h*kHScale each as an f16 value plus its f16 remainder (22
+// significant bits), G = hi.hi + (hi.lo + lo.hi) with fp32 accumulation and
+// an exact power-of-two unscale: the dropped lo.lo term is below 2^-22 of
+// each product, under the rounding of an fp32 dot product of this length,
+// and the step costs 24 matrix instructions per wave (fp32 matrix cores
+// took 64 of twice the cycles each; at 16 runs the fp32 product bound the
+// step). For head size 32: v_mfma_f32_16x16x4_f32 when the chunk has more
+// than kValuRuns runs, else VALU dot products over the same weights.
 //
 // h_t crosses work-groups (and XCDs) through an exchange buffer of 64-bit
 // words (value bits | tag << 32) stored and loaded with agent-scope atomics.
@@ -332,6 +338,34 @@ struct SlstmPersistArgs {
 };
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 halfx8_t __attribute__((ext_vector_type(8)));
+
+// The split-f16 product stages h as h * kHScale (hi = f16 of it, lo = f16 of
+// the remainder): every h the recurrence produces has |h| < 1 (|c| <= n),
+// the scale keeps small values clear of f16 subnormals, and |h| below
+// 65504 / kHScale stays finite.
+constexpr float kHScale = 256.0f;
+
+// Power of two that puts a row's largest |w| (m) in [2^13, 2^14), so that
+// w*S splits into an f16 hi part and an f16 remainder with 22 significant
+// bits together and no overflow (S = 2^100 for an all-zero row).
+__device__ __forceinline__ float row_split_scale(float m) {
+  const int ex = (int)((__float_as_uint(m) >> 23) & 0xffu);
+  return ldexpf(1.0f, min(max(140 - ex, -100), 100));
+}
+
+__device__ __forceinline__ void stage_split4(_Float16* hi, _Float16* lo, float4 v) {
+  const float x[4] = {v.x * kHScale, v.y * kHScale, v.z * kHScale, v.w * kHScale};
+  _Float16 h[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = (_Float16)x[e];
+    l[e] = (_Float16)(x[e] - (float)h[e]);
+  }
+  typedef _Float16 halfx4_t __attribute__((ext_vector_type(4)));
+  *reinterpret_cast<halfx4_t*>(hi) = halfx4_t{h[0], h[1], h[2], h[3]};
+  *reinterpret_cast<halfx4_t*>(lo) = halfx4_t{l[0], l[1], l[2], l[3]};
+}
 
 // LDS ints of the run descriptors (run_off, slot_ids, act), kept even so
 // that what follows stays 8-byte aligned.
@@ -394,7 +428,14 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
   constexpr int PAD = hs + 8;       // LDS row stride of h (spreads runs over banks)
   constexpr int KH = hs / 2;        // k per wave
   constexpr int KG = KH / 16;       // groups of 4 MFMA k-steps per wave
-  float* hbuf = smem;                               // [16][PAD]
+  // head sizes 64-512 multiply on split f16 (hi/lo) matrix cores, 32 on fp32
+  constexpr bool kF16 = HS >= 64;
+  constexpr int PADH = PAD;         // f16 row stride of the split h planes
+  float* hbuf = smem;                               // [16][PAD] (fp32 path)
+  // split-f16 path: the same bytes as two [16][PADH] planes of f16, h*kHScale
+  // rounded (hi) and its remainder (lo)
+  _Float16* hhi = reinterpret_cast<_Float16*>(smem);
+  _Float16* hlo = hhi + kPersistRuns * PADH;
   float* gsum = hbuf + kPersistRuns * PAD;          // [16 runs][64 rows], k half 0
   float* xbuf = gsum + kPersistRuns * 64;           // [16 runs][64 rows], k half 1
   // The run descriptors, copied to LDS once: every step reads them, and a
@@ -417,21 +458,66 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
   const int fr = lane & 15;         // A row / B column (run) / C column
   const int fk = lane >> 4;         // k sub-group / C row group
 
-  // A fragments: for k-step group g and step c, this lane covers
-  // k = kh*KH + 16*g + 4*fk + c of row 16*mt + fr (A and B use the same map).
-  float w[4 * KG];
+  // Weights, fp32 path (head size 32): A fragments of v_mfma_f32_16x16x4f32;
+  // for k-step group g and step c this lane covers k = kh*KH + 16*g + 4*fk
+  // + c of row 16*mt + fr (A and B use the same map).
+  // Split-f16 path (head sizes 64-512): A fragments of
+  // v_mfma_f32_16x16x32_f16 for k-step s: k = kh*KH + 32*s + 8*fk .. +7 of
+  // row 16*mt + fr, each weight w*S (S a power of two per row, |w*S| <
+  // 2^14) held as hi = f16(w*S) and lo = f16(w*S - hi).
+  constexpr int KS = kF16 ? KH / 32 : 1;
+  float w[kF16 ? 1 : 4 * KG];
+  halfx8_t whi[KS], wlo[KS];
+  float inv_row[4] = {1.0f, 1.0f, 1.0f, 1.0f};  // 1/(S_row * kHScale), output rows 4*fk + e
   {
     const int row = 16 * mt + fr;
     const int unit = row >> 2, gate = row & 3;
-    const float* src = a.w_state + (((int64_t)gate * a.heads + head) * hs + (u0 + unit)) * hs +
-                       kh * KH + 4 * fk;
+    const float* rsrc = a.w_state + (((int64_t)gate * a.heads + head) * hs + (u0 + unit)) * hs;
+    if constexpr (!kF16) {
+      const float* src = rsrc + kh * KH + 4 * fk;
 #pragma unroll
-    for (int g = 0; g < KG; ++g) {
-      const float4 v = *reinterpret_cast<const float4*>(src + 16 * g);
-      w[4 * g + 0] = v.x;
-      w[4 * g + 1] = v.y;
-      w[4 * g + 2] = v.z;
-      w[4 * g + 3] = v.w;
+      for (int g = 0; g < KG; ++g) {
+        const float4 v = *reinterpret_cast<const float4*>(src + 16 * g);
+        w[4 * g + 0] = v.x;
+        w[4 * g + 1] = v.y;
+        w[4 * g + 2] = v.z;
+        w[4 * g + 3] = v.w;
+      }
+    } else {
+      const float* src = rsrc + kh * KH + 8 * fk;
+      float wf[KS][8];
+      float m = 0.0f;
+#pragma unroll
+      for (int q = 0; q < KS; ++q) {
+        const float4 v0 = *reinterpret_cast<const float4*>(src + 32 * q);
+        const float4 v1 = *reinterpret_cast<const float4*>(src + 32 * q + 4);
+        wf[q][0] = v0.x; wf[q][1] = v0.y; wf[q][2] = v0.z; wf[q][3] = v0.w;
+        wf[q][4] = v1.x; wf[q][5] = v1.y; wf[q][6] = v1.z; wf[q][7] = v1.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(wf[q][e]));
+      }
+      // the row's largest |w|: over the four k groups, then the two k halves
+      m = fmaxf(m, __shfl_xor(m, 16, 64));
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      float* rmax = gsum;  // [2][64], before the step loop uses gsum
+      if (fk == 0) rmax[kh * 64 + row] = m;
+      lds_barrier();
+      const float rs = row_split_scale(fmaxf(rmax[row], rmax[64 + row]));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int orow = 16 * mt + 4 * fk + e;
+        inv_row[e] = 1.0f / (row_split_scale(fmaxf(rmax[orow], rmax[64 + orow])) * kHScale);
+      }
+      lds_barrier();
+#pragma unroll
+      for (int q = 0; q < KS; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = wf[q][e] * rs;
+          const _Float16 h = (_Float16)v;
+          whi[q][e] = h;
+          wlo[q][e] = (_Float16)(v - (float)h);
+        }
     }
   }
   // Cell-update role (threads 0..255): unit uu, run jr of each chunk.
@@ -501,7 +587,12 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
           const int i = u * NT + tid;
           if (i < nvec) {
             const int j = i / vph;
-            *reinterpret_cast<float4*>(hbuf + j * PAD + 4 * (i - j * vph)) = v[u];
+            if constexpr (kF16) {
+              stage_split4(hhi + j * PADH + 4 * (i - j * vph), hlo + j * PADH + 4 * (i - j * vph),
+                           v[u]);
+            } else {
+              *reinterpret_cast<float4*>(hbuf + j * PAD + 4 * (i - j * vph)) = v[u];
+            }
           }
         }
       } else {
@@ -524,7 +615,14 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
           const int i = u * NT + tid;
           if (i < nel) {
             const int j = i / hs;
-            hbuf[j * PAD + (i - j * hs)] = v[u];
+            if constexpr (kF16) {
+              const float x = v[u] * kHScale;
+              const _Float16 h = (_Float16)x;
+              hhi[j * PADH + (i - j * hs)] = h;
+              hlo[j * PADH + (i - j * hs)] = (_Float16)(x - (float)h);
+            } else {
+              hbuf[j * PAD + (i - j * hs)] = v[u];
+            }
           }
         }
       }
@@ -534,7 +632,26 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
       // Each k half writes its partial gate sums to its own LDS plane
       // (gsum: k half 0, xbuf: k half 1); the cell update adds the two.
       float* half = kh == 0 ? gsum : xbuf;
-      if (nj > kValuRuns) {
+      if constexpr (kF16) {
+        // G = W . H as hi*hi + (hi*lo + lo*hi) over this k half, every
+        // chunk size (columns fr >= nj read stale LDS rows; their results
+        // are dropped), then unscaled (powers of two: exact).
+        floatx4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+        const _Float16* bh = hhi + fr * PADH + kh * KH + 8 * fk;
+        const _Float16* bl = hlo + fr * PADH + kh * KH + 8 * fk;
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+          const halfx8_t b_hi = *reinterpret_cast<const halfx8_t*>(bh + 32 * q);
+          const halfx8_t b_lo = *reinterpret_cast<const halfx8_t*>(bl + 32 * q);
+          a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi[q], b_hi, a0, 0, 0, 0);
+          a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi[q], b_lo, a1, 0, 0, 0);
+          a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo[q], b_hi, a1, 0, 0, 0);
+        }
+        const floatx4_t acc = a0 + a1;
+        *reinterpret_cast<float4*>(half + fr * 64 + 16 * mt + 4 * fk) =
+            make_float4(acc[0] * inv_row[0], acc[1] * inv_row[1], acc[2] * inv_row[2],
+                        acc[3] * inv_row[3]);
+      } else if (nj > kValuRuns) {
         // Columns fr >= nj read stale LDS rows; their results are dropped.
         // Four independent accumulator chains (one per step c of a group),
         // summed at the end, so consecutive MFMAs do not wait on each other.
