@@ -170,11 +170,11 @@ MID = spec.ModelConfig(hidden_size=256, proj_size=512, tower_depth=2, num_heads=
 
 
 def test_persistent_slstm_skewed_runs_fp32(dev):
-    # Hidden 256 with 4 sLSTM heads of 64 runs the persistent sLSTM kernel.
-    # Batches shaped like a skewed tick: 40 runs at step 0 (three 16-run
-    # chunks), 5-8 runs at the next steps (MFMA product), then 1-4 runs
-    # (VALU product); then launches with one and with two steps. Predictions
-    # and every state leaf against the oracle's reference rounds.
+    # Hidden 256 with 4 sLSTM heads of 64 runs the persistent sLSTM kernel
+    # (split-f16 matrix-core product). Batches shaped like a skewed tick: 40
+    # runs at step 0 (three 16-run chunks), 5-8 runs at the next steps, then
+    # 1-4 runs; then launches with one and with two steps. Predictions and
+    # every state leaf against the oracle's reference rounds.
     from hackathon_amd.client import NnInferenceClient, PendingRequest
 
     cfg = MID
