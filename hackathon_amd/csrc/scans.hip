@@ -636,18 +636,24 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
         // G = W . H as hi*hi + (hi*lo + lo*hi) over this k half, every
         // chunk size (columns fr >= nj read stale LDS rows; their results
         // are dropped), then unscaled (powers of two: exact).
-        floatx4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+        // four accumulator chains (hi.hi of even and of odd k-steps, hi.lo,
+        // lo.hi), so consecutive matrix instructions seldom wait on each other
+        floatx4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, c0 = a0, c1 = a0;
         const _Float16* bh = hhi + fr * PADH + kh * KH + 8 * fk;
         const _Float16* bl = hlo + fr * PADH + kh * KH + 8 * fk;
 #pragma unroll
         for (int q = 0; q < KS; ++q) {
           const halfx8_t b_hi = *reinterpret_cast<const halfx8_t*>(bh + 32 * q);
           const halfx8_t b_lo = *reinterpret_cast<const halfx8_t*>(bl + 32 * q);
-          a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi[q], b_hi, a0, 0, 0, 0);
-          a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi[q], b_lo, a1, 0, 0, 0);
-          a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo[q], b_hi, a1, 0, 0, 0);
+          if (q % 2 == 0) {
+            a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi[q], b_hi, a0, 0, 0, 0);
+          } else {
+            a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi[q], b_hi, a1, 0, 0, 0);
+          }
+          c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(whi[q], b_lo, c0, 0, 0, 0);
+          c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wlo[q], b_hi, c1, 0, 0, 0);
         }
-        const floatx4_t acc = a0 + a1;
+        const floatx4_t acc = (a0 + a1) + (c0 + c1);
         *reinterpret_cast<float4*>(half + fr * 64 + 16 * mt + 4 * fk) =
             make_float4(acc[0] * inv_row[0], acc[1] * inv_row[1], acc[2] * inv_row[2],
                         acc[3] * inv_row[3]);
