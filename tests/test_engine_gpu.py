@@ -216,6 +216,60 @@ def test_persistent_slstm_skewed_runs_fp32(dev):
     eng.close()
 
 
+def test_persistent_slstm_head512_fp32(dev):
+    """The persistent sLSTM kernel at the default dims' head size (512: the
+    split-f16 product over 8 k-steps per wave) in a one-layer model of width
+    1024 (2 sLSTM heads, so 64 work-groups), on skewed ticks: 20 runs at
+    step 0 (two 16-run chunks), one of 24 steps, then single requests, then
+    a tick of 13 / 6 / 5-step runs. Every prediction and state leaf of the
+    engine against the float64 reference, within 4x the distance of the
+    reference's own fp32 run from it (at this width the fp32 reference is up
+    to 7e-5 relative and 2e-6 absolute from float64), and every prediction
+    within 1e-5 relative + 1e-5 absolute of the float64 result."""
+    from hackathon_amd.engine import Engine, pack_runs
+    from refrun import leaf_rel, reference_rounds, rel_err
+
+    cfg = spec.ModelConfig(hidden_size=1024, proj_size=1024, tower_depth=1, num_heads=4,
+                           num_features=7)
+    params = weights.generate(cfg, 0)
+    n = 20
+    eng = Engine(cfg, capacity=n, max_rows=128, linear_dtype="fp32", device=dev)
+    eng.load_weights(params)
+    schedule = [[24, 9, 7, 6, 5, 3, 2, 2] + [1] * 12, [1] * n,
+                [13, 1, 1, 6, 5, 5, 5, 5, 5, 2] + [1] * 10]
+    rng = np.random.default_rng(7)
+    hist = [[] for _ in range(n)]
+    got = [[] for _ in range(n)]
+    for counts in schedule:
+        syms = rng.permutation(n).astype(np.int32)
+        counts = np.asarray(counts)
+        runs, order = pack_runs(syms, counts)
+        x = np.clip(rng.standard_normal((int(counts.sum()), cfg.num_features)), -5, 5).astype(np.float32)
+        preds = eng.tick(runs, torch.from_numpy(x).to(dev)).cpu().double().numpy()
+        for pos, i in enumerate(order):
+            a, b = int(runs.run_off[pos]), int(runs.run_off[pos + 1])
+            hist[int(syms[i])].extend(x[a:b])
+            got[int(syms[i])].extend(preds[a:b])
+    eng.check()
+    state = eng.export_state(0, n)
+    eng.close()
+    p32, s32 = reference_rounds(om.Params(params), cfg, hist)
+    p64, s64 = reference_rounds(om.Params(params, dtype=torch.float64), cfg, hist)
+    cat = lambda v: np.concatenate([np.asarray(a) for a in v])
+    g, r32, r64 = cat(got), cat(p32), cat(p64)
+    e, sc = rel_err(g, r64).max(0), rel_err(r32, r64).max(0)
+    print(f"head 512: engine max rel err per tower {np.array2string(e, precision=2)}, "
+          f"reference fp32 {np.array2string(sc, precision=2)}")
+    assert (e <= 4.0 * sc).all(), f"engine {e} beyond 4x the reference's fp32 scatter {sc}"
+    _close(torch.from_numpy(g), torch.from_numpy(r64), 1e-5, 1e-5, "head 512 preds vs float64")
+    for i, (gl, al, el) in enumerate(zip(om.flatten(state), om.flatten(s32), om.flatten(s64))):
+        if el.dtype == torch.int32:
+            assert torch.equal(gl.cpu(), el), f"leaf {i}: offsets differ"
+            continue
+        rg, ra = leaf_rel(gl, el), leaf_rel(al, el)
+        assert rg <= 4.0 * ra + 1e-7, f"state leaf {i} {tuple(el.shape)}: engine {rg:.3e}, reference fp32 {ra:.3e}"
+
+
 @pytest.mark.parametrize("lp", ["bf16", "fp16"])
 def test_castlinear_small_fixture(dev, small_params, lp):
     """Engine in CastLinear mode against the reference's own
