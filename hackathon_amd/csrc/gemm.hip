@@ -867,6 +867,11 @@ int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int 
   if (fits && pick > 0 && g.K >= 4096 && 2 * tiles_of(pick - 1) >= min_tiles) {
     --pick;
     long_k_splits = 2;
+  } else if (!fits && g.K >= 4096) {
+    // too few rows for even the smallest tile: 32x64 tiles with K split up
+    // to 4 ways (64x2048x4096 9.4 against 11.0 us for 32x32 split 2)
+    pick = 2;
+    long_k_splits = (int)std::min<int64_t>(4, std::max<int64_t>(2, (256 + tiles_of(2) - 1) / tiles_of(2)));
   }
   const int mf = kTiles[pick][0];
   const int nw = kTiles[pick][1];
