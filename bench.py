@@ -80,9 +80,45 @@ def matrix_scan_bytes(ticks, first, depth, tile_bytes, entry_bytes, row_bytes):
 
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 GEMM_COUNTERS = os.path.join(PROFILES, "gemm_cast_linear_tick_replay_hbm_counters.txt")
+GEMM_L1_L2 = os.path.join(PROFILES, "gemm_cast_linear_tick_replay_l1_l2_requests.txt")
+CU_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
+N_CUS = 256
 # The packed projection kernel's tile rule inside an engine tick (gemm.h
 # kMinTilesShared); 0 selects the rule for a GEMM alone on the device.
 TICK_MIN_WORK_GROUPS = 112
+
+
+def _summary_values(path):
+    """key: value lines of a committed counter summary ({} if absent)."""
+    try:
+        text = open(path).read()
+    except OSError:
+        return {}
+    vals = {}
+    for line in text.splitlines():
+        key, _, rest = line.partition(":")
+        if rest.strip() and not key.lstrip().startswith("#"):
+            try:
+                vals[key.strip()] = float(rest.split()[0])
+            except ValueError:
+                pass
+    return vals
+
+
+def l1_l2_reads(path, avg_s):
+    """The GEMM's L1 -> L2 read bytes per dispatch from a committed
+    rocprofv3 summary (TCP_TCC_READ_REQ x line size), and the rate that
+    makes at the given average launch duration, summed over the device and
+    per CU per cycle; None if the summary is absent."""
+    v = _summary_values(path)
+    if "read_req_per_dispatch" not in v or "read_req_bytes" not in v or avg_s <= 0:
+        return None
+    b = v["read_req_per_dispatch"] * v["read_req_bytes"]
+    return {"read_bytes_per_launch": b, "TBps": b / avg_s / 1e12,
+            "bytes_per_cu_per_clk": b / avg_s / N_CUS / CU_CLOCK_HZ,
+            "source": os.path.relpath(path, os.path.dirname(PROFILES)),
+            "note": "the kernel's bound: L1 -> L2 line reads (W once per row tile, A once per "
+                    "column tile) at a per-CU rate capped by the L1's in-flight request limit"}
 
 
 def counter_traffic(path, algorithmic_per_dispatch):
@@ -590,7 +626,8 @@ def bench_gemm(args) -> int:
                    "rows": int(run_off[-1]), "xlstm_groups_first_run": xlstm_split_point(run_off)},
         "roofline": {"bound": "hbm", "achieved": rf["achieved_GBs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": rf["hbm_frac"], "traffic": traffic,
-                     "traffic_over_algorithmic": ratio, **rf},
+                     "traffic_over_algorithmic": ratio,
+                     "l1_l2": l1_l2_reads(GEMM_L1_L2, rf["avg_us"] * 1e-6), **rf},
         "event_bracketed_us_by_shape": {f"{m}x{n}x{k}": round(1e6 * float(t), 2)
                                         for (m, n, k), t in zip(shapes[:12], each[:12])},
     }
@@ -1159,6 +1196,7 @@ def main() -> int:
             "frac": grf["hbm_frac"],
             "traffic": traffic,
             "traffic_over_algorithmic": traffic_ratio,
+            "l1_l2": l1_l2_reads(GEMM_L1_L2, grf["avg_us"] * 1e-6),
             "mfma": {"achieved": grf["achieved_TFLOPs"], "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": grf["mfma_frac"]},
             "launches": grf["launches"],
