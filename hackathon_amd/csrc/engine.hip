@@ -106,7 +106,20 @@ struct Slot {
   void* ptr = nullptr;   // device storage (16-bit when def.lp && lowp, else fp32)
   bool packed = false;   // 16-bit weight held in the pack_lp_weight layout
   bool bound = false;
+  // fp32 slots: the power of two that puts the largest |w| in [2^13, 2^14),
+  // for products run as split f16 (GemmArgs::split_wscale); set at binding
+  float split_scale = 1.0f;
 };
+
+// Power of two that puts max |w| of an fp32 weight in [2^13, 2^14) (1 for
+// an all-zero or non-finite maximum).
+float split_scale_of(const float* w, int64_t n) {
+  float m = 0.0f;
+  for (int64_t i = 0; i < n; ++i) m = std::fmax(m, std::fabs(w[i]));
+  if (!(m > 0.0f) || !std::isfinite(m)) return 1.0f;
+  const int e = std::ilogb(m);  // m in [2^e, 2^(e+1))
+  return std::ldexp(1.0f, std::min(std::max(13 - e, -100), 100));
+}
 
 struct Dims {
   int H, P, D, nh, F, Fpad;
@@ -590,11 +603,18 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
 // (or x2 for j >= x2_from) and W[b] = W + b*bs*bs, writing out columns
 // b*bs .. b*bs + bs - 1:
 //   out[:, b*bs + o] = sum_h src[:, k*bs + h] * W[b][o][h].
+// The BlockLinear products of the sLSTM gate inputs and the RG-LRU gates run
+// as split f16 on matrix cores (GemmArgs::split_wscale; `wscale` is the
+// weight slot's split_scale): fp32-level error (each operand as an f16 value
+// plus its f16 remainder), a fifth of the fp32 matrix-core time per product.
+// Their inputs (LayerNorm outputs, silu(conv) and conv outputs of
+// normalised rows) stay far below the f16 range the split needs (65504).
 int block_linear(Engine& e, TowerWS& w, const float* x, const float* x2, int x2_from, int64_t ldx,
-                 const float* W, int products, int blocks, int bs, int M, float* out, int64_t ldo,
-                 hipStream_t s) {
+                 const float* W, float wscale, int products, int blocks, int bs, int M, float* out,
+                 int64_t ldo, hipStream_t s) {
   GemmArgs g;
   g.type = GemmType::kF32;
+  g.split_wscale = wscale;
   g.A = x;
   g.A2 = x2;
   g.a2_from = x2 ? x2_from * blocks : 0;
@@ -713,7 +733,8 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
   HK_TRY(conv_scan(r, w.XN, H, H, st[XS_S_CONV], le[XS_S_CONV], F32(e, kXLSTM, l, X_S_CONV_W),
                    F32(e, kXLSTM, l, X_S_CONV_B), 1, w.XCA, H, s));
   // i, f from the conv path, z, o from LN(x): one launch of 4 x nh_s blocks
-  HK_TRY(block_linear(e, w, w.XCA, w.XN, 2, H, F32(e, kXLSTM, l, X_S_IN_W), 4, d.nh_s, d.bs_s, n,
+  HK_TRY(block_linear(e, w, w.XCA, w.XN, 2, H, F32(e, kXLSTM, l, X_S_IN_W),
+                      S(e, kXLSTM, l, X_S_IN_W)->split_scale, 4, d.nh_s, d.bs_s, n,
                       w.GIN, 4 * H, s));
   if (slstm_persist_supported(H, d.nh_s)) {
     if (ord.wait) HK_CHECK_HIP(hipStreamWaitEvent(s, ord.wait, 0));
@@ -899,7 +920,8 @@ int run_hawk(Engine& e, int l, const Runs& r, hipStream_t s) {
   HK_TRY(conv_scan(r, w.GRP + H, 2 * H, H, st[KS_CONV], le[KS_CONV], F32(e, kHawk, l, K_CONV_W),
                    F32(e, kHawk, l, K_CONV_B), 0, w.KXC, H, s));
   // input and recurrence gates of the RG-LRU, one launch of 2 x nb_h blocks
-  HK_TRY(block_linear(e, w, w.KXC, nullptr, 0, H, F32(e, kHawk, l, K_GATES_W), 2, d.nb_h, d.bs_h,
+  HK_TRY(block_linear(e, w, w.KXC, nullptr, 0, H, F32(e, kHawk, l, K_GATES_W),
+                      S(e, kHawk, l, K_GATES_W)->split_scale, 2, d.nb_h, d.bs_h,
                       n, w.GATES, 2 * H, s));
   HK_TRY(rglru_scan(r, w.KXC, w.GATES, w.GATES + H, 2 * H, w.GRP, 2 * H, F32(e, kHawk, l, K_A),
                     8.0f, H, st[KS_H], w.GH.f, w.GH.l, e.lp_fmt, s));
@@ -1335,6 +1357,7 @@ int hk_engine_load_param(void* h, int tower, int layer, int slot, const float* h
     HK_CHECK_HIP(hipMemcpy(s->ptr, v.data(), (size_t)numel * 4, hipMemcpyHostToDevice));
   } else {
     HK_CHECK_HIP(hipMemcpy(s->ptr, host, (size_t)numel * 4, hipMemcpyHostToDevice));
+    s->split_scale = hk::split_scale_of(host, numel);
   }
   s->bound = true;
   return HK_OK;
@@ -1384,6 +1407,7 @@ int hk_engine_load_param_noalloc(void* h, int tower, int layer, int slot, const 
     HK_CHECK_HIP(hipStreamSynchronize(nullptr));
   } else {
     HK_CHECK_HIP(hipMemcpy(s->ptr, host, (size_t)numel * 4, hipMemcpyHostToDevice));
+    s->split_scale = hk::split_scale_of(host, numel);
   }
   s->bound = true;
   return HK_OK;

@@ -68,6 +68,12 @@ struct GemmArgs {
   // that has the device to itself; the engine's ticks, where three other
   // streams share the device, pass kMinTilesShared).
   int min_tiles = 0;
+  // fp32 operands only: > 0 runs the product on f16 matrix cores, each
+  // operand as an f16 value plus its f16 remainder (hi.hi + hi.lo + lo.hi,
+  // fp32 accumulation), W multiplied by this power of two first and the
+  // result by its inverse (the caller picks it so that |w| * scale < 2^14);
+  // A must stay below 65504 in magnitude.
+  float split_wscale = 0.0f;
   GemmEpilogue ep;
 };
 

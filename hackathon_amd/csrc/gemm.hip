@@ -117,7 +117,23 @@ __device__ __forceinline__ void wait_slabs(int k) {
   }
 }
 
-template <GemmType T, int BK, int S>
+// Eight fp32 values (two groups of four) * scale as f16 values (hi) and the
+// f16 of their remainders (lo): hi + lo holds 22 significant bits of each.
+__device__ __forceinline__ void split_f16x8(u32x4 a, u32x4 b, float scale, halfx8& hi,
+                                            halfx8& lo) {
+  const floatx4 fa = __builtin_bit_cast(floatx4, a), fb = __builtin_bit_cast(floatx4, b);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x0 = fa[e] * scale, x1 = fb[e] * scale;
+    const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+    hi[e] = h0;
+    hi[4 + e] = h1;
+    lo[e] = (_Float16)(x0 - (float)h0);
+    lo[4 + e] = (_Float16)(x1 - (float)h1);
+  }
+}
+
+template <GemmType T, int BK, int S, bool SPLIT = false>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, int* arrivals,
                                                     int splits, int tiles_m, int tiles_n) {
   using E = typename Tr<T>::E;
@@ -250,6 +266,37 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
         __asm__ volatile("" ::: "memory");
         if (i + S - 1 < nslab) issue(stage[(j + S - 1) % S], kt0 + i + S - 1);
         const uint32_t st = lds_addr(stage[j]);
+        if constexpr (SPLIT) {
+          // fp32 operands on f16 matrix cores: a lane's 8 values of a row
+          // (k = 4*fk + c and 16 + 4*fk + c; A and B share the map, which
+          // is all the product needs) become an f16 value plus its f16
+          // remainder each (W scaled by a power of two first), and
+          // hi.hi + hi.lo + lo.hi accumulate in fp32 (v_mfma_f32_16x16x32_f16).
+          u32x4 fa[2][2], fb[2][2];  // [ks][fragment]
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            fa[ks][0] = ds_read16(st + arow[0] + (((ks * 4 + fk) ^ akey[0]) << 4));
+            fa[ks][1] = ds_read16(st + arow[1] + (((ks * 4 + fk) ^ akey[1]) << 4));
+            fb[ks][0] = ds_read16(st + brow[0] + (((ks * 4 + fk) ^ bkey[0]) << 4));
+            fb[ks][1] = ds_read16(st + brow[1] + (((ks * 4 + fk) ^ bkey[1]) << 4));
+          }
+          ds_wait4(fa[0][0], fa[0][1], fb[0][0], fb[0][1]);
+          ds_wait4(fa[1][0], fa[1][1], fb[1][0], fb[1][1]);
+          halfx8 ahi[2], alo[2], bhi[2], blo[2];
+#pragma unroll
+          for (int i2 = 0; i2 < 2; ++i2) {
+            split_f16x8(fa[0][i2], fa[1][i2], 1.0f, ahi[i2], alo[i2]);
+            split_f16x8(fb[0][i2], fb[1][i2], g.split_wscale, bhi[i2], blo[i2]);
+          }
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ii], bhi[q], acc[ii][q], 0, 0, 0);
+              acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ii], blo[q], acc[ii][q], 0, 0, 0);
+              acc[ii][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ii], bhi[q], acc[ii][q], 0, 0, 0);
+            }
+        } else {
 #pragma unroll
         for (int ks = 0; ks < BK * (int)sizeof(E) / 64; ++ks) {
           // Four 16-byte fragment reads (A rows i, B columns i) of one
@@ -293,10 +340,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
             }
           }
         }
+        }
       }
     }
   }
   // (Every transfer was waited for before its slab; nothing is in flight.)
+  if constexpr (SPLIT) {
+    const float inv = 1.0f / g.split_wscale;  // a power of two: exact
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] *= inv;
+  }
 
   // Fragment (i, j): lane holds rows 4*fk + e, column fr.
   if (splits > 1) {
@@ -985,6 +1040,10 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
                        tiles_m, tiles_n);
   } else if (g.type == GemmType::kF16) {
     hipLaunchKernelGGL((gemm_kernel<GemmType::kF16, Tr<GemmType::kF16>::BK, kStages>),
+                       dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, ws.arrivals, splits,
+                       tiles_m, tiles_n);
+  } else if (!narrow && g.split_wscale > 0.0f) {
+    hipLaunchKernelGGL((gemm_kernel<GemmType::kF32, Tr<GemmType::kF32>::BK, kStages, true>),
                        dim3((unsigned)nwg), dim3(256), 0, stream, g, ws.partial, ws.arrivals, splits,
                        tiles_m, tiles_n);
   } else if (!narrow) {
