@@ -574,9 +574,11 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
   g.W = lin.w->ptr;
   g.ldw = K;
   g.w_packed = lp && lin.w->packed;
-  // In the reduced-precision modes the linears kept fp32 (Mamba2's dt_proj)
-  // run as split f16 like the BlockLinear products (fp32-level error; their
-  // input is an RMSNorm output); the fp32 mode keeps fp32 arithmetic here.
+  // In the reduced-precision modes the kept-fp32 linears that run here
+  // (Mamba2's dt_proj, whose input is an RMSNorm output; the mLSTM gate
+  // projections over q, k, v on shapes mlstm_qkv_if does not cover) run as
+  // split f16 like the BlockLinear products (fp32-level error); the fp32
+  // mode keeps fp32 arithmetic here.
   if (!lp && e.lowp) g.split_wscale = lin.w->split_scale;
   // A tick's four streams share the device: above 64 rows the larger tiles
   // of the shared rule measure faster in the tick (C4: 9.21-9.24 against

@@ -6,7 +6,9 @@
 //        (example_model.py:92-95);
 //   fp32 (v_mfma_f32_16x16x4_f32)   - the fp32 path and the linears kept fp32
 //        (example_model.py:106), plus the fp32 BlockLinear products
-//        (model/modules.py:71-79), batched over the diagonal blocks.
+//        (model/modules.py:71-79), batched over the diagonal blocks; with
+//        GemmArgs::split_wscale set, the same fp32 operands multiply on f16
+//        matrix cores as value plus remainder (v_mfma_f32_16x16x32_f16).
 #pragma once
 
 #include "common.h"

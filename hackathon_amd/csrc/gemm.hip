@@ -27,6 +27,7 @@
 // (deterministic, independent of arrival order), applies the epilogue and
 // resets the counter for the next launch.
 #include <algorithm>
+#include <cmath>
 
 #include "gemm.h"
 
@@ -1005,6 +1006,10 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
   HK_REQUIRE(g.a_period >= 0 && g.a2_from >= 0, "gemm: bad batch-source description");
   HK_REQUIRE(g.M >= 0 && g.N > 0 && g.K > 0 && g.batch > 0, "gemm: bad shape M=%d N=%d K=%d",
              g.M, g.N, g.K);
+  int wexp = 0;
+  HK_REQUIRE(g.split_wscale == 0.0f ||
+                 (std::isfinite(g.split_wscale) && std::frexp(g.split_wscale, &wexp) == 0.5f),
+             "gemm: split_wscale %g is not a positive power of two", (double)g.split_wscale);
   const bool narrow = g.type == GemmType::kF32 && g.K % Tr<GemmType::kF32>::BK != 0;
   const bool half = g.type != GemmType::kF32;  // bf16 or fp16 operands
   const int BK = half     ? Tr<GemmType::kBF16>::BK
