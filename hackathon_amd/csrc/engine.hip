@@ -527,7 +527,8 @@ int build_workspace(Engine& e) {
     for (auto& ev : v) HK_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   }
   {
-    const int st = slstm_persist_pair_fits(d.H, d.nh_s, e.max_runs, e.max_rows, &e.sl_overlap);
+    const int st =
+        slstm_persist_pair_fits(d.H, d.nh_s, e.max_runs, e.max_rows, e.lowp, &e.sl_overlap);
     if (st != HK_OK) return st;
   }
 
@@ -609,18 +610,19 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
 // (or x2 for j >= x2_from) and W[b] = W + b*bs*bs, writing out columns
 // b*bs .. b*bs + bs - 1:
 //   out[:, b*bs + o] = sum_h src[:, k*bs + h] * W[b][o][h].
-// The BlockLinear products of the sLSTM gate inputs and the RG-LRU gates run
-// as split f16 on matrix cores (GemmArgs::split_wscale; `wscale` is the
-// weight slot's split_scale): fp32-level error (each operand as an f16 value
-// plus its f16 remainder), a fifth of the fp32 matrix-core time per product.
-// Their inputs (LayerNorm outputs, silu(conv) and conv outputs of
-// normalised rows) stay far below the f16 range the split needs (65504).
+// In the reduced-precision modes the BlockLinear products of the sLSTM gate
+// inputs and the RG-LRU gates run as split f16 on matrix cores
+// (GemmArgs::split_wscale; `wscale` is the weight slot's split_scale):
+// fp32-level error (each operand as an f16 value plus its f16 remainder), a
+// fifth of the fp32 matrix-core time per product. Their inputs (LayerNorm
+// outputs, silu(conv) and conv outputs of normalised rows) stay far below the
+// f16 range the split needs (65504). The fp32 mode keeps fp32 arithmetic.
 int block_linear(Engine& e, TowerWS& w, const float* x, const float* x2, int x2_from, int64_t ldx,
                  const float* W, float wscale, int products, int blocks, int bs, int M, float* out,
                  int64_t ldo, hipStream_t s) {
   GemmArgs g;
   g.type = GemmType::kF32;
-  g.split_wscale = wscale;
+  g.split_wscale = e.lowp ? wscale : 0.0f;
   g.A = x;
   g.A2 = x2;
   g.a2_from = x2 ? x2_from * blocks : 0;
@@ -765,7 +767,7 @@ int run_xlstm(Engine& e, TowerWS& w, int l, const Group& g, unsigned long long* 
       return slstm_persist(r, g.act_dev, (int)act.size(), w.GIN, H, d.nh_s,
                            F32(e, kXLSTM, l, X_S_ST_W), F32(e, kXLSTM, l, X_S_ST_B), st[XS_S_H],
                            st[XS_S_C], st[XS_S_N], st[XS_S_M], w.SY, xch, tag, e.d_err,
-                           (l == 0 && xch == e.d_xch) ? e.d_trace : nullptr, s);
+                           (l == 0 && xch == e.d_xch) ? e.d_trace : nullptr, e.lowp, s);
     }));
     if (ord.rec) HK_CHECK_HIP(hipEventRecord(ord.rec, s));
   } else {

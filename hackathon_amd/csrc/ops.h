@@ -189,16 +189,19 @@ int slstm_round(const Runs& r, int step, int n_active, const float* gin, int hid
 // also writes h_state. act_dev[t] = runs active at step t. xch: [n_rows]
 // [hidden] 64-bit exchange words; tag: nonzero and different from every
 // earlier launch's on the same buffer; err: set to 1 if a poll timed out.
+// split: the recurrent product on split-f16 matrix cores (head sizes
+// 64-512; the reduced-precision modes), else on fp32 matrix cores.
 bool slstm_persist_supported(int hidden, int heads);
 int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* gin, int hidden,
                   int heads, const float* w_state, const float* b_state, float* h_state,
                   float* c_state, float* n_state, float* m_state, float* y,
                   unsigned long long* xch, unsigned int tag, int* err, uint64_t* trace,
-                  hipStream_t s);
+                  bool split, hipStream_t s);
 // Whether two persistent launches (each at most max_runs runs over
 // max_rounds steps) can be co-resident at once, so that two run groups'
 // recurrences may overlap.
-int slstm_persist_pair_fits(int hidden, int heads, int max_runs, int max_rounds, bool* ok);
+int slstm_persist_pair_fits(int hidden, int heads, int max_runs, int max_rounds, bool split,
+                            bool* ok);
 // After the last round: h_state[slot] = y[last row of the run].
 int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipStream_t s);
 

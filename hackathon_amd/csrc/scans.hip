@@ -419,7 +419,7 @@ __device__ __forceinline__ bool poll_first(const unsigned long long* base, const
   return poll_words<N>(base, offs, tag, err, val);
 }
 
-template <int HS>
+template <int HS, bool SPLIT>
 __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPersistArgs a) {
   extern __shared__ __align__(16) float smem[];
   constexpr int hs = HS;
@@ -428,8 +428,10 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
   constexpr int PAD = hs + 8;       // LDS row stride of h (spreads runs over banks)
   constexpr int KH = hs / 2;        // k per wave
   constexpr int KG = KH / 16;       // groups of 4 MFMA k-steps per wave
-  // head sizes 64-512 multiply on split f16 (hi/lo) matrix cores, 32 on fp32
-  constexpr bool kF16 = HS >= 64;
+  // With SPLIT, head sizes 64-512 multiply on split f16 (hi/lo) matrix
+  // cores; head size 32, and every head size without SPLIT (the fp32 mode),
+  // on fp32 matrix cores.
+  constexpr bool kF16 = SPLIT && HS >= 64;
   constexpr int PADH = PAD;         // f16 row stride of the split h planes
   float* hbuf = smem;                               // [16][PAD] (fp32 path)
   // split-f16 path: the same bytes as two [16][PADH] planes of f16, h*kHScale
@@ -994,7 +996,7 @@ bool slstm_persist_supported(int hidden, int heads) {
 // only for other kernels' work-groups, which never wait on this kernel. (A
 // cooperative launch would also exclude concurrent kernels of the other
 // streams for the whole recurrence.)
-template <int HS>
+template <int HS, bool SPLIT>
 int launch_persist(const SlstmPersistArgs& a, size_t smem, hipStream_t s) {
   const dim3 grid(a.heads * (HS / 16)), block(kPersistThreads);
   // per process (one device type), for the last LDS size asked for
@@ -1009,13 +1011,13 @@ int launch_persist(const SlstmPersistArgs& a, size_t smem, hipStream_t s) {
   if (fits < 0 || smem != fits_smem) {
     int per_cu = 0;
     HK_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, slstm_persist_kernel<HS>, kPersistThreads, smem));
+        &per_cu, slstm_persist_kernel<HS, SPLIT>, kPersistThreads, smem));
     fits = (int64_t)cus * per_cu;
     fits_smem = smem;
   }
   HK_REQUIRE((int64_t)grid.x <= fits, "slstm_persist: %u work-groups cannot be co-resident (%d)",
              grid.x, fits);
-  hipLaunchKernelGGL(slstm_persist_kernel<HS>, grid, block, smem, s, a);
+  hipLaunchKernelGGL((slstm_persist_kernel<HS, SPLIT>), grid, block, smem, s, a);
   HK_LAUNCH_CHECK();
   return HK_OK;
 }
@@ -1029,36 +1031,41 @@ size_t persist_smem(int hs, int n_runs, int n_rounds) {
 // LDS bytes it asks for (see kPersistLdsFloor).
 size_t persist_smem_launch(size_t used) { return std::max(used, kPersistLdsFloor); }
 
-template <int HS>
+template <int HS, bool SPLIT>
 int persist_pair_fits(size_t smem, int heads, bool* ok) {
   int dev = 0, cus = 0, per_cu = 0;
   HK_CHECK_HIP(hipGetDevice(&dev));
   HK_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  HK_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, slstm_persist_kernel<HS>,
-                                                            kPersistThreads, smem));
+  HK_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+      &per_cu, slstm_persist_kernel<HS, SPLIT>, kPersistThreads, smem));
   *ok = 2LL * heads * (HS / 16) <= (int64_t)cus * per_cu;
   return HK_OK;
 }
 
-int slstm_persist_pair_fits(int hidden, int heads, int max_runs, int max_rounds, bool* ok) {
+int slstm_persist_pair_fits(int hidden, int heads, int max_runs, int max_rounds, bool split,
+                            bool* ok) {
   *ok = false;
   if (!slstm_persist_supported(hidden, heads)) return HK_OK;
   const int hs = hidden / heads;
   const size_t smem = persist_smem_launch(persist_smem(hs, max_runs, max_rounds));
+#define HK_FITS(HS)                                                                  \
+  return split ? persist_pair_fits<HS, true>(smem, heads, ok)                       \
+               : persist_pair_fits<HS, false>(smem, heads, ok)
   switch (hs) {
-    case 32: return persist_pair_fits<32>(smem, heads, ok);
-    case 64: return persist_pair_fits<64>(smem, heads, ok);
-    case 128: return persist_pair_fits<128>(smem, heads, ok);
-    case 256: return persist_pair_fits<256>(smem, heads, ok);
-    default: return persist_pair_fits<512>(smem, heads, ok);
+    case 32: HK_FITS(32);
+    case 64: HK_FITS(64);
+    case 128: HK_FITS(128);
+    case 256: HK_FITS(256);
+    default: HK_FITS(512);
   }
+#undef HK_FITS
 }
 
 int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* gin, int hidden,
                   int heads, const float* w_state, const float* b_state, float* h_state,
                   float* c_state, float* n_state, float* m_state, float* y,
                   unsigned long long* xch, unsigned int tag, int* err, uint64_t* trace,
-                  hipStream_t s) {
+                  bool split, hipStream_t s) {
   if (r.n_runs == 0 || n_rounds == 0) return HK_OK;
   HK_REQUIRE(slstm_persist_supported(hidden, heads), "slstm_persist: head size unsupported");
   HK_REQUIRE(tag != 0 && xch != nullptr, "slstm_persist: exchange buffer and nonzero tag needed");
@@ -1075,13 +1082,16 @@ int slstm_persist(const Runs& r, const int* act_dev, int n_rounds, const float* 
     smem += (size_t)n_rounds * 8 * sizeof(uint64_t);
   }
   smem = persist_smem_launch(smem);
+#define HK_LAUNCH(HS) \
+  return split ? launch_persist<HS, true>(a, smem, s) : launch_persist<HS, false>(a, smem, s)
   switch (hs) {
-    case 32: return launch_persist<32>(a, smem, s);
-    case 64: return launch_persist<64>(a, smem, s);
-    case 128: return launch_persist<128>(a, smem, s);
-    case 256: return launch_persist<256>(a, smem, s);
-    default: return launch_persist<512>(a, smem, s);
+    case 32: HK_LAUNCH(32);
+    case 64: HK_LAUNCH(64);
+    case 128: HK_LAUNCH(128);
+    case 256: HK_LAUNCH(256);
+    default: HK_LAUNCH(512);
   }
+#undef HK_LAUNCH
 }
 
 int slstm_final(const Runs& r, const float* y, int hidden, float* h_state, hipStream_t s) {

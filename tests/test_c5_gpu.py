@@ -14,6 +14,9 @@ uniform symbol ids, features N(0, 1).
   bit-identical (their initial values).
 - Determinism: the last tick replayed from its imported start state gives
   bit-identical predictions and state for its slots.
+- hipGraph replay for ticks of at most 64 requests, as the configuration
+  asks: every third tick has B ~ U(1..64) and replays a captured graph, so
+  the parity sample above covers replayed ticks too.
 """
 
 import numpy as np
@@ -31,8 +34,8 @@ CFG = spec.ModelConfig(hidden_size=512, proj_size=1024, tower_depth=12, num_head
 S, BMAX = 8192, 512
 
 
-def _tick(rng):
-    B = int(rng.integers(1, BMAX + 1))
+def _tick(rng, bmax=BMAX):
+    B = int(rng.integers(1, bmax + 1))
     ids = rng.integers(0, S, size=B)
     uniq, first, counts = np.unique(ids, return_index=True, return_counts=True)
     order = np.argsort(first, kind="stable")
@@ -54,12 +57,16 @@ def test_c5_reduced_width_8192_symbols(dev):
     params = weights.generate(CFG, 0)
     eng = Engine(CFG, capacity=S, max_rows=BMAX, max_runs=BMAX, linear_dtype="bf16", device=dev)
     eng.load_weights(params)
+    eng.graphs(max_rows=64)
     rng = np.random.default_rng(3)
     frng = np.random.default_rng(1)
-    ticks = [_tick(rng) for _ in range(12)]
+    ticks = [_tick(rng, 64 if j % 3 == 2 else BMAX) for j in range(12)]
+    n_small = sum(int(c.sum()) <= 64 for _, c in ticks)
     touched = np.unique(np.concatenate([t[0] for t in ticks]))
     seen_twice = [s for s in touched if sum(int(s in t[0]) for t in ticks) >= 2]
-    sample = [int(s) for s in (seen_twice[:3] + [int(touched[len(touched) // 2])])]
+    small = [int(s) for j, (syms_j, _) in enumerate(ticks) if j % 3 == 2 for s in syms_j]
+    sample = [int(s) for s in seen_twice[:3]]
+    sample += [next(s for s in small if s not in sample)]  # advanced by a replayed graph
     untouched = np.setdiff1d(np.arange(S), touched)
     idle = rng.choice(untouched, size=16, replace=False)
     idle_before = _rows(eng, idle)
@@ -80,6 +87,7 @@ def test_c5_reduced_width_8192_symbols(dev):
                 hist[s].extend(x[a:b])
                 got[s].extend(preds[a:b].cpu().numpy())
     eng.check()
+    assert eng.graph_info()["replays"] == n_small >= 4
     after = _rows(eng, syms)
     # determinism: the last tick again from its start state
     for s, tree in zip(syms, start):

@@ -8,10 +8,12 @@ torch on the GPU (rocBLAS GEMMs, no TF32) land up to 9e-5 (xLSTM), 1.6e-4
 (Mamba2), 1.2e-3 (RetNet) and 3.8e-3 (Hawk) relative from the float64
 result, and from each other. The engine is held to the same yardstick: per
 tower, its largest relative distance from the float64 reference over every
-prediction of the test must be within 4x the largest distance of those two
+prediction of the test must be within 2x the largest distance of those two
 reference fp32 runs (relative distances |d| / max(|exact|, 0.01)). State
-leaves: norm-wise relative distance from the float64 state within 4x that of
-the reference's fp32 runs (+1e-7).
+leaves: norm-wise relative distance from the float64 state within 2x that of
+the reference's fp32 runs (+1e-7). The float64 reference is the oracle in
+float64, itself pinned to the reference's own float64 run
+(tests/test_oracle_model.py).
 
 Reduced-precision bars (CastLinear, bf16 and fp16, example_model.py:68-148):
 over a test's predictions, the engine's mean squared distance from the
@@ -34,7 +36,7 @@ from refrun import leaf_rel, reference_rounds, rel_err, to_device, zipf_tick
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
-SCATTER_FACTOR = 4.0
+SCATTER_FACTOR = 2.0
 TOWERS = ("xlstm", "mamba2", "retnet", "hawk")
 
 
@@ -47,8 +49,9 @@ def _check_fp32_towers(got, ref64, refs32, what):
     """got, ref64: [n, 4]; refs32: the reference's own fp32 runs, each [n, 4]."""
     e = rel_err(got, ref64).max(0)
     s = np.max([rel_err(r, ref64).max(0) for r in refs32], axis=0)
-    print(f"{what}: engine max rel err per tower {np.array2string(e, precision=2)}, "
-          f"reference fp32 runs {np.array2string(s, precision=2)}")
+    fmt = lambda v, f: "[" + " ".join(f % x for x in v) + "]"
+    print(f"{what}: engine max rel err per tower {fmt(e, '%.3e')}, "
+          f"reference fp32 runs {fmt(s, '%.3e')}, ratio {fmt(e / s, '%.2f')}")
     for t in range(4):
         assert e[t] <= SCATTER_FACTOR * s[t], (
             f"{what}: {TOWERS[t]} engine {e[t]:.3e} > {SCATTER_FACTOR} x reference fp32 "
@@ -130,17 +133,77 @@ def test_default_dims_fp32_long_runs_and_logs(dev, params):
     del P64
     cat = lambda v: np.concatenate([np.asarray(a) for a in v])
     _check_fp32_towers(cat(got), cat(p64), [cat(p32), cat(pg)], "long runs")
+    _check_fp32_leaves(state, s64, [s32, sg], "long runs")
+
+
+def _check_fp32_leaves(state, s64, refs32, what):
+    """Every state leaf: the engine's norm-wise distance from the float64
+    state within SCATTER_FACTOR x the larger of the reference fp32 runs'."""
     worst = 0.0
-    for i, (g, a, b, e) in enumerate(zip(om.flatten(state), om.flatten(s32), om.flatten(sg),
-                                         om.flatten(s64))):
+    for i, leaves in enumerate(zip(om.flatten(state), om.flatten(s64),
+                                   *[om.flatten(r) for r in refs32])):
+        g, e, rs = leaves[0], leaves[1], leaves[2:]
         if e.dtype == torch.int32:
-            assert torch.equal(g.cpu(), e), f"leaf {i}: offsets differ"
+            assert torch.equal(g.cpu(), e), f"{what}: leaf {i}: offsets differ"
             continue
-        rg, ra, rb = leaf_rel(g, e), leaf_rel(a, e), leaf_rel(b, e)
-        worst = max(worst, rg / (max(ra, rb) + 1e-7))
-        assert rg <= SCATTER_FACTOR * max(ra, rb) + 1e-7, (
-            f"state leaf {i} {tuple(e.shape)}: engine {rg:.3e}, reference fp32 {ra:.3e} / {rb:.3e}")
-    print(f"state leaves: worst engine / reference-scatter ratio {worst:.2f}")
+        rg = leaf_rel(g, e)
+        ra = max(leaf_rel(r, e) for r in rs)
+        worst = max(worst, rg / (ra + 1e-7))
+        assert rg <= SCATTER_FACTOR * ra + 1e-7, (
+            f"{what}: state leaf {i} {tuple(e.shape)}: engine {rg:.3e}, reference fp32 {ra:.3e}")
+    print(f"{what}: state leaves, worst engine / reference-scatter ratio {worst:.2f}")
+
+
+def test_c1_fp32_256_steps(dev, params):
+    """C1 at its full length: 4 symbols x 256 single-request steps at the
+    default dims in fp32 (features N(0,1) clipped to +-5, seed 1), through
+    NnInferenceClient.process_batch, one request per symbol per batch (256
+    batches). The oracle in float64 on this GPU is the exact answer; the
+    reference's own two fp32 evaluations at the same length (the oracle on
+    the host's cores, in a worker thread beside the GPU legs, and in torch on
+    this GPU) give the scatter. Per tower, every prediction within 2x it;
+    every state leaf after the 256 steps likewise."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from hackathon_amd.client import NnInferenceClient, PendingRequest
+    from hackathon_amd.engine import Engine
+
+    cfg = spec.DEFAULT
+    B, steps = 4, 256
+    rng = np.random.default_rng(1)
+    x = np.clip(rng.standard_normal((steps, B, cfg.num_features), dtype=np.float32), -5, 5)
+    hist = [[x[t, i] for t in range(steps)] for i in range(B)]
+    with ThreadPoolExecutor(1) as pool:
+        # torch's CPU kernels release the GIL: the host run overlaps the GPU legs
+        cpu = pool.submit(reference_rounds, om.Params(params), cfg, hist)
+        eng = Engine(cfg, capacity=B, max_rows=16, linear_dtype="fp32", device=dev)
+        eng.load_weights(params)
+        client = NnInferenceClient(B, engine=eng)
+        got = np.zeros((B, steps, 4))
+        for t in range(steps):
+            reqs = {f"S{i}": [PendingRequest(t * B + i, f"S{i}", x[t, i].tolist())]
+                    for i in range(B)}
+            resp = client.process_batch(reqs)
+            assert resp.unique_ids == [t * B + i for i in range(B)]
+            got[:, t] = np.asarray(resp.predictions)
+        eng.check()
+        assert [client.symbol_to_idx[f"S{i}"] for i in range(B)] == list(range(B))
+        state = eng.export_state(0, B)
+        eng.close()
+        del eng, client
+        torch.cuda.empty_cache()
+        PG = om.Params({k: v.to(dev) for k, v in params.items()})
+        pg, sg = reference_rounds(PG, cfg, hist, device=dev)
+        del PG
+        torch.cuda.empty_cache()
+        P64 = om.Params({k: v.to(dev) for k, v in params.items()}, dtype=torch.float64)
+        p64, s64 = reference_rounds(P64, cfg, hist, device=dev)
+        del P64
+        torch.cuda.empty_cache()
+        p32, s32 = cpu.result()
+    cat = lambda v: np.concatenate([np.asarray(a) for a in v])
+    _check_fp32_towers(cat(got), cat(p64), [cat(p32), cat(pg)], "C1 256 steps")
+    _check_fp32_leaves(state, s64, [s32, sg], "C1 256 steps")
 
 
 def _lp_check(got, ref_lp, ref32, what):

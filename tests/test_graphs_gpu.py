@@ -7,7 +7,15 @@ two executables are both replayed several times, one-row ticks, ticks with
 runs long enough for the two xLSTM run groups, ticks above the replay limit
 run eagerly in between, a tick shape evicted from a full cache and captured
 again). Predictions of every tick and the final state of every leaf must be
-bit-identical; the cache counters must show the captures and replays."""
+bit-identical; the cache counters must show the captures and replays.
+
+The replayed ticks are also checked against the oracle: every slot's
+request history is replayed through the reference's rounds (symbols are
+independent, so a slot's predictions depend on its own history alone), in
+fp32 at the mid-width fp32 bar (|d| <= 1e-5 + 1e-5 |ref|), and with the
+reference's bf16 CastLinear at the reduced-precision bar (the engine's mean
+squared distance from the reference's bf16 result at most a tenth of that
+result's distance from fp32)."""
 
 import numpy as np
 import pytest
@@ -15,6 +23,7 @@ import torch
 
 from hackathon_amd import spec, weights
 from oracle import model as om
+from refrun import reference_rounds
 
 pytestmark = pytest.mark.gpu
 
@@ -43,17 +52,24 @@ def test_graph_replay_matches_eager(dev, lp):
     ]
     rng = np.random.default_rng(0)
     n_small = 0
+    hist = [[] for _ in range(32)]
+    got = [[] for _ in range(32)]
     for b, counts in enumerate(shapes):
         counts = np.asarray(counts)
         slots = rng.permutation(32)[: len(counts)].astype(np.int32)
-        runs, _ = pack_runs(slots, counts)
+        runs, order = pack_runs(slots, counts)
         n_small += runs.n_rows <= 32
-        x = torch.from_numpy(np.clip(rng.standard_normal((runs.n_rows, MID.num_features)),
-                                     -5, 5).astype(np.float32)).to(dev)
+        xh = np.clip(rng.standard_normal((runs.n_rows, MID.num_features)), -5, 5).astype(np.float32)
+        x = torch.from_numpy(xh).to(dev)
         p_e = eager.tick(runs, x).cpu()
         p_g = graph.tick(runs, x).cpu()
         assert torch.isfinite(p_e).all()
         assert torch.equal(p_e, p_g), f"tick {b} {counts.tolist()}: predictions differ"
+        for pos in range(len(order)):
+            a, e = int(runs.run_off[pos]), int(runs.run_off[pos + 1])
+            s = int(runs.slot_ids[pos])
+            hist[s].extend(xh[a:e])
+            got[s].extend(p_g[a:e].double().numpy())
     eager.check()
     graph.check()
     info = graph.graph_info()
@@ -66,3 +82,20 @@ def test_graph_replay_matches_eager(dev, lp):
     assert graph.graph_info()["cached"] == 0
     for e in engines:
         e.close()
+
+    used = [s for s in range(32) if hist[s]]
+    histories = [hist[s] for s in used]
+    cat = lambda v: np.concatenate([np.asarray(a, np.float64) for a in v])
+    g = cat([got[s] for s in used])
+    p32 = cat(reference_rounds(om.Params(params), MID, histories)[0])
+    if lp == "fp32":
+        err = np.abs(g - p32) - (1e-5 + 1e-5 * np.abs(p32))
+        print(f"graph replay vs oracle fp32: max |d| {np.abs(g - p32).max():.3e}")
+        assert err.max() <= 0, f"replayed ticks vs the oracle: max |d| {np.abs(g - p32).max():.3e}"
+    else:
+        plp = cat(reference_rounds(om.Params(params, lp=lp), MID, histories)[0])
+        e_lp = float(((g - plp) ** 2).mean())
+        r_32 = float(((plp - p32) ** 2).mean())
+        print(f"graph replay vs oracle {lp}: MSE engine-vs-reference-{lp} {e_lp:.3e}, "
+              f"reference-{lp}-vs-fp32 {r_32:.3e}, ratio {e_lp / r_32:.3e}")
+        assert e_lp <= 0.1 * r_32

@@ -85,6 +85,26 @@ def test_default_dims_predictions():
             torch.testing.assert_close(preds, _t(fx[f"preds/{t}"]), rtol=1e-4, atol=1e-5)
 
 
+def test_default_dims_float64_predictions():
+    """The oracle in float64 (Params(dtype=torch.float64)), the yardstick the
+    GPU fp32 parity tests measure distances from, against the reference's own
+    float64 run of the same model and inputs (default.npz preds64: the
+    seed-0 fp32 weights and the features converted to float64). Two float64
+    evaluations of one algorithm agree to far below the fp32 scatter being
+    judged (1e-4 to 4e-3 relative at these dims); a transposed operand, a
+    wrong eps or a dropped term would not."""
+    fx = np.load(GOLDEN / "default.npz")
+    cfg = spec.DEFAULT
+    P = om.Params(weights.generate(cfg, 0), dtype=torch.float64)
+    state = om.init_state(cfg, 4, torch.float64)
+    with torch.inference_mode():
+        for t in range(4):
+            x = _t(fx[f"x/{t}"]).double()
+            preds, state = om.forward(P, cfg, x, state)
+            assert preds.dtype == torch.float64
+            torch.testing.assert_close(preds, _t(fx[f"preds64/{t}"]), rtol=1e-9, atol=1e-12)
+
+
 def test_causal_conv_matches_explicit_taps():
     g = torch.Generator().manual_seed(0)
     B, C = 3, 5
