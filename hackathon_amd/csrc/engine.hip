@@ -1488,6 +1488,45 @@ int hk_engine_reset_slots(void* h, const int* slots_host, int n, void* stream) {
   return HK_OK;
 }
 
+// Appends counts_host[i] zero-valued pending-update entries to every
+// matrix-state log of slot slots_host[i] (up to the log capacity): the state
+// the slots stand for is unchanged, while the next ticks read and write the
+// log as they would after a long run of ticks. Synchronous.
+int hk_engine_log_fill(void* h, const int* slots_host, const int* counts_host, int n,
+                       void* stream) {
+  HK_REQUIRE(h, "hk_engine_log_fill: null handle");
+  Engine& e = *static_cast<Engine*>(h);
+  HK_REQUIRE(n >= 0 && (n == 0 || (slots_host && counts_host)), "hk_engine_log_fill: bad arguments");
+  if (n == 0) return HK_OK;
+  for (int i = 0; i < n; ++i) {
+    HK_REQUIRE(slots_host[i] >= 0 && slots_host[i] < e.capacity,
+               "hk_engine_log_fill: slot %d out of range", slots_host[i]);
+    HK_REQUIRE(counts_host[i] >= 0, "hk_engine_log_fill: negative count");
+  }
+  hipStream_t s = (hipStream_t)stream;
+  int* buf = nullptr;
+  HK_CHECK_HIP(hipMalloc(&buf, 2 * sizeof(int) * (size_t)n));
+  int st = HK_OK;
+  if (hipMemcpyAsync(buf, slots_host, sizeof(int) * n, hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipMemcpyAsync(buf + n, counts_host, sizeof(int) * n, hipMemcpyHostToDevice, s) !=
+          hipSuccess) {
+    hk::set_error("hk_engine_log_fill: copy failed");
+    st = HK_ERR_HIP;
+  }
+  for (int t = 0; t < hk::kTowers && st == HK_OK; ++t) {
+    if (hk::matrix_leaf(t) < 0) continue;
+    for (int l = 0; l < e.d.D && st == HK_OK; ++l)
+      st = hk::mat_log_fill(hk::mat_state_desc(e, t, l), buf, buf + n, n, s);
+  }
+  // the copies read host memory and the kernels read buf: wait before both go
+  if (hipStreamSynchronize(s) != hipSuccess && st == HK_OK) {
+    hk::set_error("hk_engine_log_fill: %s", hipGetErrorString(hipGetLastError()));
+    st = HK_ERR_HIP;
+  }
+  HK_CHECK_HIP(hipFree(buf));
+  return st;
+}
+
 // Waits for the work enqueued on `stream` so far (a tick ends with every side
 // stream joined back into its stream, so waiting for the tick's stream waits
 // for the whole tick; nothing else on the device is waited for) and reports a

@@ -135,5 +135,9 @@ int mat_log_flush(const MatScanDesc& d, int slot0, int n, hipStream_t stream);
 // (a device list) or, with slots_dev null, slot0 + i.
 int mat_log_clear(const MatScanDesc& d, const int* slots_dev, int slot0, int n,
                   hipStream_t stream);
+// Appends counts_dev[i] zero-valued entries to the logs of slot slots_dev[i]
+// (each head; at most up to the capacity): the leaf's value is unchanged.
+int mat_log_fill(const MatScanDesc& d, const int* slots_dev, const int* counts_dev, int n,
+                 hipStream_t stream);
 
 }  // namespace hk

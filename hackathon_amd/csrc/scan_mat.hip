@@ -389,7 +389,45 @@ __global__ void mat_log_clear_kernel(float* hdr, int heads, const int* slots, in
   h[1] = 1.0f;
 }
 
+// Appends counts[k] zero-valued entries (row and column vectors zero,
+// coefficient 1) to the logs of slot slots[k], up to the capacity: the
+// leaf's value F*B + sum_j a_j b_j g_j^T is unchanged. One thread per
+// (slot, head).
+__global__ void mat_log_fill_kernel(float* hdr, float* lb, float* lg, int heads, int cap,
+                                    int rows, int cols, const int* slots, const int* counts,
+                                    int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * heads) return;
+  const int k = i / heads;
+  const int64_t sh = (int64_t)slots[k] * heads + (i - k * heads);
+  float* h = hdr + sh * kLogHdr;
+  const int have = (int)h[0];
+  const int add = min(counts[k], cap - have);
+  if (add <= 0) return;
+  for (int j = have; j < have + add; ++j) {
+    h[2 + j] = 1.0f;
+    float* b = lb + (sh * cap + j) * rows;
+    for (int r = 0; r < rows; ++r) b[r] = 0.0f;
+    float* g = lg + (sh * cap + j) * cols;
+    for (int c = 0; c < cols; ++c) g[c] = 0.0f;
+  }
+  h[0] = (float)(have + add);
+}
+
 }  // namespace
+
+int mat_log_fill(const MatScanDesc& d, const int* slots_dev, const int* counts_dev, int n,
+                 hipStream_t stream) {
+  if (d.log_cap == 0 || n == 0) return HK_OK;
+  HK_REQUIRE(n > 0 && d.log_hdr && d.log_b && d.log_g && slots_dev && counts_dev,
+             "mat_log_fill: bad arguments");
+  const int total = n * d.heads;
+  hipLaunchKernelGGL(mat_log_fill_kernel, dim3((total + 255) / 256), dim3(256), 0, stream,
+                     d.log_hdr, d.log_b, d.log_g, d.heads, d.log_cap, d.rows, d.cols, slots_dev,
+                     counts_dev, n);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
 
 LogCommit log_commit_of(const MatScanDesc& d) {
   LogCommit c;

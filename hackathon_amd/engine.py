@@ -34,6 +34,7 @@ _lib.register(
     "hk_engine_state_copy", c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p]
 )
 _lib.register("hk_engine_reset_slots", c_int, [c_void_p, c_void_p, c_int, c_void_p])
+_lib.register("hk_engine_log_fill", c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p])
 _lib.register("hk_engine_tick", c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p])
 
 _lib.register("hk_engine_check", c_int, [c_void_p, c_void_p])
@@ -259,6 +260,19 @@ class Engine:
                 arr = np.ascontiguousarray(np.asarray(slots, dtype=np.int32))
                 st = _lib.lib().hk_engine_reset_slots(self._h, arr.ctypes.data, len(arr), self._stream())
         _lib.check(st, "hk_engine_reset_slots")
+
+    def log_fill(self, slots, counts):
+        """Append counts[i] zero-valued pending-update entries to every
+        write-back log of slot slots[i] (up to the capacity of 8): the state
+        is unchanged, and later ticks find the logs as full as after a long
+        run (a benchmark starts at steady state with it)."""
+        sl = np.ascontiguousarray(np.asarray(slots, dtype=np.int32))
+        ct = np.ascontiguousarray(np.asarray(counts, dtype=np.int32))
+        assert sl.shape == ct.shape and sl.ndim == 1
+        with torch.cuda.device(self.device):
+            st = _lib.lib().hk_engine_log_fill(self._h, sl.ctypes.data, ct.ctypes.data, len(sl),
+                                              self._stream())
+        _lib.check(st, "hk_engine_log_fill")
 
     def _leaf_numel(self, tower: int, leaf: int) -> int:
         n = c_int64()

@@ -236,6 +236,16 @@ int hk_engine_state_copy(void* handle, int tower, int layer, int leaf, int slot0
  * model/xlstm.py:375); n < 0 resets every slot. */
 int hk_engine_reset_slots(void* handle, const int* slots_host, int n, void* stream);
 
+/* Appends counts_host[i] zero-valued entries to every pending-update log
+ * (matrix-state write-back log, each layer and head) of slot slots_host[i],
+ * up to the log capacity (8): the state the slots stand for is unchanged,
+ * while later ticks read and write the logs as they do in a long-running
+ * store. Measurement support with no reference counterpart (the reference
+ * writes every state back each round): it starts a benchmark window at the
+ * log occupancy a long run reaches. Synchronous. */
+int hk_engine_log_fill(void* handle, const int* slots_host, const int* counts_host, int n,
+                       void* stream);
+
 /* One tick: n_runs runs, run i = slot slot_ids_host[i] advanced over request
  * rows run_off_host[i] .. run_off_host[i+1]-1 in order; runs sorted by
  * non-increasing length, slots distinct. features_dev [n_rows, features]

@@ -14,10 +14,21 @@ import torch
 from . import model as om
 
 
+def _to(tree, device):
+    if isinstance(tree, (list, tuple)):
+        out = [_to(t, device) for t in tree]
+        return tuple(out) if isinstance(tree, tuple) else out
+    return tree.to(device)
+
+
 class OracleClient:
-    def __init__(self, P: om.Params, cfg, capacity: int):
+    """`device`: where the state and each round's inputs live (the params
+    `P` must be there too); "cpu" by default."""
+
+    def __init__(self, P: om.Params, cfg, capacity: int, device="cpu"):
         self.P, self.cfg, self.capacity = P, cfg, capacity
-        self.state = om.init_state(cfg, capacity, P.dtype)
+        self.device = torch.device(device)
+        self.state = _to(om.init_state(cfg, capacity, P.dtype), self.device)
         self.symbol_to_idx = {}
 
     def _row_for(self, symbol):
@@ -57,10 +68,12 @@ class OracleClient:
             x[idx] = torch.as_tensor(np.asarray(feats), dtype=self.P.dtype)
             mask = torch.zeros(self.capacity, dtype=torch.bool)
             mask[idx] = True
-            out, self.state = om.forward(self.P, self.cfg, x, self.state, mask)
+            out, self.state = om.forward(self.P, self.cfg, x.to(self.device), self.state,
+                                         mask.to(self.device))
+            out = out.to(torch.float64).cpu()
             for r, row in zip(batch, idx):
                 ids.append(r.unique_id)
-                preds.append(out[row].to(torch.float64).tolist())
+                preds.append(out[row].tolist())
         return ids, preds
 
 

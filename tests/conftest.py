@@ -24,6 +24,15 @@ def gpu_available() -> bool:
 
 
 @pytest.fixture(scope="session")
+def default_params():
+    """The default-dims weights (init spec, seed 0; 2 B values, 8 GB on the
+    host), generated once per session for every test that needs them."""
+    from hackathon_amd import spec, weights
+
+    return weights.generate(spec.DEFAULT, 0)
+
+
+@pytest.fixture(scope="session")
 def dev():
     import torch
 

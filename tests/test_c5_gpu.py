@@ -7,9 +7,9 @@ uniform symbol ids, features N(0, 1).
 - Parity: four symbols that the ticks touch are replayed on the oracle from
   their own histories (symbols are independent), in fp32 and with the
   reference's bf16 CastLinear: over their predictions the engine's mean
-  squared distance from the reference's bf16 result is at most that
-  result's distance from fp32, and its distance from fp32 at most twice the
-  reference's own.
+  squared distance from the reference's bf16 result is at most 3% of that
+  result's distance from fp32 (r_32), and its distance from fp32 at most
+  r_32 (measured 1.95% and 0.84).
 - Idle slots: a sample of slots the ticks never touch keeps every state leaf
   bit-identical (their initial values).
 - Determinism: the last tick replayed from its imported start state gives
@@ -112,6 +112,8 @@ def test_c5_reduced_width_8192_symbols(dev):
     e_32 = float(((g_ - r32) ** 2).mean())
     r_32 = float(((r_lp - r32) ** 2).mean())
     print(f"C5 sample {sample} ({[len(h) for h in histories]} requests): MSE engine-vs-bf16-ref "
-          f"{e_lp:.3e}, engine-vs-fp32 {e_32:.3e}, bf16-ref-vs-fp32 {r_32:.3e}")
-    assert e_lp <= r_32
-    assert e_32 <= 2.0 * r_32
+          f"{e_lp:.3e}, engine-vs-fp32 {e_32:.3e}, bf16-ref-vs-fp32 {r_32:.3e}; "
+          f"e_lp/r_32 {e_lp / r_32:.4f}, e_32/r_32 {e_32 / r_32:.4f}")
+    # measured e_lp/r_32 0.0195, e_32/r_32 0.844
+    assert e_lp <= 0.03 * r_32
+    assert e_32 <= 1.0 * r_32

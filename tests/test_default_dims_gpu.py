@@ -15,13 +15,18 @@ the reference's fp32 runs (+1e-7). The float64 reference is the oracle in
 float64, itself pinned to the reference's own float64 run
 (tests/test_oracle_model.py).
 
-Reduced-precision bars (CastLinear, bf16 and fp16, example_model.py:68-148):
-over a test's predictions, the engine's mean squared distance from the
-reference's own reduced-precision result is at most that result's mean
-squared distance from the fp32 reference (the engine reproduces the
-reference's rounding, not just fp32 within the mode's error), and the
-engine's mean squared distance from the fp32 reference is at most twice the
-reference's own.
+Reduced-precision bars (CastLinear, bf16 and fp16, example_model.py:68-148),
+over a test's predictions, in units of r_32 = the mean squared distance of
+the reference's own reduced-precision result from its fp32 result: the
+engine's distance from the reference's reduced-precision result (e_lp) and
+from its fp32 result (e_32), each held just above what it measures on these
+fixed inputs. Two 16-bit evaluations of the model round their GEMM outputs
+apart now and then (a one-ulp flip is 0.4% in bf16), and the recurrences
+carry each flip forward, so e_lp grows with a symbol's history: measured
+e_lp/r_32 = 0.005 (bf16) and 0.032 (fp16) over 2 steps, 0.39 over the
+headline configuration's 8 ticks (symbols with up to 370 requests); in the
+limit of long histories it tends to 2 (two independent 16-bit errors), while
+e_32/r_32 stays near 1 (measured 0.91, 1.29, 1.13).
 """
 
 from pathlib import Path
@@ -41,8 +46,8 @@ TOWERS = ("xlstm", "mamba2", "retnet", "hawk")
 
 
 @pytest.fixture(scope="module")
-def params():
-    return weights.generate(spec.DEFAULT, 0)
+def params(default_params):
+    return default_params
 
 
 def _check_fp32_towers(got, ref64, refs32, what):
@@ -206,15 +211,22 @@ def test_c1_fp32_256_steps(dev, params):
     _check_fp32_leaves(state, s64, [s32, sg], "C1 256 steps")
 
 
-def _lp_check(got, ref_lp, ref32, what):
+def _lp_check(got, ref_lp, ref32, what, max_lp=1.0, max_32=2.0):
+    """Mean squared distances: engine from the reference's reduced-precision
+    result (e_lp) and from its fp32 result (e_32), against the reference's
+    own reduced-precision error r_32; e_lp <= max_lp * r_32 and e_32 <=
+    max_32 * r_32."""
     got, ref_lp, ref32 = (np.asarray(a, np.float64) for a in (got, ref_lp, ref32))
     e_lp = float(((got - ref_lp) ** 2).mean())
     e_32 = float(((got - ref32) ** 2).mean())
     r_32 = float(((ref_lp - ref32) ** 2).mean())
     print(f"{what}: MSE engine-vs-reference-lp {e_lp:.3e}, engine-vs-fp32 {e_32:.3e}, "
-          f"reference-lp-vs-fp32 {r_32:.3e}, signal {float((ref32 ** 2).mean()):.3e}")
-    assert e_lp <= r_32, f"{what}: engine is farther from the reference's {what} than it is from fp32"
-    assert e_32 <= 2.0 * r_32, f"{what}: engine's error vs fp32 above twice the reference's own"
+          f"reference-lp-vs-fp32 {r_32:.3e}, signal {float((ref32 ** 2).mean()):.3e}; "
+          f"e_lp/r_32 {e_lp / r_32:.4f}, e_32/r_32 {e_32 / r_32:.4f}")
+    assert e_lp <= max_lp * r_32, (
+        f"{what}: engine-vs-reference-lp MSE {e_lp:.3e} above {max_lp} x {r_32:.3e}")
+    assert e_32 <= max_32 * r_32, (
+        f"{what}: engine-vs-fp32 MSE {e_32:.3e} above {max_32} x {r_32:.3e}")
     return e_lp, e_32, r_32
 
 
@@ -234,31 +246,40 @@ def test_default_dims_castlinear_golden(dev, params, lp):
         got.append(p.cpu().numpy())
     model.engine.check()
     model.close()
+    # measured e_lp/r_32, e_32/r_32: bf16 0.0051, 0.905; fp16 0.0317, 1.29
+    max_lp, max_32 = {"bf16": (0.01, 1.0), "fp16": (0.05, 1.5)}[lp]
     _lp_check(np.concatenate(got), np.concatenate([fx[f"{lp}/preds/{t}"] for t in range(2)]),
-              np.concatenate([f32[f"preds/{t}"] for t in range(2)]), lp)
+              np.concatenate([f32[f"preds/{t}"] for t in range(2)]), lp, max_lp, max_32)
 
 
 def test_c4_bf16_zipf_ticks_sampled_symbols(dev, params):
-    """The headline configuration's tick shape at the default dims in bf16:
-    128 resident symbols, ticks of 256 Zipf(1.1) requests (runs of 50+
-    requests: two xLSTM run groups, row-split scans, long persistent sLSTM
-    launches). Four symbols of different request rates are replayed on the
-    oracle from their own histories (symbols are independent), in fp32 and
-    with the reference's bf16 CastLinear; the reduced-precision bars apply
-    to their predictions."""
+    """The headline configuration at the default dims in bf16: 1024
+    resident symbols (157 GB of state), eight ticks of 256 Zipf(1.1)
+    requests (runs of 50+ requests: two xLSTM run groups, row-split scans,
+    long persistent sLSTM launches; the write-back logs fill and are written
+    back). Five symbols are replayed on the oracle from their own histories
+    (symbols are independent), in fp32 and with the reference's bf16
+    CastLinear, on this GPU: four of different request rates and one whose
+    slot is 512 or above (its mLSTM tiles sit past 4 GiB into their leaves).
+    The reduced-precision bars apply to their predictions."""
     from hackathon_amd.engine import Engine, pack_runs
 
     cfg = spec.DEFAULT
-    S = 128
+    S = 1024
     eng = Engine(cfg, capacity=S, max_rows=256, max_runs=256, linear_dtype="bf16", device=dev)
     eng.load_weights(params)
     rng = np.random.default_rng(2)
-    ticks = [zipf_tick(rng, S, 256) for _ in range(2)]
+    ticks = [zipf_tick(rng, S, 256) for _ in range(8)]
     tot = np.zeros(S, np.int64)
+    seen = np.zeros(S, np.int64)
     for syms, counts in ticks:
         tot[syms] += counts
+        seen[syms] += 1
     by_rate = np.argsort(-tot, kind="stable")
     sample = [int(by_rate[r]) for r in (3, 11, 40, 90) if tot[by_rate[r]] > 0]
+    far = [s for s in np.flatnonzero(seen >= 2) if s >= 512]
+    assert far, "no symbol of slot 512 or above seen twice"
+    sample.append(int(far[0]))
     hist = {s: [] for s in sample}
     got = {s: [] for s in sample}
     max_run = 0
@@ -278,9 +299,14 @@ def test_c4_bf16_zipf_ticks_sampled_symbols(dev, params):
     torch.cuda.empty_cache()
     assert max_run >= 16
     histories = [hist[s] for s in sample]
-    p32, _ = reference_rounds(om.Params(params), cfg, histories)
-    plp, _ = reference_rounds(om.Params(params, lp="bf16"), cfg, histories)
+    pd = {k: v.to(dev) for k, v in params.items()}
+    p32, _ = reference_rounds(om.Params(pd), cfg, histories, device=dev)
+    torch.cuda.empty_cache()
+    plp, _ = reference_rounds(om.Params(pd, lp="bf16"), cfg, histories, device=dev)
+    del pd
+    torch.cuda.empty_cache()
     cat = lambda v: np.concatenate([np.asarray(a) for a in v])
     print(f"C4 sample: symbols {sample} with {[len(h) for h in histories]} requests, "
           f"longest run in the ticks {max_run}")
-    _lp_check(cat([got[s] for s in sample]), cat(plp), cat(p32), "bf16")
+    # measured e_lp/r_32 0.389, e_32/r_32 1.13
+    _lp_check(cat([got[s] for s in sample]), cat(plp), cat(p32), "bf16", 0.5, 1.25)

@@ -7,12 +7,13 @@ The weights are the init spec (the trained checkpoint is not available
 offline), so the errors against the parquet's targets are not the
 reference's published ones; what is checked is that the engine answers every
 request in the reference's order with the reference algorithm's predictions
-and that the metrics follow. Bars (relative, floor 0.01): 5e-3 for the
-xLSTM, Mamba2 and Hawk towers; 5e-2 for RetNet, whose per-head RMSNorm of
-near-cancelling contractions amplifies fp32 reassociation (one of these 400
-predictions moved by 1.3e-2 between two fp32 evaluations); both well inside
-the default dims' fp32 scatter bounds held against float64 in
-test_default_dims_gpu.py."""
+and that the metrics follow. The same evaluator loop runs over the oracle's
+process_batch three times: in float64 on the GPU (the exact answer), and in
+fp32 on the host and on the GPU (the reference's own fp32 scatter). Per
+tower, the engine's largest relative distance from float64 (floor 0.01) is
+within 2x the larger of the two fp32 runs' (RetNet's per-head RMSNorm of
+near-cancelling contractions amplifies fp32 reassociation: one of these 400
+predictions moves by about 1e-2 between two fp32 evaluations)."""
 
 from pathlib import Path
 
@@ -36,27 +37,48 @@ def _recording(fn, log):
     return wrapped
 
 
-def test_tiny_parquet_engine_vs_oracle(dev):
+def test_tiny_parquet_engine_vs_oracle(dev, default_params):
     from hackathon_amd.client import InferenceResponse, NnInferenceClient
     from hackathon_amd.evaluator import LocalEvaluator
 
     ev = LocalEvaluator(TINY)
     cfg = spec.DEFAULT
-    params = weights.generate(cfg, 0)
+    params = default_params
     client = NnInferenceClient(ev.num_symbols, weights=params, linear_dtype="fp32")
     got, want = [], []
     m_gpu = ev.evaluate_model(_recording(client.process_batch, got), batch_size=8)
     client.engine.check()
     client2 = NnInferenceClient(ev.num_symbols, engine=None, weights=params, linear_dtype="fp32")
     m_arr = ev.evaluate_arrays(client2, batch_size=8)
-    oracle = OracleClient(om.Params(params), cfg, ev.num_symbols)
-    m_ref = ev.evaluate_model(
-        _recording(lambda b: InferenceResponse(*oracle.process_batch(b), 0.0), want), batch_size=8)
+    client2.engine.close()
+    client.engine.close()
+    del client, client2
+    torch.cuda.empty_cache()
+
+    def oracle_run(P, device, log):
+        oracle = OracleClient(P, cfg, ev.num_symbols, device=device)
+        return ev.evaluate_model(
+            _recording(lambda b: InferenceResponse(*oracle.process_batch(b), 0.0), log),
+            batch_size=8)
+
+    want_g, want64 = [], []
+    m_ref = oracle_run(om.Params(params), "cpu", want)
+    oracle_run(om.Params({k: v.to(dev) for k, v in params.items()}), dev, want_g)
+    torch.cuda.empty_cache()
+    oracle_run(om.Params({k: v.to(dev) for k, v in params.items()}, dtype=torch.float64), dev,
+               want64)
+    torch.cuda.empty_cache()
     assert m_gpu["response_rate"] == 1.0 == m_ref["response_rate"] == m_arr["response_rate"]
-    for (ids_g, p_g), (ids_r, p_r) in zip(got, want):
-        assert ids_g == ids_r
-        rel = np.abs(p_g - p_r) / np.maximum(np.abs(p_r), 1e-2)
-        assert (rel.max(0) <= np.array([5e-3, 5e-3, 5e-2, 5e-3])).all(), f"max rel {rel.max(0)}"
+    for log in (want, want_g, want64):
+        assert [ids for ids, _ in got] == [ids for ids, _ in log]
+    cat = lambda log: np.concatenate([p for _, p in log])
+    rel = lambda a, e: (np.abs(a - e) / np.maximum(np.abs(e), 1e-2)).max(0)
+    exact = cat(want64)
+    e = rel(cat(got), exact)
+    sc = np.maximum(rel(cat(want), exact), rel(cat(want_g), exact))
+    print(f"tiny.parquet: engine max rel err per tower {e}, reference fp32 runs {sc}, "
+          f"ratio {e / sc}")
+    assert (e <= 2.0 * sc).all(), f"engine {e} against 2x the fp32 scatter {sc}"
     for t in range(4):
         assert m_gpu[f"tower_{t}"] == pytest.approx(m_ref[f"tower_{t}"], rel=1e-3)
         # process_arrays on a second client: the same predictions bit for bit

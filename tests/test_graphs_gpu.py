@@ -14,8 +14,8 @@ request history is replayed through the reference's rounds (symbols are
 independent, so a slot's predictions depend on its own history alone), in
 fp32 at the mid-width fp32 bar (|d| <= 1e-5 + 1e-5 |ref|), and with the
 reference's bf16 CastLinear at the reduced-precision bar (the engine's mean
-squared distance from the reference's bf16 result at most a tenth of that
-result's distance from fp32)."""
+squared distance from the reference's bf16 result at most 2% of that
+result's distance from fp32; measured 1.06%)."""
 
 import numpy as np
 import pytest
@@ -98,4 +98,4 @@ def test_graph_replay_matches_eager(dev, lp):
         r_32 = float(((plp - p32) ** 2).mean())
         print(f"graph replay vs oracle {lp}: MSE engine-vs-reference-{lp} {e_lp:.3e}, "
               f"reference-{lp}-vs-fp32 {r_32:.3e}, ratio {e_lp / r_32:.3e}")
-        assert e_lp <= 0.1 * r_32
+        assert e_lp <= 0.02 * r_32

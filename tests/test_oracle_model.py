@@ -74,10 +74,10 @@ def test_small_model_masked_steps():
         torch.testing.assert_close(leaf, _t(fx[f"state/{i}"]), rtol=RTOL, atol=ATOL)
 
 
-def test_default_dims_predictions():
+def test_default_dims_predictions(default_params):
     fx = np.load(GOLDEN / "default.npz")
     cfg = spec.DEFAULT
-    P = om.Params(weights.generate(cfg, 0))
+    P = om.Params(default_params)
     state = om.init_state(cfg, 4)
     with torch.inference_mode():
         for t in range(4):
@@ -85,7 +85,7 @@ def test_default_dims_predictions():
             torch.testing.assert_close(preds, _t(fx[f"preds/{t}"]), rtol=1e-4, atol=1e-5)
 
 
-def test_default_dims_float64_predictions():
+def test_default_dims_float64_predictions(default_params):
     """The oracle in float64 (Params(dtype=torch.float64)), the yardstick the
     GPU fp32 parity tests measure distances from, against the reference's own
     float64 run of the same model and inputs (default.npz preds64: the
@@ -95,7 +95,7 @@ def test_default_dims_float64_predictions():
     wrong eps or a dropped term would not."""
     fx = np.load(GOLDEN / "default.npz")
     cfg = spec.DEFAULT
-    P = om.Params(weights.generate(cfg, 0), dtype=torch.float64)
+    P = om.Params(default_params, dtype=torch.float64)
     state = om.init_state(cfg, 4, torch.float64)
     with torch.inference_mode():
         for t in range(4):
@@ -193,12 +193,12 @@ def test_castlinear_small_model_masked_steps(lp):
 
 
 @pytest.mark.parametrize("lp", ["bf16", "fp16"])
-def test_castlinear_default_dims_predictions(lp):
+def test_castlinear_default_dims_predictions(lp, default_params):
     """Default dims after the reference's convert_linears: the first two
     steps of default.npz's inputs (tests/golden/default_lp.npz)."""
     fx = np.load(GOLDEN / "default_lp.npz")
     cfg = spec.DEFAULT
-    P = om.Params(weights.generate(cfg, 0), lp=lp)
+    P = om.Params(default_params, lp=lp)
     state = om.init_state(cfg, 4)
     with torch.inference_mode():
         for t in range(2):
