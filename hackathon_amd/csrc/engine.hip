@@ -43,6 +43,10 @@ static __device__ __align__(256) float scratch[kScratchFloats];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_dev[kMaxDevices] = {};
+// Held by a binding for as long as it stages through a device's array, so
+// that two bindings on one device (from two engines or threads) never
+// overwrite each other's chunks.
+std::mutex g_scratch_use_mu[kMaxDevices];
 
 // The device address of `scratch` on the current device.
 int scratch_on_current_device(float** out) {
@@ -1375,8 +1379,8 @@ int hk_engine_load_param(void* h, int tower, int layer, int slot, const float* h
 // through this device's `scratch` array, kScratchFloats values at a time
 // (copy in, convert into the slot, wait, next chunk), so a slot of any size
 // binds through the 16 MiB array; biases are rounded in place in the slot and
-// fp32 slots copied straight in. Calls on one device share its array: two
-// calls that overlap in time race.
+// fp32 slots copied straight in. Calls on one device share its array; a lock
+// per device serialises their staging within the process.
 int hk_engine_load_param_noalloc(void* h, int tower, int layer, int slot, const float* host,
                                  int64_t numel) {
   HK_REQUIRE(h && host, "hk_engine_load_param_noalloc: null argument");
@@ -1399,15 +1403,26 @@ int hk_engine_load_param_noalloc(void* h, int tower, int layer, int slot, const 
     const int64_t step = s->packed ? (hk::kScratchFloats / K) / 32 * 32 * K : hk::kScratchFloats;
     HK_REQUIRE(step > 0, "hk_engine_load_param_noalloc: %s rows do not fit the staging array",
                s->def.name);
-    for (int64_t off = 0; off < numel; off += step) {
-      const int64_t n = std::min(step, numel - off);
-      HK_CHECK_HIP(hipMemcpy(e.scratch, host + off, (size_t)n * 4, hipMemcpyHostToDevice));
-      if (s->packed) {
-        HK_TRY(hk::pack_f32_to_lp(e.scratch, dst + off, (int)(n / K), (int)K, e.lp_fmt, nullptr));
-      } else {
-        HK_TRY(hk::to_lp(e.scratch, dst + off, n, e.lp_fmt, nullptr));
+    std::lock_guard<std::mutex> lock(hk::g_scratch_use_mu[dev]);
+    auto chunks = [&]() -> int {
+      for (int64_t off = 0; off < numel; off += step) {
+        const int64_t n = std::min(step, numel - off);
+        HK_CHECK_HIP(hipMemcpy(e.scratch, host + off, (size_t)n * 4, hipMemcpyHostToDevice));
+        if (s->packed) {
+          HK_TRY(hk::pack_f32_to_lp(e.scratch, dst + off, (int)(n / K), (int)K, e.lp_fmt, nullptr));
+        } else {
+          HK_TRY(hk::to_lp(e.scratch, dst + off, n, e.lp_fmt, nullptr));
+        }
+        HK_CHECK_HIP(hipStreamSynchronize(nullptr));  // the next chunk overwrites the array
       }
-      HK_CHECK_HIP(hipStreamSynchronize(nullptr));  // the next chunk overwrites the array
+      return HK_OK;
+    };
+    const int st = chunks();
+    if (st != HK_OK) {
+      // a failed chunk may have left a conversion reading the array: wait
+      // for it before the lock lets another binding overwrite the array
+      (void)hipStreamSynchronize(nullptr);
+      return st;
     }
   } else if (s->def.lp_bias && e.lowp) {
     HK_CHECK_HIP(hipMemcpy(s->ptr, host, (size_t)numel * 4, hipMemcpyHostToDevice));

@@ -379,8 +379,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
           if (off[i][j][e] >= 0)
             __hip_atomic_store(pb + split * MN + off[i][j][e], acc[i][j][e], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-    // Every partial store of this lane acknowledged at the agent-coherent
-    // level, then every wave's, before the tile counter sees this split.
+    // Release side: the partials are stored with agent scope (sc1, written
+    // through this XCD's L2), so once every lane's stores are acknowledged
+    // (vmcnt 0) and every wave has passed the barrier, they are visible to
+    // any XCD before the tile counter sees this split. An agent-scope
+    // release fence would also write back the whole L2 (buffer_wbl2): the
+    // CastLinear replay measured 16.6 against 13.8 us per launch with one.
     wait_vmcnt<0>();
     __shared__ int last_split;
     __syncthreads();
@@ -390,6 +394,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
                                           __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
     if (!last_split) return;
+    // Acquire side: the last split's loads of the other partials (agent
+    // scope, sc1) come after the counter showed every split, and no stale
+    // line of this CU's L1 can serve them.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(arrival, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Sum in split order, four splits' loads in flight at a time; this
     // split's own part comes from its registers.
@@ -682,8 +690,12 @@ __global__ __launch_bounds__(64 * NW) void gemm_wp_kernel(GemmArgs g, float* par
                                                  lane_b + (m * 2 + c) * 1024, split * TILE * 4,
                                                  kCoherentSc1);
     }
-    // Every partial store of this lane acknowledged at the agent-coherent
-    // level, then every wave's, before the tile counter sees this split.
+    // Release side: the partials are stored with agent scope (sc1, written
+    // through this XCD's L2), so once every lane's stores are acknowledged
+    // (vmcnt 0) and every wave has passed the barrier, they are visible to
+    // any XCD before the tile counter sees this split. An agent-scope
+    // release fence would also write back the whole L2 (buffer_wbl2): the
+    // CastLinear replay measured 16.6 against 13.8 us per launch with one.
     wait_vmcnt<0>();
     __shared__ int last_split;
     __syncthreads();
@@ -693,6 +705,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_wp_kernel(GemmArgs g, float* par
                                           __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
     if (!last_split) return;
+    // Acquire side: the last split's loads of the other partials (agent
+    // scope, sc1) come after the counter showed every split, and no stale
+    // line of this CU's L1 can serve them.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(arrival, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!cols_live) return;
     // Sum in split order; this split's own part comes from its registers.

@@ -296,6 +296,18 @@ class Engine:
             out.append(buf)
         return out
 
+    def copy_slots(self, src0: int, dst0: int, nslots: int):
+        """Copy the state of slots [src0, src0+nslots) to [dst0, dst0+nslots)
+        (ranges disjoint), stream-ordered: every leaf of every block, pending
+        write-back entries applied (the source's value is unchanged)."""
+        assert nslots >= 0 and 0 <= src0 and 0 <= dst0
+        assert max(src0, dst0) + nslots <= self.capacity
+        assert src0 + nslots <= dst0 or dst0 + nslots <= src0, "slot ranges overlap"
+        for t in range(4):
+            for b in range(self.cfg.tower_depth):
+                for leaf, buf in enumerate(self._raw_leaves(t, b, src0, nslots)):
+                    self._copy_leaf(t, b, leaf, dst0, nslots, buf, True)
+
     def export_state(self, slot0: int = 0, nslots: int | None = None):
         """State of slots [slot0, slot0+nslots) in the reference's init_state
         tree: [tower][block] -> the layer's nested leaves (conv windows as

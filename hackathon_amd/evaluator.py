@@ -32,18 +32,21 @@ from .client import PendingRequest
 TOWER_NAMES = ("XLSTM", "Mamba2", "RetNet", "Hawk")
 
 
-def calculate_metrics(targets: np.ndarray, predictions: dict, latencies: dict) -> dict:
-    """targets [n, 4] indexed by request id (the row index); predictions and
-    latencies keyed by request id (local_evaluator.py:64-101)."""
+def calculate_metrics(targets: np.ndarray, predictions: dict, latencies: dict,
+                      ids=None) -> dict:
+    """targets [n, 4], row r the targets of request ids[r] (ids: the
+    requests' unique ids in file order, the parquet's index labels; default
+    0 .. n-1); predictions and latencies keyed by request id
+    (local_evaluator.py:64-101)."""
     tower_err = defaultdict(list)
     lat = []
-    for uid in range(len(targets)):
+    for r, uid in enumerate(range(len(targets)) if ids is None else ids):
         if uid not in predictions:
             continue
         pred = predictions[uid]
         if len(pred) != targets.shape[1]:
             raise ValueError(f"request {uid}: {len(pred)} predictions for {targets.shape[1]} targets")
-        for t, (p, y) in enumerate(zip(pred, targets[uid])):
+        for t, (p, y) in enumerate(zip(pred, targets[r])):
             tower_err[t].append(abs(float(p) - float(y)))
         lat.append(latencies[uid])
     out = {
@@ -70,6 +73,9 @@ class LocalEvaluator:
         self.features = df[self.feature_cols].to_numpy(dtype=np.float32)
         self.targets = df[self.target_cols].to_numpy(dtype=np.float64)
         self.symbols = df["symbol"].tolist()
+        # request ids: the index labels, as the reference's iterrows() gives
+        # them (local_evaluator.py:26-35)
+        self.ids = df.index.tolist()
 
     def _batches(self, batch_size):
         n = len(self.symbols)
@@ -81,7 +87,7 @@ class LocalEvaluator:
         for rows in self._batches(batch_size):
             batch_by_symbol = {}
             for r in rows:
-                req = PendingRequest(unique_id=r, symbol=self.symbols[r],
+                req = PendingRequest(unique_id=self.ids[r], symbol=self.symbols[r],
                                      features=self.features[r].tolist(), received_time=time.time())
                 batch_by_symbol.setdefault(req.symbol, []).append(req)
             t0 = time.perf_counter()
@@ -90,7 +96,7 @@ class LocalEvaluator:
             for uid, pred in zip(resp.unique_ids, resp.predictions):
                 predictions[uid] = pred
                 latencies[uid] = ms
-        return calculate_metrics(self.targets, predictions, latencies)
+        return calculate_metrics(self.targets, predictions, latencies, self.ids)
 
     def evaluate_arrays(self, client, batch_size: int) -> dict:
         """evaluate_model through client.process_arrays: the batch's rows
@@ -106,9 +112,10 @@ class LocalEvaluator:
                                                 self.features[order])
             ms = (time.perf_counter() - t0) * 1000
             for j, p in zip(resp, preds):
-                predictions[int(order[j])] = p.tolist()
-                latencies[int(order[j])] = ms
-        return calculate_metrics(self.targets, predictions, latencies)
+                uid = self.ids[int(order[j])]
+                predictions[uid] = p.tolist()
+                latencies[uid] = ms
+        return calculate_metrics(self.targets, predictions, latencies, self.ids)
 
     @staticmethod
     def print_report(metrics: dict):

@@ -19,19 +19,27 @@ engine's HBM store, and `init_state` hands out an `EngineState`, a handle on
   already done.
 - With mask None the reference writes nothing in place and returns fresh
   tensors (model/inference_model.py:132-134), so the old state stays
-  usable. Copying the whole state per step would double the state traffic,
-  so this build advances the slots in place, returns a new handle on them
-  and retires the old handle: any later use of it raises `StaleStateError`
-  rather than silently reading the advanced state.
+  usable. Here too: the rows are copied to `batch_size` fresh slots, which
+  then advance, and a new handle on them is returned; the old handle still
+  holds the old state. Each handle gives its slots back when it is released
+  or garbage-collected, as the reference's tensors are freed, so the model
+  needs room for both states at once (2 x batch_size rows) during the call.
 
 `EngineState.export()` gives the reference's init_state tree (tensors) for
 inspection, and `EngineState.load(tree)` writes one in.
 
-Rows whose mask is False come back as zero predictions (the reference
-returns the full model's output on those rows, which its client discards).
-The mask is read on the host: a CPU bool tensor, numpy array or sequence
-costs nothing; a mask on the GPU is copied to the host first, which waits
-for the work queued before it.
+Two deliberate deviations:
+- Rows whose mask is False come back as zero predictions (the reference
+  returns the full model's output on those rows, computed with the matrix
+  cells' outputs zeroed, and its client discards them). The engine runs
+  only the active rows.
+- The mask is read on the host, because the tick's launch shapes (rows,
+  runs, steps) come from it: a CPU bool tensor, numpy array or sequence
+  costs nothing; a mask on the GPU is copied to the host first, which waits
+  for the work queued before it (the reference reads a device mask inside
+  its captured step, example_model.py:865-871). The engine's own client
+  (NnInferenceClient.process_batch) builds its runs on the host and never
+  waits for a mask.
 
 `load_state_dict(sd)` binds a reference state_dict (weights only, as the
 reference client loads its checkpoint with torch.load(weights_only=True),
@@ -50,7 +58,7 @@ from .spec import DEFAULT, ModelConfig
 
 
 class StaleStateError(RuntimeError):
-    """A state handle retired by a mask=None forward was used again."""
+    """A released state handle was used again."""
 
 
 class EngineState:
@@ -64,8 +72,7 @@ class EngineState:
 
     def _check(self, model):
         if not self._live:
-            raise StaleStateError("this state was advanced by a mask=None forward; use the "
-                                  "state that forward returned")
+            raise StaleStateError("this state was released")
         if model is not self._model:
             raise ValueError("the state belongs to another model")
 
@@ -84,6 +91,12 @@ class EngineState:
         if self._live:
             self._live = False
             self._model._free(self.slot0, self.batch_size)
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:  # interpreter shutdown: the model may be gone
+            pass
 
 
 class MultiTowerModel:
@@ -167,7 +180,17 @@ class MultiTowerModel:
         assert x.dtype == torch.float32 and tuple(x.shape) == (B, self.config.num_features), (
             f"x must be float32 [{B}, {self.config.num_features}]")
         if mask is None:
+            # the reference leaves the old state as it was: advance a copy
             active = np.arange(B, dtype=np.int32)
+            try:
+                s0 = self._alloc(B)
+            except _lib.CapacityError as exc:
+                raise _lib.CapacityError(
+                    f"a mask=None forward keeps the old state: it needs {B} more free rows "
+                    f"(model capacity {self.engine.capacity})") from exc
+            with torch.cuda.device(self.device):
+                self.engine.copy_slots(state.slot0, s0, B)
+            state = EngineState(self, s0, B)
         else:
             m = mask.detach().cpu().numpy() if isinstance(mask, torch.Tensor) else np.asarray(mask)
             assert m.dtype == np.bool_ and m.shape == (B,), "mask must be bool [B]"
@@ -185,10 +208,6 @@ class MultiTowerModel:
                     self.device, non_blocking=True)
                 preds = self.engine.tick(runs, x.index_select(0, idx).contiguous())
                 out.index_copy_(0, idx, preds)
-        if mask is None:
-            state._live = False
-            fresh = EngineState(self, state.slot0, B)
-            return out, fresh
         return out, state
 
     __call__ = forward

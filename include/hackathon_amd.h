@@ -217,8 +217,8 @@ int hk_engine_load_param(void* handle, int tower, int layer, int slot, const flo
  * array that the library holds in every GPU's memory for the life of the
  * process, 4 Mi values at a time, so a slot of any size binds; results are
  * bit-identical to hk_engine_load_param's. Synchronous. The engine's device
- * must be current. Calls on one GPU share its array: calls that overlap in
- * time race. */
+ * must be current. Calls on one GPU share its array; a lock per GPU makes
+ * calls from several threads of the process take turns with it. */
 int hk_engine_load_param_noalloc(void* handle, int tower, int layer, int slot, const float* host,
                                  int64_t numel);
 

@@ -73,7 +73,7 @@ def test_default_dims_fp32_golden(dev, params):
 
     fx = np.load(GOLDEN / "default.npz")
     cfg = spec.DEFAULT
-    model = MultiTowerModel(cfg, capacity=4, linear_dtype="fp32", weights=params)
+    model = MultiTowerModel(cfg, capacity=8, linear_dtype="fp32", weights=params)
     st = model.init_state(4, dev)
     PG = om.Params({k: v.to(dev) for k, v in params.items()})
     sg = to_device(om.init_state(cfg, 4), dev)
@@ -238,7 +238,7 @@ def test_default_dims_castlinear_golden(dev, params, lp):
 
     fx = np.load(GOLDEN / "default_lp.npz")
     f32 = np.load(GOLDEN / "default.npz")
-    model = MultiTowerModel(spec.DEFAULT, capacity=4, linear_dtype=lp, weights=params)
+    model = MultiTowerModel(spec.DEFAULT, capacity=8, linear_dtype=lp, weights=params)
     st = model.init_state(4, dev)
     got = []
     for t in range(2):

@@ -222,10 +222,11 @@ def test_persistent_slstm_head512_fp32(dev):
     1024 (2 sLSTM heads, so 64 work-groups), on skewed ticks: 20 runs at
     step 0 (two 16-run chunks), one of 24 steps, then single requests, then
     a tick of 13 / 6 / 5-step runs. Every prediction and state leaf of the
-    engine against the float64 reference, within 4x the distance of the
-    reference's own fp32 run from it (at this width the fp32 reference is up
-    to 7e-5 relative and 2e-6 absolute from float64), and every prediction
-    within 1e-5 relative + 1e-5 absolute of the float64 result."""
+    engine against the float64 reference, within 2x the larger distance of
+    the reference's own two fp32 runs (on the host and in torch on this GPU)
+    from it (at this width the fp32 reference is up to 7e-5 relative and
+    2e-6 absolute from float64), and every prediction within 1e-5 relative +
+    1e-5 absolute of the float64 result."""
     from hackathon_amd.engine import Engine, pack_runs
     from refrun import leaf_rel, reference_rounds, rel_err
 
@@ -254,20 +255,23 @@ def test_persistent_slstm_head512_fp32(dev):
     state = eng.export_state(0, n)
     eng.close()
     p32, s32 = reference_rounds(om.Params(params), cfg, hist)
+    pg, sg = reference_rounds(om.Params({k: v.to(dev) for k, v in params.items()}), cfg, hist,
+                              device=dev)
     p64, s64 = reference_rounds(om.Params(params, dtype=torch.float64), cfg, hist)
     cat = lambda v: np.concatenate([np.asarray(a) for a in v])
-    g, r32, r64 = cat(got), cat(p32), cat(p64)
-    e, sc = rel_err(g, r64).max(0), rel_err(r32, r64).max(0)
-    print(f"head 512: engine max rel err per tower {np.array2string(e, precision=2)}, "
-          f"reference fp32 {np.array2string(sc, precision=2)}")
-    assert (e <= 4.0 * sc).all(), f"engine {e} beyond 4x the reference's fp32 scatter {sc}"
+    g, r32, rg32, r64 = cat(got), cat(p32), cat(pg), cat(p64)
+    e = rel_err(g, r64).max(0)
+    sc = np.maximum(rel_err(r32, r64).max(0), rel_err(rg32, r64).max(0))
+    print(f"head 512: engine max rel err per tower {e}, reference fp32 runs {sc}, ratio {e / sc}")
+    assert (e <= 2.0 * sc).all(), f"engine {e} beyond 2x the reference's fp32 scatter {sc}"
     _close(torch.from_numpy(g), torch.from_numpy(r64), 1e-5, 1e-5, "head 512 preds vs float64")
-    for i, (gl, al, el) in enumerate(zip(om.flatten(state), om.flatten(s32), om.flatten(s64))):
+    for i, (gl, al, bl, el) in enumerate(zip(om.flatten(state), om.flatten(s32), om.flatten(sg),
+                                             om.flatten(s64))):
         if el.dtype == torch.int32:
             assert torch.equal(gl.cpu(), el), f"leaf {i}: offsets differ"
             continue
-        rg, ra = leaf_rel(gl, el), leaf_rel(al, el)
-        assert rg <= 4.0 * ra + 1e-7, f"state leaf {i} {tuple(el.shape)}: engine {rg:.3e}, reference fp32 {ra:.3e}"
+        rg, ra = leaf_rel(gl, el), max(leaf_rel(al, el), leaf_rel(bl, el))
+        assert rg <= 2.0 * ra + 1e-7, f"state leaf {i} {tuple(el.shape)}: engine {rg:.3e}, reference fp32 {ra:.3e}"
 
 
 @pytest.mark.parametrize("lp", ["bf16", "fp16"])
@@ -302,6 +306,49 @@ def test_castlinear_small_fixture(dev, small_params, lp):
           f"reference-vs-fp32 {r_32:.3e}")
     assert e_lp <= (0.01 if lp == "bf16" else 0.1) * r_32
     assert e_32 <= 1.1 * r_32
+
+
+def test_model_mask_none_keeps_the_old_state(dev, small_params):
+    """model(x, state) without a mask returns a fresh state and writes
+    nothing in place (model/inference_model.py:132-134): the old handle still
+    holds the old state (a second forward from it gives the same
+    predictions bit for bit), the new one has advanced (predictions against
+    the oracle's unmasked forward at the fp32 bar), and a handle's slots go
+    back to the model when it is garbage-collected."""
+    import gc
+
+    from hackathon_amd.model import MultiTowerModel
+
+    cfg = spec.SMALL
+    fx = np.load(GOLDEN / "small.npz")
+    model = MultiTowerModel(cfg, capacity=18, linear_dtype="fp32", weights=small_params)
+    P = om.Params(small_params)
+    st0 = model.init_state(6, dev)
+    ref = om.init_state(cfg, 6)
+    x0, x1 = (torch.from_numpy(fx[f"x/{t}"]) for t in range(2))
+    p1, st1 = model(x0.to(dev), st0)
+    q1, ref1 = om.forward(P, cfg, x0, ref)
+    _close(p1, q1, P_RTOL, P_ATOL, "step 0 preds")
+    for a, b in zip(om.flatten(st0.export()), om.flatten(ref)):
+        assert torch.equal(a.cpu(), b), "the old state changed"
+    p1b, st1b = model(x0.to(dev), st0)
+    assert torch.equal(p1, p1b), "a second forward from the old state differs"
+    assert st1b.slot0 not in (st0.slot0, st1.slot0)
+    del st1b, st0
+    gc.collect()
+    p2, st2 = model(x1.to(dev), st1)
+    q2, _ = om.forward(P, cfg, x1, ref1)
+    _close(p2, q2, P_RTOL, P_ATOL, "step 1 preds")
+    del st1
+    gc.collect()
+    assert sum(c for _, c in model._free_ranges) == 12  # only st2 holds slots
+    a, b = model.init_state(6, dev), model.init_state(6, dev)
+    from hackathon_amd import _lib
+
+    with pytest.raises(_lib.CapacityError):
+        model(x1.to(dev), a)  # no room for the fresh copy
+    model.engine.check()
+    model.close()
 
 
 def test_state_roundtrip_and_reset(dev, small_params):

@@ -69,6 +69,35 @@ def test_tiny_parquet_batching_and_capacity():
         assert m2[f"tower_{t}"] == pytest.approx(m[f"tower_{t}"])
 
 
+def test_request_ids_are_the_index_labels(tmp_path):
+    """The reference numbers requests by the DataFrame's index labels
+    (iterrows(), local_evaluator.py:26-35): a parquet whose index is not
+    0..n-1 gives those labels as unique_ids, and the metric pairs each
+    answer with its own row's targets."""
+    import pandas as pd
+
+    df = pd.read_parquet(TINY)
+    df.index = pd.Index(1000 + 7 * np.arange(len(df))[::-1])
+    path = tmp_path / "relabelled.parquet"
+    df.to_parquet(path)
+    ev = LocalEvaluator(path)
+    seen = []
+
+    def fake_process_batch(by_sym):
+        ids = [r.unique_id for reqs in by_sym.values() for r in reqs]
+        seen.extend(ids)
+        row = {label: i for i, label in enumerate(ev.ids)}
+        return SimpleNamespace(unique_ids=ids,
+                               predictions=[ev.features[row[i], :4].tolist() for i in ids])
+
+    m = ev.evaluate_model(fake_process_batch, batch_size=8)
+    assert sorted(seen) == sorted(df.index.tolist()) and m["response_rate"] == 1.0
+    err = np.abs(ev.features[:, :4].astype(np.float64) - ev.targets)
+    for t in range(4):
+        assert m[f"tower_{t}"][0] == pytest.approx(err[:, t].max())
+        assert m[f"tower_{t}"][1] == pytest.approx(err[:, t].mean())
+
+
 def test_checkpoint_ingest_weights_only(tmp_path):
     cfg = spec.SMALL
     sd = weights.generate(cfg, 0)
