@@ -394,10 +394,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
                                           __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
     if (!last_split) return;
-    // Acquire side: the last split's loads of the other partials (agent
-    // scope, sc1) come after the counter showed every split, and no stale
-    // line of this CU's L1 can serve them.
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // Acquire side: the last split's loads of the other partials are
+    // issued only after the counter's returned value (through LDS and the
+    // barrier) selected this work-group, and they are agent-scope loads
+    // (sc1) that no line of this CU's L1 or of a non-coherent L2 state
+    // serves. An agent-scope acquire fence here would also invalidate the
+    // XCD's L2 (buffer_inv sc1): the CastLinear replay measured 0.199
+    // against 0.210 of HBM peak, and the C4 tick 8.78 against 8.70 ms.
     if (tid == 0) __hip_atomic_store(arrival, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Sum in split order, four splits' loads in flight at a time; this
     // split's own part comes from its registers.
@@ -705,10 +708,13 @@ __global__ __launch_bounds__(64 * NW) void gemm_wp_kernel(GemmArgs g, float* par
                                           __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
     if (!last_split) return;
-    // Acquire side: the last split's loads of the other partials (agent
-    // scope, sc1) come after the counter showed every split, and no stale
-    // line of this CU's L1 can serve them.
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // Acquire side: the last split's loads of the other partials are
+    // issued only after the counter's returned value (through LDS and the
+    // barrier) selected this work-group, and they are agent-scope loads
+    // (sc1) that no line of this CU's L1 or of a non-coherent L2 state
+    // serves. An agent-scope acquire fence here would also invalidate the
+    // XCD's L2 (buffer_inv sc1): the CastLinear replay measured 0.199
+    // against 0.210 of HBM peak, and the C4 tick 8.78 against 8.70 ms.
     if (tid == 0) __hip_atomic_store(arrival, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!cols_live) return;
     // Sum in split order; this split's own part comes from its registers.

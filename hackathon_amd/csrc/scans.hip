@@ -104,82 +104,94 @@ __global__ __launch_bounds__(256) void retnet_prep_kernel(
 }
 
 
-// grid (runs, ceil(hidden/256)); thread per channel. Only h' = h*a_t + u_t
-// is sequential: a run's rows go through in chunks of kRgChunk, the next
-// chunk's loads in flight while this one is computed, and within a chunk the
-// gates (a_t, u_t and the output gate) of all rows are formed before the
-// recurrence runs over them.
+// RG-LRU over each run's rows (model/hawk.py:31-37, with the output gate
+// of model/hawk.py:83). grid (runs, ceil(hidden/64)); 256 threads = 64
+// channels x 4 row lanes. Only h' = h*a_t + u_t is sequential over a run's
+// rows; the gates (a_t = a^(c r_t), u_t = sqrt(1 - a_t^2) i_t x_t and the
+// output gate gelu(g_t)), the bulk of the arithmetic, are independent per
+// row. A run's rows go through in chunks of kRgChunk: each row lane forms
+// the gates of every fourth row of the chunk into LDS (the next chunk's
+// inputs already loading into registers), then row lane 0 runs the
+// recurrence over the chunk and writes the outputs, so a long run's serial
+// chain holds two multiplies and an add per row.
 constexpr int kRgChunk = 16;
+constexpr int kRgLanes = 4;                  // row lanes per channel
+constexpr int kRgPer = kRgChunk / kRgLanes;  // rows per lane per chunk
 __global__ __launch_bounds__(256) void rglru_scan_kernel(
     const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ x,
     const float* __restrict__ gi, const float* __restrict__ gr, int64_t ldg,
     const float* __restrict__ gate, int64_t ld_gate, const float* __restrict__ a, float c_exp,
     int hidden, float* __restrict__ h_state, float* __restrict__ out,
     uint16_t* __restrict__ out_lp, int lp_fmt) {
+  __shared__ float s_at[2][kRgChunk][64], s_ut[2][kRgChunk][64], s_og[2][kRgChunk][64];
   const int run = blockIdx.x;
-  const int c = blockIdx.y * 256 + threadIdx.x;
-  if (c >= hidden) return;
+  const int cl = threadIdx.x & 63;
+  const int lr = threadIdx.x >> 6;  // row lane (= wave)
+  const int c = blockIdx.y * 64 + cl;
+  const bool live = c < hidden;
+  const int cc = live ? c : 0;      // loads of a channel past hidden read channel 0
   const int slot = slot_ids[run];
   const int r0 = run_off[run];
   const int r1 = run_off[run + 1];
   if (r1 <= r0) return;
-  float h = h_state[(int64_t)slot * hidden + c];
-  const float base = a[c];
+  const float base = a[cc];
   struct Rows {
-    float i[kRgChunk], r[kRgChunk], x[kRgChunk], g[kRgChunk];
+    float i[kRgPer], r[kRgPer], x[kRgPer], g[kRgPer];
   };
-  // rows past the run read its last row (unused)
+  // this lane's rows of the chunk at rb: rb + lr + kRgLanes*k (rows past the
+  // run read its last row; their gates are never used)
   auto load = [&](Rows& v, int rb) {
 #pragma unroll
-    for (int k = 0; k < kRgChunk; ++k) {
-      const int64_t ri = (int64_t)min(rb + k, r1 - 1);
-      v.i[k] = gi[ri * ldg + c];
-      v.r[k] = gr[ri * ldg + c];
-      v.x[k] = x[ri * hidden + c];
-      v.g[k] = gate[ri * ld_gate + c];
+    for (int k = 0; k < kRgPer; ++k) {
+      if (k > 0 && rb + lr + kRgLanes * k >= r1) break;
+      const int64_t ri = (int64_t)min(rb + lr + kRgLanes * k, r1 - 1);
+      v.i[k] = gi[ri * ldg + cc];
+      v.r[k] = gr[ri * ldg + cc];
+      v.x[k] = x[ri * hidden + cc];
+      v.g[k] = gate[ri * ld_gate + cc];
     }
   };
-  auto step = [&](const Rows& v, int rb) {
+  auto gates = [&](const Rows& v, int rb, int buf) {
     // Each product and sum rounded on its own, as the reference's tensor
-    // ops do (model/hawk.py:35-37): no multiply-add is fused here, so the
-    // result does not depend on how the compiler lays out the chunk.
+    // ops do (model/hawk.py:35-37): no multiply-add is fused. Rows past the
+    // run are skipped (most runs are a few rows long).
 #pragma clang fp contract(off)
-    // The gates of the chunk's rows in the run only (the bound is uniform
-    // over the work-group, so rows past the run cost a branch, not the math).
-    float at[kRgChunk], ut[kRgChunk], og[kRgChunk];
 #pragma unroll
-    for (int k = 0; k < kRgChunk; ++k) {
-      at[k] = ut[k] = og[k] = 0.0f;
-      if (rb + k < r1) {
-        const float it = sigmoid(v.i[k]);
-        const float rt = sigmoid(v.r[k]);
-        at[k] = powf(base, c_exp * rt);
-        const float mult = sqrtf(1.0f - at[k] * at[k]);
-        ut[k] = mult * (it * v.x[k]);
-        og[k] = gelu_erf(v.g[k]);
-      }
+    for (int k = 0; k < kRgPer; ++k) {
+      if (rb + lr + kRgLanes * k >= r1) break;
+      const float it = sigmoid(v.i[k]);
+      const float rt = sigmoid(v.r[k]);
+      const float at = powf(base, c_exp * rt);
+      const float mult = sqrtf(1.0f - at * at);
+      const int j = lr + kRgLanes * k;
+      s_at[buf][j][cl] = at;
+      s_ut[buf][j][cl] = mult * (it * v.x[k]);
+      s_og[buf][j][cl] = gelu_erf(v.g[k]);
     }
-#pragma unroll
-    for (int k = 0; k < kRgChunk; ++k) {
-      if (rb + k < r1) {
-        h = (h * at[k]) + ut[k];
-        const float o = og[k] * h;
-        const int64_t ri = (int64_t)(rb + k);
+  };
+  float h = lr == 0 ? h_state[(int64_t)slot * hidden + cc] : 0.0f;
+  Rows v;
+  load(v, r0);
+  int buf = 0;
+  for (int rb = r0; rb < r1; rb += kRgChunk, buf ^= 1) {
+    gates(v, rb, buf);
+    if (rb + kRgChunk < r1) load(v, rb + kRgChunk);
+    // the chunk's gates are in LDS; buffer buf was last read two chunks ago,
+    // before the previous barrier
+    lds_barrier();
+    if (lr == 0 && live) {
+#pragma clang fp contract(off)
+      const int n = min(kRgChunk, r1 - rb);
+      for (int j = 0; j < n; ++j) {
+        h = (h * s_at[buf][j][cl]) + s_ut[buf][j][cl];
+        const float o = s_og[buf][j][cl] * h;
+        const int64_t ri = (int64_t)(rb + j);
         if (out) out[ri * hidden + c] = o;
         if (out_lp) out_lp[ri * hidden + c] = f32_to_lp_bits(o, lp_fmt);
       }
     }
-  };
-  Rows va, vb;
-  load(va, r0);
-  for (int rb = r0; rb < r1; rb += 2 * kRgChunk) {
-    if (rb + kRgChunk < r1) load(vb, rb + kRgChunk);
-    step(va, rb);
-    if (rb + kRgChunk >= r1) break;
-    if (rb + 2 * kRgChunk < r1) load(va, rb + 2 * kRgChunk);
-    step(vb, rb + kRgChunk);
   }
-  h_state[(int64_t)slot * hidden + c] = h;
+  if (lr == 0 && live) h_state[(int64_t)slot * hidden + c] = h;
 }
 
 // One sLSTM step. grid (heads, units/16, ceil(n_active/16)); 256 threads =
@@ -789,11 +801,14 @@ __global__ void slstm_final_kernel(const int* __restrict__ slot_ids,
 //    butterfly leaves step j's wave sum in lane 8j after 10 shuffles (one
 //    wave sum per step would take 6 dependent shuffles each), and the waves'
 //    sums meet in LDS.
-// The rows of the next two blocks are prefetched into a register double
-// buffer; loads are unconditional (rows clamped to the run) so that the
-// compiler's wait counts stay exact.
+// The rows of the next NB - 1 blocks are prefetched into a ring of NB
+// register buffers: 4 for launches with runs of more than two blocks (a
+// load takes about as long as three blocks' compute), else 2, since every
+// buffer is filled whether or not the run reaches it; loads are
+// unconditional (rows clamped to the run) so that the compiler's wait
+// counts stay exact.
 constexpr int kGateBlock = 8;
-template <int NWV, int PER>
+template <int NWV, int PER, int NB>
 __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
     const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ if_pre,
     int n_parts, int64_t part_stride, int heads, const float* __restrict__ qkv, int inner, const float* __restrict__ ks,
@@ -842,7 +857,8 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
   // gate pre-activations: lane j < 8 holds i of step j, lane 8 + j holds f
   const int gj = lane & 7;
   const float* gh = if_pre + head + ((lane & 8) ? heads : 0);
-  float rq[2][B][PER], rk[2][B][PER], rg[2];
+  static_assert(NB >= 2 && NB % 2 == 0, "the LDS sum buffers alternate by block");
+  float rq[NB][B][PER], rk[NB][B][PER], rg[NB];
   auto fill = [&](float (&q)[B][PER], float (&k)[B][PER], float& g, int tb) {
 #pragma unroll
     for (int j = 0; j < B; ++j) {
@@ -854,8 +870,8 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
     g = gp[0];
     for (int p = 1; p < n_parts; ++p) g += gp[p * part_stride];
   };
-  fill(rq[0], rk[0], rg[0], 0);
-  fill(rq[1], rk[1], rg[1], B);
+#pragma unroll
+  for (int b = 0; b < NB - 1; ++b) fill(rq[b], rk[b], rg[b], b * B);
 
   auto block = [&](const float (&q)[B][PER], const float (&k)[B][PER], float g, int tb, int par) {
     float ig[B], fg[B], em[B];
@@ -907,12 +923,18 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
     }
   };
 
-  for (int tb = 0; tb < len; tb += 2 * B) {
-    block(rq[0], rk[0], rg[0], tb, 0);
-    if (tb + B >= len) break;  // the second block would hold no step of the run
-    fill(rq[0], rk[0], rg[0], tb + 2 * B);
-    block(rq[1], rk[1], rg[1], tb + B, 1);
-    fill(rq[1], rk[1], rg[1], tb + 3 * B);
+  // Block u of each group of NB uses buffer u; the loads of the block NB - 1
+  // ahead go into the buffer the previous block used, before this block
+  // runs, so NB - 1 blocks of loads are in flight behind the one computed.
+  for (int tb = 0; tb < len; tb += NB * B) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int t = tb + u * B;
+      if (t >= len) break;  // no step of the run left
+      const int nb = (u + NB - 1) % NB;
+      fill(rq[nb], rk[nb], rg[nb], t + (NB - 1) * B);
+      block(rq[u], rk[u], rg[u], t, u & 1);
+    }
   }
   if (e0 < hs) {
     VecT x;
@@ -960,7 +982,7 @@ int rglru_scan(const Runs& r, const float* x, const float* gi, const float* gr, 
                const float* gate, int64_t ld_gate, const float* a, float c_exp, int hidden,
                float* h_state, float* out, uint16_t* out_lp, int lp_fmt, hipStream_t s) {
   if (r.n_runs == 0) return HK_OK;
-  dim3 grid(r.n_runs, (hidden + 255) / 256);
+  dim3 grid(r.n_runs, (hidden + 63) / 64);
   hipLaunchKernelGGL(rglru_scan_kernel, grid, dim3(256), 0, s, r.slot_ids, r.run_off, x, gi, gr,
                      ldg, gate, ld_gate, a, c_exp, hidden, h_state, out, out_lp, lp_fmt);
   HK_LAUNCH_CHECK();
@@ -1118,10 +1140,16 @@ int mlstm_gates(const Runs& r, const float* if_pre, int n_parts, int64_t part_st
                   reinterpret_cast<uintptr_t>(n_state)) % (4 * per) == 0,
              "mlstm_gates: head size %d needs %d-float aligned rows", hs, per);
   const dim3 grid(r.n_runs * heads), block(64 * nwv);
-#define HK_GATES(W, P)                                                                    \
-  hipLaunchKernelGGL((mlstm_gates_kernel<W, P>), grid, block, 0, s, r.slot_ids, r.run_off, \
-                     if_pre, n_parts, part_stride, heads, qkv, inner, ks, n_state, m_state, ig, \
-                     fg, den)
+  const bool deep = r.max_len > 2 * kGateBlock;
+#define HK_GATES(W, P)                                                                        \
+  if (deep)                                                                                   \
+    hipLaunchKernelGGL((mlstm_gates_kernel<W, P, 4>), grid, block, 0, s, r.slot_ids, r.run_off, \
+                       if_pre, n_parts, part_stride, heads, qkv, inner, ks, n_state, m_state, ig, \
+                       fg, den);                                                              \
+  else                                                                                        \
+    hipLaunchKernelGGL((mlstm_gates_kernel<W, P, 2>), grid, block, 0, s, r.slot_ids, r.run_off, \
+                       if_pre, n_parts, part_stride, heads, qkv, inner, ks, n_state, m_state, ig, \
+                       fg, den)
   if (nwv == 1) {
     HK_GATES(1, 1);
   } else if (nwv == 2) {
