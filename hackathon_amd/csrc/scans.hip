@@ -801,14 +801,11 @@ __global__ void slstm_final_kernel(const int* __restrict__ slot_ids,
 //    butterfly leaves step j's wave sum in lane 8j after 10 shuffles (one
 //    wave sum per step would take 6 dependent shuffles each), and the waves'
 //    sums meet in LDS.
-// The rows of the next NB - 1 blocks are prefetched into a ring of NB
-// register buffers: 4 for launches with runs of more than two blocks (a
-// load takes about as long as three blocks' compute), else 2, since every
-// buffer is filled whether or not the run reaches it; loads are
-// unconditional (rows clamped to the run) so that the compiler's wait
-// counts stay exact.
+// The rows of the next two blocks are prefetched into a register double
+// buffer; loads are unconditional (rows clamped to the run) so that the
+// compiler's wait counts stay exact.
 constexpr int kGateBlock = 8;
-template <int NWV, int PER, int NB>
+template <int NWV, int PER>
 __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
     const int* __restrict__ slot_ids, const int* __restrict__ run_off, const float* __restrict__ if_pre,
     int n_parts, int64_t part_stride, int heads, const float* __restrict__ qkv, int inner, const float* __restrict__ ks,
@@ -857,8 +854,7 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
   // gate pre-activations: lane j < 8 holds i of step j, lane 8 + j holds f
   const int gj = lane & 7;
   const float* gh = if_pre + head + ((lane & 8) ? heads : 0);
-  static_assert(NB >= 2 && NB % 2 == 0, "the LDS sum buffers alternate by block");
-  float rq[NB][B][PER], rk[NB][B][PER], rg[NB];
+  float rq[2][B][PER], rk[2][B][PER], rg[2];
   auto fill = [&](float (&q)[B][PER], float (&k)[B][PER], float& g, int tb) {
 #pragma unroll
     for (int j = 0; j < B; ++j) {
@@ -870,8 +866,8 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
     g = gp[0];
     for (int p = 1; p < n_parts; ++p) g += gp[p * part_stride];
   };
-#pragma unroll
-  for (int b = 0; b < NB - 1; ++b) fill(rq[b], rk[b], rg[b], b * B);
+  fill(rq[0], rk[0], rg[0], 0);
+  fill(rq[1], rk[1], rg[1], B);
 
   auto block = [&](const float (&q)[B][PER], const float (&k)[B][PER], float g, int tb, int par) {
     float ig[B], fg[B], em[B];
@@ -923,18 +919,12 @@ __global__ __launch_bounds__(64 * NWV) void mlstm_gates_kernel(
     }
   };
 
-  // Block u of each group of NB uses buffer u; the loads of the block NB - 1
-  // ahead go into the buffer the previous block used, before this block
-  // runs, so NB - 1 blocks of loads are in flight behind the one computed.
-  for (int tb = 0; tb < len; tb += NB * B) {
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int t = tb + u * B;
-      if (t >= len) break;  // no step of the run left
-      const int nb = (u + NB - 1) % NB;
-      fill(rq[nb], rk[nb], rg[nb], t + (NB - 1) * B);
-      block(rq[u], rk[u], rg[u], t, u & 1);
-    }
+  for (int tb = 0; tb < len; tb += 2 * B) {
+    block(rq[0], rk[0], rg[0], tb, 0);
+    if (tb + B >= len) break;  // the second block would hold no step of the run
+    fill(rq[0], rk[0], rg[0], tb + 2 * B);
+    block(rq[1], rk[1], rg[1], tb + B, 1);
+    fill(rq[1], rk[1], rg[1], tb + 3 * B);
   }
   if (e0 < hs) {
     VecT x;
@@ -1140,16 +1130,10 @@ int mlstm_gates(const Runs& r, const float* if_pre, int n_parts, int64_t part_st
                   reinterpret_cast<uintptr_t>(n_state)) % (4 * per) == 0,
              "mlstm_gates: head size %d needs %d-float aligned rows", hs, per);
   const dim3 grid(r.n_runs * heads), block(64 * nwv);
-  const bool deep = r.max_len > 2 * kGateBlock;
-#define HK_GATES(W, P)                                                                        \
-  if (deep)                                                                                   \
-    hipLaunchKernelGGL((mlstm_gates_kernel<W, P, 4>), grid, block, 0, s, r.slot_ids, r.run_off, \
-                       if_pre, n_parts, part_stride, heads, qkv, inner, ks, n_state, m_state, ig, \
-                       fg, den);                                                              \
-  else                                                                                        \
-    hipLaunchKernelGGL((mlstm_gates_kernel<W, P, 2>), grid, block, 0, s, r.slot_ids, r.run_off, \
-                       if_pre, n_parts, part_stride, heads, qkv, inner, ks, n_state, m_state, ig, \
-                       fg, den)
+#define HK_GATES(W, P)                                                                    \
+  hipLaunchKernelGGL((mlstm_gates_kernel<W, P>), grid, block, 0, s, r.slot_ids, r.run_off, \
+                     if_pre, n_parts, part_stride, heads, qkv, inner, ks, n_state, m_state, ig, \
+                     fg, den)
   if (nwv == 1) {
     HK_GATES(1, 1);
   } else if (nwv == 2) {
