@@ -625,6 +625,11 @@ def bench_gemm(args) -> int:
     syms, counts = ticks[args.warmup]
     run_off = np.concatenate([[0], np.cumsum(np.sort(counts)[::-1])])
     shapes = tick_projections(cfg, run_off)
+    if args.gemm_shape:
+        # one shape alone (the counter summaries' single-shape runs): 32
+        # launches, each with weights of its own
+        m, n, k = (int(v) for v in args.gemm_shape.lower().split("x"))
+        shapes = [(m, n, k)] * 32
     avg_s, each, bytes_, flops = gemm_replay(torch, dev, shapes)
     rf = gemm_roofline(avg_s, bytes_, flops)
     traffic, ratio = counter_traffic(GEMM_COUNTERS, rf["algorithmic_bytes_per_launch"])
@@ -1009,6 +1014,8 @@ def main() -> int:
                          "schedule reach (replayed on the host, filled with zero-valued "
                          "entries); warm-up and timed ticks follow them in the schedule")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemm-shape", default="",
+                    help="gemm: replay one MxNxK shape (32 launches) instead of a tick's GEMMs")
     ap.add_argument("--graph-rows", type=int, default=64,
                     help="c5: ticks of at most this many rows replay cached hipGraphs")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
