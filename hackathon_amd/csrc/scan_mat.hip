@@ -16,6 +16,33 @@ namespace hk {
 namespace {
 
 constexpr int kSteps = 8;  // steps whose row vectors are staged per LDS block
+static_assert(kSteps >= kLogCapMax, "a log fits one staging block");
+
+typedef const __attribute__((address_space(1))) void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+// s_waitcnt with only the vector-memory count constrained to zero (gfx9
+// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+__device__ __forceinline__ void wait_vmem_all() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  __asm__ volatile("" ::: "memory");
+}
+
+// Copies n_chunks 16-byte chunks global -> LDS with global_load_lds, one
+// 1 KB transfer (64 lanes) per instruction, transfers dealt to the NW waves:
+// chunk c lands at LDS byte 16 c of dst, read from src(c). Lanes past the
+// last chunk read chunk 0 again and write the LDS after the used area, which
+// must have room for whole transfers.
+template <int NW, typename Src>
+__device__ __forceinline__ void dma_chunks(float* dst, int n_chunks, int wave, int lane, Src src) {
+  const int n_tr = (n_chunks + 63) / 64;
+  for (int q = wave; q < n_tr; q += NW) {
+    const int c = q * 64 + lane;
+    __builtin_amdgcn_global_load_lds((gptr_t)src(c < n_chunks ? c : 0), (lptr_t)(dst + q * 256),
+                                     16, 0, 0);
+  }
+}
 
 // Raw buffer resource over `bytes` bytes from `base` (gfx9 word 3: 32-bit
 // data format, no stride, no swizzle). A buffer access takes the row offset
@@ -47,6 +74,14 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
   __shared__ __align__(16) float sg[kSteps][CW];     // gamma of this column tile
   __shared__ float sa[kSteps];                       // alpha
   __shared__ __align__(16) float red[2][NW][CW];
+  // The pending log's entries (full tiles: copied global -> LDS while the
+  // tile and the first block's step vectors load, in whole 1 KB transfers).
+  constexpr int kLogB = (kSteps * kRows + 255) / 256 * 256;
+  constexpr int kLogG = (kSteps * CW + 255) / 256 * 256;
+  __shared__ __align__(16) float slb[kLogB];  // [entry][kRows]
+  __shared__ __align__(16) float slg[kLogG];  // [entry][CW]
+  __shared__ float shdr[64];                   // log header: n, F, a_0 ..
+  constexpr bool kLateLog = RPW <= 32;         // log applied in the staging
 
   // Column tile varies fastest in dispatch order: the work-groups of one
   // (run, head) tile stream adjacent segments of the same rows together.
@@ -95,6 +130,22 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
       sw[i / kRows][r] = 0.0f;
     }
   }
+
+  // The pending log's count (a scalar load). Up to 32 rows per wave its
+  // factor and coefficients go global -> LDS (one dword per lane from wave 0,
+  // lanes past the header repeat its last word) and are read from there after
+  // the first staging barrier; with 64 they are scalar loads.
+  int log_n = 0;
+  bool defer = false;
+  const float* lh = d.log_hdr + ((int64_t)slot * d.heads + head) * kLogHdr;
+  if (d.log_cap > 0) {
+    log_n = (int)lh[0];
+    defer = log_n + len <= d.log_cap;
+    if (kLateLog && wave == 0 && log_n > 0)
+      __builtin_amdgcn_global_load_lds((gptr_t)(lh + (lane < kLogHdr ? lane : kLogHdr - 1)),
+                                       (lptr_t)shdr, 4, 0, 0);
+  }
+  const int64_t le0 = ((int64_t)slot * d.heads + head) * d.log_cap;  // first log entry
 
   // Uniform tile base (scalar registers) + 32-bit per-lane offsets: a tile
   // spans well under 2^32 elements, and this keeps 64-bit address math out
@@ -145,20 +196,42 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
     }
   }
 
-  // ---- deferred write-back: materialise the tile from B and the log
+  // ---- deferred write-back: the tile is materialised from B and the log
   // (s = F s, then s = fma(b_j, a_j g_j, s) in entry order, as mat_log_flush
-// does)
-  int log_n = 0;
-  bool defer = false;
-  if (d.log_cap > 0) {
-    const float* lh = d.log_hdr + ((int64_t)slot * d.heads + head) * kLogHdr;
-    log_n = (int)lh[0];
-    defer = log_n + len <= d.log_cap;
-    if (log_n > 0) {
-      const float F = lh[1];
-      const int64_t le = ((int64_t)slot * d.heads + head) * d.log_cap;
-      const float* lb = d.log_b + le * d.rows + row_off;
-      const float* lg = d.log_g + le * d.cols + col0;
+  // does). The entries reach LDS behind the tile's loads: full tiles by
+  // global -> LDS transfers, other tiles by loads (rows past the part's rows
+  // zero). Up to 32 rows per wave the log is applied after the first staging
+  // barrier, so the step vectors' loads overlap it; with 64 the registers
+  // held across the staging do not fit beside the tile, and it is applied
+  // here with plain loads.
+  if (log_n > 0) {
+    const float* lb = d.log_b + le0 * d.rows + row_off;
+    const float* lg = d.log_g + le0 * d.cols + col0;
+    if constexpr (kLateLog) {
+      if constexpr (FULL) {
+        constexpr int bq = kRows / 4;  // chunks per entry (prows == kRows)
+        constexpr int gq = CW / 4;
+        dma_chunks<NW>(slb, log_n * bq, wave, lane, [&](int c) {
+          const int j = c / bq;
+          return lb + (int64_t)j * d.rows + 4 * (c - j * bq);
+        });
+        dma_chunks<NW>(slg, log_n * gq, wave, lane, [&](int c) {
+          const int j = c / gq;
+          return lg + (int64_t)j * d.cols + 4 * (c - j * gq);
+        });
+      } else {
+        for (int i = tid; i < log_n * kRows; i += NT) {
+          const int j = i / kRows;
+          const int r = i - j * kRows;
+          slb[i] = r < prows ? lb[(int64_t)j * d.rows + r] : 0.0f;
+        }
+        for (int i = tid; i < log_n * CW; i += NT) {
+          const int j = i / CW;
+          const int c = i - j * CW;
+          slg[i] = col0 + c < d.cols ? lg[(int64_t)j * d.cols + c] : 0.0f;
+        }
+      }
+    } else {
       for (int i = tid; i < log_n * prows; i += NT) {
         const int j = i / prows;
         sb[j][i - j * prows] = lb[(int64_t)j * d.rows + (i - j * prows)];
@@ -169,6 +242,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
         sg[j][c] = col0 + c < d.cols ? lg[(int64_t)j * d.cols + c] : 0.0f;
       }
       lds_barrier();
+      const float F = lh[1];
       for (int j = 0; j < log_n; ++j) {
         const float a = lh[2 + j];
         const float f = j == 0 ? F : 1.0f;
@@ -253,7 +327,27 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
       const int64_t row = row0 + tid;
       sa[tid] = d.alpha.ptr[row * d.alpha.row_stride + head * d.alpha.head_stride];
     }
+    // the log's transfers (this wave's) are in LDS before the barrier
+    if (kLateLog && log_n > 0 && t0 == 0) wait_vmem_all();
     lds_barrier();
+    if (kLateLog && log_n > 0 && t0 == 0) {
+      for (int j = 0; j < log_n; ++j) {
+        const float a = shdr[2 + j];
+        const float f = j == 0 ? shdr[1] : 1.0f;
+        float gj[VW];
+#pragma unroll
+        for (int v = 0; v < VW; ++v) gj[v] = a * slg[j * CW + lane * VW + v];
+#pragma unroll
+        for (int i = 0; i < RPW; i += 4) {
+          const float4 bv = *reinterpret_cast<const float4*>(&slb[j * kRows + rbase + i]);
+          const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int v = 0; v < VW; ++v) s[i + k][v] = fmaf(bb[k], gj[v], f * s[i + k][v]);
+        }
+      }
+    }
 
     // ---- advance the tile through the staged steps
     for (int st = 0; st < ns; ++st) {
@@ -297,7 +391,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 8 && RPW == 64) ? 4 : 1) void mat_s
     // B stays; the run's steps (len <= log_cap <= kSteps: all in the one
     // staging block, still in LDS) become log entries log_n .. log_n+len-1.
     // Column tile 0 writes each part's rows of b; part 0 each tile's g.
-    const int64_t le = ((int64_t)slot * d.heads + head) * d.log_cap + log_n;
+    const int64_t le = le0 + log_n;
     if (blockIdx.x == 0) {
       float* lb = d.log_b + le * d.rows + row_off;
       for (int i = tid; i < len * prows; i += NT) {
