@@ -132,7 +132,8 @@ def l1_l2_reads(path, avg_s):
             "bytes_per_cu_per_clk": b / avg_s / N_CUS / CU_CLOCK_HZ,
             "source": os.path.relpath(path, os.path.dirname(PROFILES)),
             "note": "the kernel's bound: L1 -> L2 line reads (W once per row tile, A once per "
-                    "column tile) at a per-CU rate capped by the L1's in-flight request limit"}
+                    "column tile) at the rate each CU's vector-memory pipeline takes the "
+                    "slab loop's loads"}
 
 
 def counter_traffic(path, algorithmic_per_dispatch):
