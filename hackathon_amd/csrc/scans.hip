@@ -648,13 +648,16 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
       float* half = kh == 0 ? gsum : xbuf;
       if constexpr (kF16) {
         // G = W . H as hi*hi + (hi*lo + lo*hi) over this k half, every
-        // chunk size (columns fr >= nj read stale LDS rows; their results
-        // are dropped), then unscaled (powers of two: exact).
+        // chunk size, then unscaled (powers of two: exact). Columns fr >= nj
+        // read run 0's row again (their results are dropped): lanes reading
+        // one address share an LDS access, so a chunk of few runs reads
+        // little more than its own rows.
         // four accumulator chains (hi.hi of even and of odd k-steps, hi.lo,
         // lo.hi), so consecutive matrix instructions seldom wait on each other
         floatx4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, c0 = a0, c1 = a0;
-        const _Float16* bh = hhi + fr * PADH + kh * KH + 8 * fk;
-        const _Float16* bl = hlo + fr * PADH + kh * KH + 8 * fk;
+        const int fb = fr < nj ? fr : 0;
+        const _Float16* bh = hhi + fb * PADH + kh * KH + 8 * fk;
+        const _Float16* bl = hlo + fb * PADH + kh * KH + 8 * fk;
 #pragma unroll
         for (int q = 0; q < KS; ++q) {
           const halfx8_t b_hi = *reinterpret_cast<const halfx8_t*>(bh + 32 * q);
@@ -672,11 +675,12 @@ __global__ __launch_bounds__(kPersistThreads) void slstm_persist_kernel(SlstmPer
             make_float4(acc[0] * inv_row[0], acc[1] * inv_row[1], acc[2] * inv_row[2],
                         acc[3] * inv_row[3]);
       } else if (nj > kValuRuns) {
-        // Columns fr >= nj read stale LDS rows; their results are dropped.
-        // Four independent accumulator chains (one per step c of a group),
-        // summed at the end, so consecutive MFMAs do not wait on each other.
+        // Columns fr >= nj read run 0's row again (one shared LDS access);
+        // their results are dropped. Four independent accumulator chains
+        // (one per step c of a group), summed at the end, so consecutive
+        // MFMAs do not wait on each other.
         floatx4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0, a2 = a0, a3 = a0;
-        const float* hb = hbuf + fr * PAD + kh * KH + 4 * fk;
+        const float* hb = hbuf + (fr < nj ? fr : 0) * PAD + kh * KH + 4 * fk;
 #pragma unroll
         for (int g = 0; g < KG; ++g) {
           const float4 hv = *reinterpret_cast<const float4*>(hb + 16 * g);
