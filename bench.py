@@ -396,6 +396,19 @@ def _timed_ticks(torch, eng, packed, feats, preds, dev):
     return t1 - t0, np.array([a.elapsed_time(b) * 1000.0 for a, b in ev])
 
 
+def _sync_ticks(torch, eng, packed, feats, preds):
+    """One tick at a time: per-tick latency (µs) from the host's call to the
+    tick's completion (a synchronisation before and after each tick)."""
+    lat = []
+    for r, x in zip(packed, feats):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.tick(r, x, preds[: r.n_rows])
+        torch.cuda.synchronize()
+        lat.append((time.perf_counter() - t0) * 1e6)
+    return np.array(lat)
+
+
 def _lat_stats(lat, rows, small):
     sel = rows <= small
     out = {"p50_us": float(np.percentile(lat, 50)), "p99_us": float(np.percentile(lat, 99))}
@@ -458,11 +471,24 @@ def bench_c5(args) -> int:
     tot, lat = _timed_ticks(torch, eng, packed[W:], feats[W:], preds, dev)
     info1 = eng.graph_info()
     eng.check()
+    small = [i for i in range(W, W + K) if packed[i].n_rows <= G]
+    sync_g = _sync_ticks(torch, eng, [packed[i] for i in small], [feats[i] for i in small], preds)
+    eng.check()
     eng.graphs(0)
     tot_off, lat_off = _timed_ticks(torch, eng, packed[W:], feats[W:], preds, dev)
     eng.check()
+    sync_e = _sync_ticks(torch, eng, [packed[i] for i in small], [feats[i] for i in small], preds)
+    eng.check()
     assert torch.isfinite(preds).all()
     rows = np.array([r.n_rows for r in packed[W:]])
+    sync = {"ticks": len(small),
+            "note": f"the timed sequence's ticks of at most {G} rows again, one at a time, from "
+                    "the host's call to the tick's completion"}
+    if small:
+        sync["graphs"] = {"p50_us": float(np.percentile(sync_g, 50)),
+                          "p99_us": float(np.percentile(sync_g, 99))}
+        sync["eager"] = {"p50_us": float(np.percentile(sync_e, 50)),
+                         "p99_us": float(np.percentile(sync_e, 99))}
     reqs = int(rows.sum())
     line = {
         "metric": "C5 stress: requests/sec at 8192 symbols, B~U(1..512); p50/p99 tick latency (us)",
@@ -485,6 +511,7 @@ def bench_c5(args) -> int:
                    "replays_timed": info1["replays"] - info0["replays"]},
         "graphs_off": {"value": reqs / tot_off, "ms_per_step": 1000.0 * tot_off / K,
                        **_lat_stats(lat_off, rows, G)},
+        "sync_latency_small_ticks": sync,
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -783,9 +810,14 @@ def bench_latency(args) -> int:
         eng.tick(packed[i], feats[i], preds)
     tot, lat = _timed_ticks(torch, eng, packed[W:], feats[W:], preds, dev)
     eng.check()
+    n_sync = min(K, 50)
+    sync_g = _sync_ticks(torch, eng, packed[W:W + n_sync], feats[W:W + n_sync], preds)
+    eng.check()
     info = eng.graph_info()
     eng.graphs(0)
     tot_off, lat_off = _timed_ticks(torch, eng, packed[W:], feats[W:], preds, dev)
+    eng.check()
+    sync_e = _sync_ticks(torch, eng, packed[W:W + n_sync], feats[W:W + n_sync], preds)
     eng.check()
     # HBM floor of a tick: the weights once (CastLinear weights in bf16,
     # the rest fp32) and every touched symbol's state read and written once.
@@ -815,6 +847,14 @@ def bench_latency(args) -> int:
         "graphs_off": {"p50_us": float(np.percentile(lat_off, 50)),
                        "p99_us": float(np.percentile(lat_off, 99)),
                        "requests_per_s": K * B / tot_off},
+        "sync_latency": {"ticks": n_sync,
+                         "graphs": {"p50_us": float(np.percentile(sync_g, 50)),
+                                    "p99_us": float(np.percentile(sync_g, 99))},
+                         "eager": {"p50_us": float(np.percentile(sync_e, 50)),
+                                   "p99_us": float(np.percentile(sync_e, 99))},
+                         "note": "one tick at a time, from the host's call to the tick's "
+                                 "completion; p50_us / p99_us above are HIP-event spans of "
+                                 "back-to-back ticks on the caller's stream"},
         "floor": {"weight_bytes": w_bytes, "state_bytes_per_symbol": state_bytes,
                   "floor_us": floor_s * 1e6, "p50_over_floor": float(np.percentile(lat, 50)) / (floor_s * 1e6),
                   "note": "HBM floor = weights once + 2 x 64 x state bytes per symbol, at 8 TB/s"},

@@ -17,18 +17,24 @@
 //   pred[tower] = output_proj(x)                          (shared weights)
 #include <algorithm>
 #include <cmath>
+#include <condition_variable>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
+#include <functional>
 #include <map>
 #include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "common.h"
 #include "gemm.h"
 #include "ops.h"
 #include "scan_mat.h"
+
+extern "C" const char* hk_last_error(void);  // api_ops.hip: this thread's last error text
 
 namespace hk {
 namespace {
@@ -262,6 +268,98 @@ struct TowerWS {
   GemmWorkspace gemm_ws;
 };
 
+// Host threads that enqueue the side streams' share of a tick. A kernel
+// launch costs the calling thread ~2.6 us in the HIP runtime, so one thread
+// spends ~2 ms on a tick's ~700 launches, longer than a small tick runs on
+// the GPU; launches to different streams from different threads go through
+// the runtime concurrently (four threads: ~0.9 us per launch in all).
+// Worker i runs the task posted for it; wait() returns once every posted
+// task has finished, with each task's status and error text.
+class EnqueuePool {
+ public:
+  EnqueuePool(int device, int n) : w_(n) {
+    for (int i = 0; i < n; ++i) w_[i].th = std::thread([this, device, i] { loop(device, i); });
+  }
+  ~EnqueuePool() {
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    for (auto& w : w_) w.th.join();
+  }
+  int size() const { return (int)w_.size(); }
+  void post(int i, std::function<int()> fn) {
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      w_[i].fn = std::move(fn);
+      w_[i].has = true;
+      w_[i].st = HK_OK;
+      w_[i].err.clear();
+      ++pending_;
+    }
+    cv_.notify_all();
+  }
+  // The first failing task's status (its error text in *err), else HK_OK.
+  int wait(std::string* err) {
+    std::unique_lock<std::mutex> lk(mu_);
+    done_.wait(lk, [this] { return pending_ == 0; });
+    for (auto& w : w_)
+      if (w.st != HK_OK) {
+        *err = w.err;
+        return w.st;
+      }
+    return HK_OK;
+  }
+
+ private:
+  struct Worker {
+    std::thread th;
+    std::function<int()> fn;
+    bool has = false;
+    int st = HK_OK;
+    std::string err;
+  };
+  void loop(int device, int i) {
+    const hipError_t dev_st = hipSetDevice(device);
+    for (;;) {
+      std::function<int()> fn;
+      {
+        std::unique_lock<std::mutex> lk(mu_);
+        cv_.wait(lk, [&] { return stop_ || w_[i].has; });
+        if (!w_[i].has) return;  // stop_ with nothing posted
+        fn = std::move(w_[i].fn);
+        w_[i].has = false;
+      }
+      int st;
+      std::string err;
+      if (dev_st != hipSuccess) {
+        st = HK_ERR_HIP;
+        err = std::string("enqueue thread: hipSetDevice: ") + hipGetErrorString(dev_st);
+      } else {
+        try {
+          st = fn();
+          if (st != HK_OK) err = hk_last_error();
+        } catch (const std::exception& ex) {
+          st = HK_ERR_HIP;
+          err = std::string("enqueue thread: ") + ex.what();
+        }
+      }
+      {
+        std::lock_guard<std::mutex> lk(mu_);
+        w_[i].st = st;
+        w_[i].err = std::move(err);
+        if (--pending_ == 0) done_.notify_all();
+      }
+    }
+  }
+  std::vector<Worker> w_;
+  std::mutex mu_;
+  std::condition_variable cv_, done_;
+  int pending_ = 0;
+  bool stop_ = false;
+};
+
 }  // namespace
 
 struct Engine {
@@ -361,8 +459,12 @@ struct Engine {
   int prof = 0;  // bit k: time launches of kind k
   std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[5];
   size_t prof_used[5] = {0, 0, 0, 0, 0};
+  // Threads enqueueing the side streams' launches (created on the first
+  // tick that uses them).
+  std::unique_ptr<EnqueuePool> pool;
 
   ~Engine() {
+    pool.reset();
     for (auto& kv : graphs)
       for (auto& x : kv.second.exec)
         if (x) (void)hipGraphExecDestroy(x);
@@ -1036,6 +1138,63 @@ int run_towers(Engine& e, const Group& all, const Group& g1, const Group* g2, hi
   return HK_OK;
 }
 
+// One xLSTM run group's tower on stream s.
+int xlstm_stream(Engine& e, TowerWS& w, const Group& g, unsigned long long* xch, float* preds,
+                 hipStream_t s) {
+  HK_TRY(tower_head(e, kXLSTM, w, g, s));
+  for (int l = 0; l < e.d.D; ++l) HK_TRY(tower_layer(e, kXLSTM, w, g, l, xch, SlOrder{}, s));
+  return tower_tail(e, kXLSTM, w, g, preds, s);
+}
+
+// Mamba2 on side[1].
+int mamba2_stream(Engine& e, const Group& all, float* preds) {
+  hipStream_t s = e.side[1];
+  TowerWS& w = e.ws[kMamba2];
+  HK_TRY(tower_head(e, kMamba2, w, all, s));
+  for (int l = 0; l < e.d.D; ++l) HK_TRY(tower_layer(e, kMamba2, w, all, l, nullptr, SlOrder{}, s));
+  return tower_tail(e, kMamba2, w, all, preds, s);
+}
+
+// RetNet and Hawk, layer by layer, on side[2].
+int retnet_hawk_stream(Engine& e, const Group& all, float* preds) {
+  hipStream_t s = e.side[2];
+  HK_TRY(tower_head(e, kRetNet, e.ws[kRetNet], all, s));
+  HK_TRY(tower_head(e, kHawk, e.ws[kHawk], all, s));
+  for (int l = 0; l < e.d.D; ++l) {
+    HK_TRY(tower_layer(e, kRetNet, e.ws[kRetNet], all, l, nullptr, SlOrder{}, s));
+    HK_TRY(tower_layer(e, kHawk, e.ws[kHawk], all, l, nullptr, SlOrder{}, s));
+  }
+  HK_TRY(tower_tail(e, kRetNet, e.ws[kRetNet], all, preds, s));
+  return tower_tail(e, kHawk, e.ws[kHawk], all, preds, s);
+}
+
+// The work of run_towers with each side stream's launches enqueued by a
+// thread of its own while this thread enqueues the first xLSTM group's. Only
+// for ticks whose streams need no cross-stream order inside the tick (the
+// two groups' persistent sLSTM launches fit side by side); the enqueue order
+// within each stream is run_towers'. Returns 1 (nothing enqueued) when the
+// threads cannot be started.
+int run_towers_mt(Engine& e, const Group& all, const Group& g1, const Group* g2, hipStream_t s,
+                  float* preds) {
+  if (!e.pool) {
+    try {
+      e.pool = std::make_unique<EnqueuePool>(e.device, Engine::kSide);
+    } catch (...) {
+      return 1;
+    }
+  }
+  EnqueuePool& p = *e.pool;
+  if (g2) p.post(0, [&] { return xlstm_stream(e, e.ws_x2, *g2, e.d_xch2, preds, e.side[0]); });
+  p.post(1, [&] { return mamba2_stream(e, all, preds); });
+  p.post(2, [&] { return retnet_hawk_stream(e, all, preds); });
+  const int st = xlstm_stream(e, e.ws[kXLSTM], g1, e.d_xch, preds, s);
+  std::string err;
+  const int wst = p.wait(&err);  // the threads use e, all, g1, g2 until here
+  if (st != HK_OK) return st;
+  if (wst != HK_OK) set_error("%s", err.c_str());
+  return wst;
+}
+
 // Where to split the length-sorted runs into two xLSTM groups (returns
 // n_runs for no split). Per layer a group costs about kStepUs per sLSTM step
 // of its longest run plus kSymbolUs per symbol for the mLSTM state traffic;
@@ -1081,8 +1240,9 @@ int enqueue_tick(Engine& e, const TickShape& sh, const float* features_dev, floa
   HK_TRY(stage_features(features_dev, sh.n_rows, e.d.F, e.d.Fpad, e.FE.f, e.FE.l, e.lp_fmt, s));
   HK_CHECK_HIP(hipEventRecord(e.fork_ev, s));
   for (int i = 0; i < Engine::kSide; ++i) HK_CHECK_HIP(hipStreamWaitEvent(e.side[i], e.fork_ev, 0));
-  if (sh.split < sh.n_runs) {
-    Group g1, g2;
+  const bool split = sh.split < sh.n_runs;
+  Group g1, g2;
+  if (split) {
     g1.r = Runs{e.d_slots, e.d_off, sh.split, sh.row_split, sh.steps, e.d_pos, e.d_rslot};
     g1.act_dev = e.d_act1;
     g1.act = sh.act1;
@@ -1091,10 +1251,16 @@ int enqueue_tick(Engine& e, const TickShape& sh, const float* features_dev, floa
     g2.act_dev = e.d_act2;
     g2.act = sh.act2;
     g2.row0 = sh.row_split;
-    HK_TRY(run_towers(e, all, g1, &g2, s, preds_dev));
-  } else {
-    HK_TRY(run_towers(e, all, all, nullptr, s, preds_dev));
   }
+  const Group& first = split ? g1 : all;
+  const Group* second = split ? &g2 : nullptr;
+  // Threads enqueue the streams' launches unless the tick is being captured
+  // or profiled, or the groups' sLSTM launches alternate across streams.
+  int st = 1;
+  if (!e.capturing && e.prof == 0 && e.d_trace == nullptr && (!split || e.sl_overlap))
+    st = run_towers_mt(e, all, first, second, s, preds_dev);
+  if (st == 1) st = run_towers(e, all, first, second, s, preds_dev);
+  HK_TRY(st);
   for (int i = 0; i < Engine::kSide; ++i) {
     HK_CHECK_HIP(hipEventRecord(e.join_ev[i], e.side[i]));
     HK_CHECK_HIP(hipStreamWaitEvent(s, e.join_ev[i], 0));

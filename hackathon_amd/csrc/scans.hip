@@ -2,6 +2,7 @@
 // in order, carrying that symbol's small recurrent state in registers, so the
 // state is read once and written once per tick.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "ops.h"
@@ -1015,21 +1016,26 @@ bool slstm_persist_supported(int hidden, int heads) {
 template <int HS, bool SPLIT>
 int launch_persist(const SlstmPersistArgs& a, size_t smem, hipStream_t s) {
   const dim3 grid(a.heads * (HS / 16)), block(kPersistThreads);
-  // per process (one device type), for the last LDS size asked for
+  // per process (one device type), for the last LDS size asked for; two
+  // threads may launch at once (the engine's two xLSTM run groups)
+  static std::mutex mu;
   static int cus = -1;
   static size_t fits_smem = 0;
   static int64_t fits = -1;
-  if (cus < 0) {
-    int dev = 0;
-    HK_CHECK_HIP(hipGetDevice(&dev));
-    HK_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  }
-  if (fits < 0 || smem != fits_smem) {
-    int per_cu = 0;
-    HK_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, slstm_persist_kernel<HS, SPLIT>, kPersistThreads, smem));
-    fits = (int64_t)cus * per_cu;
-    fits_smem = smem;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    if (cus < 0) {
+      int dev = 0;
+      HK_CHECK_HIP(hipGetDevice(&dev));
+      HK_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    }
+    if (fits < 0 || smem != fits_smem) {
+      int per_cu = 0;
+      HK_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, slstm_persist_kernel<HS, SPLIT>, kPersistThreads, smem));
+      fits = (int64_t)cus * per_cu;
+      fits_smem = smem;
+    }
   }
   HK_REQUIRE((int64_t)grid.x <= fits, "slstm_persist: %u work-groups cannot be co-resident (%d)",
              grid.x, fits);
