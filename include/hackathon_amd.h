@@ -252,7 +252,10 @@ int hk_engine_log_fill(void* handle, const int* slots_host, const int* counts_ho
  * fp32, preds_dev [n_rows, 4] (one column per tower). Equivalent to the
  * reference's rounds (example_model.py:885-899), each a masked forward +
  * _blend_state (example_model.py:400-429, :907-949). Returns -3 when the
- * tick exceeds max_rows / max_runs. */
+ * tick exceeds max_rows / max_runs. The side streams' launches are enqueued
+ * by three engine-owned host threads (started on the first tick) while the
+ * calling thread enqueues its stream's; the call returns once all are
+ * enqueued. Not reentrant: one calling thread per engine at a time. */
 int hk_engine_tick(void* handle, const int* slot_ids_host, const int* run_off_host, int n_runs,
                    const float* features_dev, float* preds_dev, void* stream);
 
