@@ -268,7 +268,10 @@ int hk_engine_tick(void* handle, const int* slot_ids_host, const int* run_off_ho
  * evicted; hk_engine_tick then enqueues one copy in, one graph launch and
  * one copy out. Results are bit-identical to the eager tick's. max_rows 0
  * (the default) enqueues every tick's kernels eagerly and frees the cache.
- * Not used while hk_engine_profile records. */
+ * Not used while hk_engine_profile records. The graph launch replays its
+ * nodes from the calling thread, so one tick at a time a replayed tick ends
+ * later than an eager one (whose side streams are enqueued by the engine's
+ * threads); back to back they run alike. */
 int hk_engine_graphs(void* handle, int max_rows, int max_graphs);
 
 /* Shapes cached, graphs captured and ticks replayed so far. No reference
