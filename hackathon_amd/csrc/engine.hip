@@ -278,16 +278,14 @@ struct TowerWS {
 class EnqueuePool {
  public:
   EnqueuePool(int device, int n) : w_(n) {
-    for (int i = 0; i < n; ++i) w_[i].th = std::thread([this, device, i] { loop(device, i); });
-  }
-  ~EnqueuePool() {
-    {
-      std::lock_guard<std::mutex> lk(mu_);
-      stop_ = true;
+    try {
+      for (int i = 0; i < n; ++i) w_[i].th = std::thread([this, device, i] { loop(device, i); });
+    } catch (...) {
+      shutdown();  // the threads already started end before the error goes on
+      throw;
     }
-    cv_.notify_all();
-    for (auto& w : w_) w.th.join();
   }
+  ~EnqueuePool() { shutdown(); }
   int size() const { return (int)w_.size(); }
   void post(int i, std::function<int()> fn) {
     {
@@ -320,6 +318,15 @@ class EnqueuePool {
     int st = HK_OK;
     std::string err;
   };
+  void shutdown() {
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    for (auto& w : w_)
+      if (w.th.joinable()) w.th.join();
+  }
   void loop(int device, int i) {
     const hipError_t dev_st = hipSetDevice(device);
     for (;;) {
