@@ -286,7 +286,6 @@ class EnqueuePool {
     }
   }
   ~EnqueuePool() { shutdown(); }
-  int size() const { return (int)w_.size(); }
   void post(int i, std::function<int()> fn) {
     {
       std::lock_guard<std::mutex> lk(mu_);
