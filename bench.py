@@ -624,6 +624,39 @@ def gemm_replay(torch, dev, shapes, reps=3, min_work_groups=0):
     return seq_avg_s, each, bytes_, flops
 
 
+def vendor_gemm_replay(torch, dev, shapes, reps=3):
+    """The same GEMM sequence through the vendor library, for comparison:
+    torch.nn.functional.linear in bf16 with a bf16 bias (hipBLASLt on
+    ROCm), row-major weights of their own per launch (streamed from HBM as
+    in gemm_replay). Returns the average launch duration over `reps`
+    back-to-back passes. Its output is bf16 (half the bytes of the engine
+    kernel's fp32 output)."""
+    F = torch.nn.functional
+    g = torch.Generator(device=dev).manual_seed(1)
+    Mmax = max(m for m, _, _ in shapes)
+    Kmax = max(k for _, _, k in shapes)
+    x = (torch.randn(Mmax, Kmax, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    weights = [((torch.rand(n, k, device=dev, generator=g) - 0.5) * k ** -0.5).to(torch.bfloat16)
+               for _, n, k in shapes]
+    biases = {n: torch.zeros(n, dtype=torch.bfloat16, device=dev) for _, n, _ in shapes}
+    xs = {(m, k): x[:m, :k] for m, _, k in shapes}
+    for (m, n, k), w in zip(shapes, weights):
+        F.linear(xs[(m, k)], w, biases[n])
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(reps):
+        for (m, n, k), w in zip(shapes, weights):
+            F.linear(xs[(m, k)], w, biases[n])
+    e1.record(cur)
+    torch.cuda.synchronize()
+    avg_s = e0.elapsed_time(e1) * 1e-3 / (reps * len(shapes))
+    del weights
+    torch.cuda.empty_cache()
+    return avg_s
+
+
 def gemm_roofline(avg_s, bytes_, flops):
     """Roofline of a GEMM sequence from its average launch duration."""
     t = avg_s * len(bytes_)
@@ -660,6 +693,7 @@ def bench_gemm(args) -> int:
         shapes = [(m, n, k)] * 32
     avg_s, each, bytes_, flops = gemm_replay(torch, dev, shapes)
     rf = gemm_roofline(avg_s, bytes_, flops)
+    vrf = gemm_roofline(vendor_gemm_replay(torch, dev, shapes), bytes_, flops)
     traffic, ratio = counter_traffic(GEMM_COUNTERS, rf["algorithmic_bytes_per_launch"])
     line = {
         "metric": "CastLinear GEMM replay of one ensemble tick: achieved HBM bandwidth",
@@ -680,6 +714,10 @@ def bench_gemm(args) -> int:
                      "l1_l2": l1_l2_reads(GEMM_L1_L2, rf["avg_us"] * 1e-6), **rf},
         "event_bracketed_us_by_shape": {f"{m}x{n}x{k}": round(1e6 * float(t), 2)
                                         for (m, n, k), t in zip(shapes[:12], each[:12])},
+        "vendor_library": {"avg_us": vrf["avg_us"], "achieved": vrf["achieved_GBs"],
+                           "frac": vrf["hbm_frac"],
+                           "note": "torch.nn.functional.linear (hipBLASLt), bf16 output and "
+                                   "bias, weights streamed the same way"},
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -1224,6 +1262,8 @@ def main() -> int:
     # (at least 112 work-groups: three other streams share the device).
     t_avg, _, _, _ = gemm_replay(torch, dev, shapes, min_work_groups=TICK_MIN_WORK_GROUPS)
     trf = gemm_roofline(t_avg, g_bytes, g_flops)
+    v_avg = vendor_gemm_replay(torch, dev, shapes)
+    vrf = gemm_roofline(v_avg, g_bytes, g_flops)
 
     # The serving path on the same engine: NnInferenceClient.process_batch
     # on dicts of request objects (the reference's interface), wall clock
@@ -1315,6 +1355,11 @@ def main() -> int:
                                "note": "the same replay with the tile rule the engine uses "
                                        "inside a tick (larger tiles: the tick is faster, the "
                                        "lone GEMM slower)"},
+            "vendor_library": {"avg_us": vrf["avg_us"], "achieved": vrf["achieved_GBs"],
+                               "frac": vrf["hbm_frac"],
+                               "note": "the same 250 GEMMs through torch.nn.functional.linear "
+                                       "(hipBLASLt, bf16 output and bias), weights streamed "
+                                       "the same way; frac on the same algorithmic bytes"},
             "secondary": {"mlstm_scan_isolated": isolated_mlstm_scan(torch, dev)},
         },
         "kernels": kernels,
