@@ -416,6 +416,7 @@ struct Engine {
   unsigned int xch_tag[2] = {0, 0};      // tag of the last eager sLSTM launch on d_xch / d_xch2
   unsigned int graph_tag_next = 0x80000000u;
   bool sl_overlap = false;  // the two groups' persistent launches can be co-resident together
+  double x_weight_us = 0.0;  // one xLSTM layer's weights read at 5 TB/s (the split rule's cost)
   int* d_err = nullptr;      // [1]: set by a kernel whose barrier timed out
   uint64_t* d_trace = nullptr;  // HK_TRACE_SLSTM: per-step stamps of layer 0's sLSTM
   int* h_stage = nullptr;    // pinned [2][stage_ints()]
@@ -1204,10 +1205,13 @@ int run_towers_mt(Engine& e, const Group& all, const Group& g1, const Group* g2,
 // Where to split the length-sorted runs into two xLSTM groups (returns
 // n_runs for no split). Per layer a group costs about kStepUs per sLSTM step
 // of its longest run plus kSymbolUs per symbol for the mLSTM state traffic;
-// the two groups run concurrently, so a split pays when the larger of the
-// two costs is well below the unsplit cost (each group also reads every
-// projection weight, hence the margin).
-int xlstm_split_point(const int* run_off, int n_runs) {
+// the two groups run concurrently, but each reads every weight of the layer
+// (weight_us, the layer's weight bytes at 5 TB/s), so a split pays when the
+// larger of the two costs plus that second read is well below the unsplit
+// cost. (Four one-request symbols in fp32 (C1): unsplit 23 us against 13 +
+// 41 split, measured 3.90 against 4.10 ms per step; 256 Zipf requests in
+// bf16 (C4): about 1000 against 500 + 24.)
+int xlstm_split_point(const int* run_off, int n_runs, double weight_us) {
   constexpr double kStepUs = 3.0, kSymbolUs = 5.0, kGain = 0.8;
   if (n_runs < 2) return n_runs;
   const int len0 = run_off[1] - run_off[0];
@@ -1217,7 +1221,8 @@ int xlstm_split_point(const int* run_off, int n_runs) {
   for (int k = 1; k < n_runs; ++k) {
     const int lenk = run_off[k + 1] - run_off[k];
     const double c = std::max(kStepUs * len0 + kSymbolUs * k,
-                              kStepUs * lenk + kSymbolUs * (n_runs - k));
+                              kStepUs * lenk + kSymbolUs * (n_runs - k)) +
+                     weight_us;
     if (c < best) {
       best = c;
       best_k = k;
@@ -1435,6 +1440,12 @@ int hk_engine_create(const int* cfg, int n_cfg, void** out) {
           hk::set_error("hk_engine_create: out of device memory for weights");
           return HK_ERR_HIP;
         }
+  {
+    double bytes = 0.0;
+    for (const auto& s : e->slots[hk::kXLSTM][1])
+      bytes += (double)s.def.numel * (s.def.lp && e->lowp ? 2 : 4);
+    e->x_weight_us = bytes / 5.0e6;
+  }
   for (auto& s : e->gslots)
     if (!alloc_slot(s)) {
       hk::set_error("hk_engine_create: out of device memory for weights");
@@ -1853,7 +1864,7 @@ int hk_engine_tick(void* h, const int* slot_ids_host, const int* run_off_host, i
   HK_CHECK_HIP(hipEventSynchronize(e.stage_done[k]));
   const int steps = run_off_host[1] - run_off_host[0];
   // xLSTM run groups: runs [0, split) and [split, n_runs).
-  const int split = hk::xlstm_split_point(run_off_host, n_runs);
+  const int split = hk::xlstm_split_point(run_off_host, n_runs, e.x_weight_us);
   const int row_split = run_off_host[split];
   const int steps2 = split < n_runs ? run_off_host[split + 1] - run_off_host[split] : 0;
   int* stage = e.h_stage + (size_t)k * e.stage_ints();

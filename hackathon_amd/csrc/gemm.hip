@@ -493,6 +493,118 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
   }
 }
 
+// Skinny fp32 products: at most 16 rows of A (kSkinnyRows), e.g. the fp32
+// mode's four symbols, one request each. The 64x64 tile above would stage
+// and multiply 64 rows of A per slab for these, and its split-K partial sums
+// add a chain of dependent round trips (store, counter, reload) to every
+// launch; the product is a stream of W. Here a work-group of 16 waves owns
+// 16 output columns and all of K: the waves take interleaved 16-deep k steps
+// (together 1 KB of each W row per round), each step one A fragment and one
+// W fragment loaded straight into registers (16 rows x 64 bytes each) and
+// four v_mfma_f32_16x16x4f32 (A rows past M read row 0; their outputs are
+// never stored). Two steps per round; a round past a wave's last step loads
+// its first step again and skips the products, so every load is unconditional.
+// The waves' sums meet in LDS and are added in wave order (deterministic).
+// (Measured alone, M = 4, W streamed from HBM, microseconds per launch:
+// 8192x2048 17.3, 2048x4096 14.9, 4096x2048 9.7, 8448x2048 22.6, 2048x2048
+// 8.9, 64x2048 8.2; with K split to fill the device as gemm_kernel does,
+// 22.8, 20.7, 17.4, 27.1, 18.8, 14.7: the split's round trips cost more than
+// its parallelism gains.)
+constexpr int kSkinnyRows = 16;
+constexpr int kSkinnyWaves = 16;
+constexpr int kSkinnyU = 2;  // k steps per wave per round of loads
+
+__global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(GemmArgs g, int tiles_n) {
+  constexpr int NWV = kSkinnyWaves;
+  constexpr int U = kSkinnyU;
+  const int nwg = gridDim.x;
+  int bid = blockIdx.x;
+  const int full = (nwg / 8) * 8;
+  if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
+  const int tn = bid % tiles_n;
+  const int b = bid / tiles_n;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int fr = lane & 15;  // A row / W column of the fragments
+  const int fk = lane >> 4;  // k group: k = 16*step + 4*fk + c
+  const int n0 = tn * 16;
+  const int M = g.M;
+  const void* Asrc = (g.A2 != nullptr && b >= g.a2_from) ? g.A2 : g.A;
+  const float* Ab = static_cast<const float*>(Asrc) +
+                    (int64_t)(g.a_period > 0 ? b % g.a_period : b) * g.a_bstride;
+  const float* Wb = static_cast<const float*>(g.W) + (int64_t)b * g.w_bstride;
+  const float* a_src = Ab + (int64_t)(fr < M ? fr : 0) * g.lda + 4 * fk;
+  const int wr = n0 + fr;
+  const float* w_src = Wb + (int64_t)(wr < g.N ? wr : 0) * g.ldw + 4 * fk;
+
+  // this wave's 16-deep k steps: wave, wave + NWV, ...
+  const int ksteps = g.K / 16;
+  const int nsteps = ksteps > wave ? (ksteps - wave + NWV - 1) / NWV : 0;
+
+  floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < nsteps; s0 += U) {
+    floatx4 av[U], wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int st = s0 + u < nsteps ? s0 + u : 0;
+      const int64_t k = (int64_t)(wave + NWV * st) * 16;
+      av[u] = *reinterpret_cast<const floatx4*>(a_src + k);
+      wv[u] = *reinterpret_cast<const floatx4*>(w_src + k);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (s0 + u < nsteps) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u].x, wv[u].x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u].y, wv[u].y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u].z, wv[u].z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u].w, wv[u].w, acc, 0, 0, 0);
+      }
+    }
+  }
+
+  // Waves 1.. hand their sums to wave 0, which adds them in wave order.
+  __shared__ floatx4 red[NWV - 1][64];
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int w = 0; w < NWV - 1; ++w) acc += red[w][lane];
+
+  // The fragment: lane holds rows 4*fk + e of column n0 + fr.
+  const int n = n0 + fr;
+  // The epilogue of gemm_kernel: residual reads first (the residual may be
+  // the output itself), then every value, then every store.
+  if (n >= g.N) return;
+  const GemmEpilogue& ep = g.ep;
+  const int64_t cb = (int64_t)b * g.c_bstride;
+  const float bias_v = ep.bias ? ep.bias[n + cb] : 0.0f;
+  float res[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = 4 * fk + e;
+    res[e] = (ep.residual && m < M) ? ep.residual[(int64_t)m * ep.ldr + n + cb] : 0.0f;
+  }
+  float outv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float v = acc[e] + bias_v;
+    if (ep.round_lp) v = round_lp(v, ep.lp_fmt);
+    if (ep.act == 1) v = fmaxf(v, 0.0f);
+    outv[e] = v + res[e];
+    if (ep.dt_a) outv[e] = softplus(outv[e]);
+  }
+  const int64_t nc = n + cb;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = 4 * fk + e;
+    if (m >= M) continue;
+    if (ep.out) ep.out[(int64_t)m * ep.ldo + nc] = outv[e];
+    if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + nc] = f32_to_lp_bits(outv[e], ep.lp_fmt);
+    if (ep.dt_decay) ep.dt_decay[(int64_t)m * ep.ldd + nc] = expf(ep.dt_a[n] * outv[e]);
+  }
+}
+
 // lgkmcnt(0) tying every register of r (in groups of 8 or 4) to the wait.
 template <int N>
 __device__ __forceinline__ void ds_wait_all(u32x4 (&r)[N]) {
@@ -994,6 +1106,17 @@ int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int 
   return HK_ERR_ARG;
 }
 
+// fp32 products of at most kSkinnyRows rows (any batch description).
+int gemm_skinny(const GemmArgs& g, hipStream_t stream) {
+  const int tiles_n = (g.N + 15) / 16;
+  const int64_t tiles = (int64_t)tiles_n * g.batch;
+  HK_REQUIRE(tiles < (1LL << 31), "gemm: grid too large");
+  hipLaunchKernelGGL(gemm_skinny_kernel, dim3((unsigned)tiles), dim3(64 * kSkinnyWaves), 0, stream,
+                     g, tiles_n);
+  HK_LAUNCH_CHECK();
+  return HK_OK;
+}
+
 }  // namespace
 
 bool packable(int N, int K) { return N > 0 && K > 0 && N % 32 == 0 && K % 64 == 0; }
@@ -1044,6 +1167,7 @@ int gemm(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int spl
              "gemm: leading dimensions must keep 16-byte alignment");
   if (g.M == 0) return HK_OK;
   if (g.w_packed) return gemm_wp(g, ws, stream, splits_hint);
+  if (g.type == GemmType::kF32 && g.M <= kSkinnyRows) return gemm_skinny(g, stream);
   const int tiles_m = (g.M + BM - 1) / BM;
   const int tiles_n = (g.N + BN - 1) / BN;
   const int64_t tiles = (int64_t)tiles_m * tiles_n * g.batch;

@@ -84,7 +84,8 @@ def test_conv1d_steps_in_sequence_without_bias(dev):
 @pytest.mark.parametrize("batch,blocks,bs,bias", [(39, 4, 512, False), (39, 4, 512, True),
                                                   (256, 8, 64, True), (6, 1024, 4, False),
                                                   (5, 3, 48, True), (7, 2, 20, True),
-                                                  (1, 4, 16, False)])
+                                                  (1, 4, 16, False), (16, 2, 256, True),
+                                                  (17, 2, 256, True), (3, 1, 1024, True)])
 def test_block_linear(dev, batch, blocks, bs, bias):
     from hackathon_amd import kernels as hk
 
