@@ -517,12 +517,26 @@ def bench_c5(args) -> int:
     return 0
 
 
-def xlstm_split_point(run_off):
+def xlstm_layer_weight_us(cfg, lowp=True):
+    """One xLSTM layer's weights read at 5 TB/s, in microseconds (16-bit
+    CastLinear weights when lowp, fp32 otherwise): the engine's charge for
+    the second weight read of a split."""
+    from hackathon_amd import spec
+
+    nbytes = 0
+    for p in spec.param_specs(cfg):
+        if p.name.startswith("towers.0.blocks.0."):
+            nbytes += int(np.prod(p.shape)) * (2 if lowp and spec.is_cast_linear(p.name) else 4)
+    return nbytes / 5.0e6
+
+
+def xlstm_split_point(run_off, weight_us=0.0):
     """The engine's split of a tick's length-sorted runs into two xLSTM run
     groups (engine.hip xlstm_split_point: 3 us per sLSTM step of a group's
-    longest run plus 5 us per symbol, split when the larger group costs
-    under 0.8 of the whole). Returns the first run of the second group
-    (len(runs) for no split)."""
+    longest run plus 5 us per symbol, a split charged one more read of a
+    layer's weights (weight_us), split when the larger group's cost plus
+    that read is under 0.8 of the whole). Returns the first run of the
+    second group (len(runs) for no split)."""
     n = len(run_off) - 1
     if n < 2:
         return n
@@ -530,7 +544,7 @@ def xlstm_split_point(run_off):
     whole = 3.0 * lens[0] + 5.0 * n
     best, best_k = whole, n
     for k in range(1, n):
-        c = max(3.0 * lens[0] + 5.0 * k, 3.0 * lens[k] + 5.0 * (n - k))
+        c = max(3.0 * lens[0] + 5.0 * k, 3.0 * lens[k] + 5.0 * (n - k)) + weight_us
         if c < best:
             best, best_k = c, k
     return best_k if best < 0.8 * whole else n
@@ -544,7 +558,7 @@ def tick_projections(cfg, run_off):
     H, P, I, D = cfg.hidden_size, cfg.proj_size, cfg.inner, cfg.tower_depth
     F = (cfg.num_features + 63) // 64 * 64
     n = int(run_off[-1])
-    k = xlstm_split_point(run_off)
+    k = xlstm_split_point(run_off, xlstm_layer_weight_us(cfg))
     groups = [int(run_off[k])] + ([n - int(run_off[k])] if k < len(run_off) - 1 else [])
     C = cfg.inner + 2 * cfg.mamba_bc_size
     per_layer = {"mamba2": [(C + I, H), (H, I)], "retnet": [(4 * H, H), (H, H)],
@@ -707,7 +721,7 @@ def bench_gemm(args) -> int:
         "data": "synthetic",
         "config": {"workload": "one C4 tick's bf16 projection GEMMs (1024 symbols, 256 Zipf(1.1) "
                                "requests), replayed alone, weights from HBM",
-                   "rows": int(run_off[-1]), "xlstm_groups_first_run": xlstm_split_point(run_off)},
+                   "rows": int(run_off[-1]), "xlstm_groups_first_run": xlstm_split_point(run_off, xlstm_layer_weight_us(cfg))},
         "roofline": {"bound": "hbm", "achieved": rf["achieved_GBs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": rf["hbm_frac"], "traffic": traffic,
                      "traffic_over_algorithmic": ratio,

@@ -59,3 +59,21 @@ def test_log_occupancy_is_bounded_on_zipf_ticks():
     # every symbol that ever had a request has an entry
     seen = set(int(s) for syms, _ in ticks for s in syms)
     assert set(occ) == seen
+
+
+def test_xlstm_split_point_hand_cases():
+    """The replica of the engine's xLSTM group split (bench.xlstm_split_point):
+    per group 3 us per sLSTM step of its longest run plus 5 us per symbol, a
+    split charged one more read of a layer's weights."""
+    one_each = lambda n: np.arange(n + 1)  # n runs of one request
+    # four one-request symbols: 3 + 20 = 23 unsplit; two and two cost 13
+    assert bench.xlstm_split_point(one_each(4)) == 2
+    # ... plus a second fp32 weight read (41 us): 54 > 0.8 * 23, no split
+    assert bench.xlstm_split_point(one_each(4), 40.5) == 4
+    # 64 one-request symbols: 323 unsplit, 163 + 24 split at 32 < 258.4
+    assert bench.xlstm_split_point(one_each(64), 23.7) == 32
+    # a 40-request run and 100 single ones: max(120 + 5k, 3 + 5(101 - k))
+    # is least at k = 39 (315 against 318 at k = 38 and 320 at k = 40)
+    run_off = np.concatenate([[0], np.cumsum([40] + [1] * 100)])
+    assert bench.xlstm_split_point(run_off, 23.7) == 39
+    assert bench.xlstm_split_point(np.array([0, 5])) == 1  # a single run
