@@ -572,6 +572,20 @@ def tick_projections(cfg, run_off):
     return out
 
 
+def tick_tile_rule(cfg, run_off):
+    """min_work_groups of each of tick_projections' GEMMs as the engine sets
+    it inside a tick: the shared rule (TICK_MIN_WORK_GROUPS) above 64 rows,
+    except for the xLSTM run groups' GEMMs, which keep the lone rule (0),
+    as every GEMM of at most 64 rows does."""
+    shapes = tick_projections(cfg, run_off)
+    n = int(run_off[-1])
+    k = xlstm_split_point(run_off, xlstm_layer_weight_us(cfg))
+    n_groups = 1 + (k < len(run_off) - 1)
+    n_xlstm = n_groups * (2 + cfg.tower_depth * 4)
+    return [0 if i < n_xlstm or m <= 64 else TICK_MIN_WORK_GROUPS
+            for i, (m, _, _) in enumerate(shapes)]
+
+
 def gemm_replay(torch, dev, shapes, reps=3, min_work_groups=0):
     """The given CastLinear GEMMs through hk_cast_linear_packed (bf16, the
     engine's projection kernel, weights packed by hk_pack_cast_weight as the
@@ -582,7 +596,9 @@ def gemm_replay(torch, dev, shapes, reps=3, min_work_groups=0):
     sequence (one HIP event pair per pass, so launch gaps are not added),
     per-launch durations from a pass with an event pair around every launch
     (these include each launch's dispatch latency), algorithmic bytes (W + A
-    in bf16, out in fp32, bias) and flops."""
+    in bf16, out in fp32, bias) and flops. min_work_groups: the tile rule's
+    minimum work-group count, one for every launch or one per shape (0: the
+    lone rule)."""
     from hackathon_amd import _lib
 
     lib = _lib.lib()
@@ -605,29 +621,32 @@ def gemm_replay(torch, dev, shapes, reps=3, min_work_groups=0):
         del w
     cur = torch.cuda.current_stream(dev)
 
-    def launch(m, n, k, w):
+    mwg = (list(min_work_groups) if hasattr(min_work_groups, "__len__")
+           else [min_work_groups] * len(shapes))
+
+    def launch(m, n, k, w, g):
         st = lib.hk_cast_linear_packed(x.data_ptr(), w.data_ptr(), bias.data_ptr(),
-                                       out.data_ptr(), m, n, k, 0, min_work_groups,
+                                       out.data_ptr(), m, n, k, 0, g,
                                        ws.data_ptr(), ws.numel(), stream)
         if st != 0:
             raise RuntimeError(lib.hk_last_error().decode())
 
-    for (m, n, k), w in zip(shapes, weights):  # warm-up pass
-        launch(m, n, k, w)
+    for (m, n, k), w, g in zip(shapes, weights, mwg):  # warm-up pass
+        launch(m, n, k, w, g)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(cur)
     for _ in range(reps):
-        for (m, n, k), w in zip(shapes, weights):
-            launch(m, n, k, w)
+        for (m, n, k), w, g in zip(shapes, weights, mwg):
+            launch(m, n, k, w, g)
     e1.record(cur)
     torch.cuda.synchronize()
     seq_avg_s = e0.elapsed_time(e1) * 1e-3 / (reps * len(shapes))
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in shapes]
-    for (m, n, k), w, (a, b) in zip(shapes, weights, ev):
+    for (m, n, k), w, g, (a, b) in zip(shapes, weights, mwg, ev):
         a.record(cur)
-        launch(m, n, k, w)
+        launch(m, n, k, w, g)
         b.record(cur)
     torch.cuda.synchronize()
     each = np.array([a.elapsed_time(b) * 1e-3 for a, b in ev])
@@ -1273,8 +1292,10 @@ def main() -> int:
     g_avg, _, g_bytes, g_flops = gemm_replay(torch, dev, shapes)
     grf = gemm_roofline(g_avg, g_bytes, g_flops)
     # The same launches under the tile rule the engine uses inside a tick
-    # (at least 112 work-groups: three other streams share the device).
-    t_avg, _, _, _ = gemm_replay(torch, dev, shapes, min_work_groups=TICK_MIN_WORK_GROUPS)
+    # (at least 112 work-groups above 64 rows, three other streams sharing
+    # the device; the xLSTM run groups' GEMMs keep the lone rule).
+    t_avg, _, _, _ = gemm_replay(torch, dev, shapes,
+                                 min_work_groups=tick_tile_rule(cfg, first.run_off))
     trf = gemm_roofline(t_avg, g_bytes, g_flops)
     v_avg = vendor_gemm_replay(torch, dev, shapes)
     vrf = gemm_roofline(v_avg, g_bytes, g_flops)
@@ -1364,7 +1385,9 @@ def main() -> int:
                        "gemm runs the same replay; profiles/ holds its rocprofv3 kernel-trace "
                        "and counter summaries); algorithmic bytes = bf16 W + bf16 A + fp32 out "
                        "+ bias"),
-            "tick_tile_rule": {"min_work_groups": TICK_MIN_WORK_GROUPS, "avg_us": trf["avg_us"],
+            "tick_tile_rule": {"min_work_groups": f"{TICK_MIN_WORK_GROUPS} above 64 rows, "
+                                                  "the lone rule for the xLSTM run groups",
+                               "avg_us": trf["avg_us"],
                                "achieved": trf["achieved_GBs"], "frac": trf["hbm_frac"],
                                "note": "the same replay with the tile rule the engine uses "
                                        "inside a tick (larger tiles: the tick is faster, the "

@@ -697,8 +697,12 @@ int linear(Engine& e, TowerWS& w, const Act& x, int64_t ldx, const Lin& lin, int
   // A tick's four streams share the device: above 64 rows the larger tiles
   // of the shared rule measure faster in the tick (C4: 9.21-9.24 against
   // 9.34-9.37 ms); at 64 rows (the B=64 latency tick) the lone rule's
-  // smaller tiles do (p50 5.09 against 5.17 ms).
-  g.min_tiles = M > 64 ? kMinTilesShared : kMinTilesAlone;
+  // smaller tiles do (p50 5.09 against 5.17 ms). The xLSTM run groups'
+  // GEMMs, on the tick's two critical chains, keep the lone rule's tiles at
+  // any row count (C4 8.60-8.62 against 8.64-8.66 ms, four alternating
+  // pairs; 200 or 256 work-groups for them: 8.67-8.74 ms).
+  const bool xlstm_group = &w == &e.ws[kXLSTM] || &w == &e.ws_x2;
+  g.min_tiles = M > 64 && !xlstm_group ? kMinTilesShared : kMinTilesAlone;
   g.M = M;
   g.N = N;
   g.K = K;
