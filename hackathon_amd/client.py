@@ -23,6 +23,7 @@ can be passed in and the response serialises the same way.
 
 from __future__ import annotations
 
+import array
 import os
 import time
 from dataclasses import dataclass, field
@@ -68,6 +69,25 @@ class InferenceResponse:
     predictions: list
     client_timestamp: float
     message_type: str = field(default="inference_response")
+
+
+def _feature_rows(requests, width: int) -> np.ndarray:
+    """[len(requests), width] float32 of the requests' feature lists. The
+    values go through one flat list and array.array (float32, round to
+    nearest, as numpy converts): 0.42 against 1.02 ms for 256 lists of 79
+    Python floats. Anything else (ragged rows, objects array.array does not
+    take) goes through numpy as before, which raises for what it cannot
+    convert, and process_arrays checks the shape."""
+    vals: list = []
+    ext = vals.extend
+    try:
+        for q in requests:
+            ext(q.features)
+        if len(vals) == len(requests) * width:
+            return np.frombuffer(array.array("f", vals), dtype=np.float32).reshape(len(requests), width)
+    except TypeError:
+        pass
+    return np.asarray([q.features for q in requests], dtype=np.float32)
 
 
 class NnInferenceClient:
@@ -149,7 +169,7 @@ class NnInferenceClient:
             flat.extend(reqs)
         if not flat:
             return InferenceResponse([], [], time.time())
-        feats = np.asarray([q.features for q in flat], dtype=np.float32)
+        feats = _feature_rows(flat, self.num_features)
         order, preds = self.process_arrays(symbols, counts, feats)
         return InferenceResponse([flat[j].unique_id for j in order], preds.tolist(), time.time())
 

@@ -112,3 +112,31 @@ def test_round_chunks_cover_rounds_within_max_rows():
             assert sorted(seen) == sorted(want) and len(seen) == len(want)
             starts = [k0 for k0, _, _ in chunks]
             assert starts == sorted(starts)
+
+
+def test_feature_rows_matches_numpy():
+    """process_batch's feature conversion (flat list through array.array)
+    against numpy's on every form a request's features may take; ragged or
+    non-numeric rows still raise as numpy does."""
+    from hackathon_amd.client import _feature_rows
+
+    rng = np.random.default_rng(5)
+    rows = [rng.standard_normal(6).tolist() for _ in range(5)]
+    forms = [
+        rows,                                               # lists of Python floats
+        [tuple(r) for r in rows],                           # tuples
+        [np.asarray(r, dtype=np.float64) for r in rows],    # float64 arrays
+        [np.asarray(r, dtype=np.float32) for r in rows],    # float32 arrays
+        [[int(10 * v) for v in r] for r in rows],           # ints
+        [[1e-45, 3.4e38, -0.0, float("inf"), float("nan"), 1.0 + 2 ** -30]] * 2,  # rounding edges
+    ]
+    for f in forms:
+        reqs = [PendingRequest(i, "S", r) for i, r in enumerate(f)]
+        got = _feature_rows(reqs, 6)
+        want = np.asarray([q.features for q in reqs], dtype=np.float32)
+        assert got.dtype == np.float32 and got.shape == want.shape
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(ValueError):
+        _feature_rows([PendingRequest(0, "S", [1.0, 2.0]), PendingRequest(1, "S", [1.0])], 2)
+    with pytest.raises(ValueError):
+        _feature_rows([PendingRequest(0, "S", ["a", "b"])], 2)
