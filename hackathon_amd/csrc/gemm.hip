@@ -505,11 +505,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, float* partial, i
 // never stored). Two steps per round; a round past a wave's last step loads
 // its first step again and skips the products, so every load is unconditional.
 // The waves' sums meet in LDS and are added in wave order (deterministic).
-// (Measured alone, M = 4, W streamed from HBM, microseconds per launch:
-// 8192x2048 17.3, 2048x4096 14.9, 4096x2048 9.7, 8448x2048 22.6, 2048x2048
-// 8.9, 64x2048 8.2; with K split to fill the device as gemm_kernel does,
-// 22.8, 20.7, 17.4, 27.1, 18.8, 14.7: the split's round trips cost more than
-// its parallelism gains.)
+// (Measured alone, M = 4, W streamed from HBM, microseconds per launch, this
+// kernel / gemm_kernel: 8192x2048 17.3 / 28.9, 2048x4096 14.9 / 20.5,
+// 4096x2048 9.7 / 18.6, 8448x2048 22.6 / 42.2, 2048x2048 8.9 / 15.5, 64x2048
+// 8.2 / 13.5. A form with 64-column work-groups and gemm_kernel's split K
+// ran 22.8, 20.7, 17.4, 27.1, 18.8 and 14.7: the split's round trips cost
+// more than its parallelism gains.)
 constexpr int kSkinnyRows = 16;
 constexpr int kSkinnyWaves = 16;
 constexpr int kSkinnyU = 2;  // k steps per wave per round of loads
