@@ -1,9 +1,11 @@
-// Projection GEMM kernels (see gemm.h). Two kernels:
+// Projection GEMM kernels (see gemm.h). Three kernels:
 // - gemm_wp_kernel, for the engine's 16-bit CastLinear projections, whose
 //   weights are stored packed in MFMA fragment order (described at the
 //   kernel);
 // - gemm_kernel, below, for fp32 products (the fp32 mode's linears and the
-//   BlockLinear batches) and 16-bit weights in row-major layout.
+//   BlockLinear batches) and 16-bit weights in row-major layout;
+// - gemm_skinny_kernel, for fp32 products of at most 16 rows (described at
+//   the kernel).
 //
 // gemm_kernel: 64x64 output tile per 256-thread work-group, 4 wave64s in a 2x2 layout,
 // each wave owning a 32x32 sub-tile = 2x2 MFMA 16x16 fragments. K advances in
