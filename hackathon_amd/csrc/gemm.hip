@@ -608,6 +608,104 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(GemmArgs
   }
 }
 
+// The 16-bit CastLinear projection of at most 16 rows on packed weights:
+// gemm_skinny_kernel's scheme on v_mfma_f32_16x16x32_bf16 / _f16. A
+// work-group of 16 waves owns one 16-column MFMA fragment of a packed
+// 32-column block and all of K; each 32-deep k step is one 1 KB contiguous W
+// fragment and one A fragment (16 rows x 64 bytes; rows past M read row 0),
+// taken in interleaved steps by the waves, two per round, loads
+// unconditional (a round past a wave's last step reloads its first). The
+// waves' sums meet in LDS in wave order; wave 0 applies gemm_wp_kernel's
+// epilogue (bias, rounding to the operand format, relu, residual, fp32 and
+// 16-bit stores).
+template <GemmType T>
+__global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_wp_kernel(GemmArgs g,
+                                                                           int tiles_n) {
+  constexpr int NWV = kSkinnyWaves;
+  constexpr int U = kSkinnyU;
+  constexpr int FMT = T == GemmType::kF16 ? kLpF16 : kLpBF16;
+  typedef uint16_t E;
+  const int nwg = gridDim.x;
+  int bid = blockIdx.x;
+  const int full = (nwg / 8) * 8;
+  if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
+  const int tn = bid % tiles_n;  // 16-column fragment: block tn / 2, half tn % 2
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int fr = lane & 15;
+  const int fq = lane >> 4;
+  const int M = g.M;
+  const int kb32 = g.K / 32;
+  const E* a_src = static_cast<const E*>(g.A) + (int64_t)(fr < M ? fr : 0) * g.lda + 8 * fq;
+  // fragment (block, kb, half) starts at ((block * kb32 + kb) * 2 + half) * 512
+  const E* w_src = static_cast<const E*>(g.W) +
+                   (((int64_t)(tn >> 1) * kb32) * 2 + (tn & 1)) * 512 + 8 * lane;
+  const int nsteps = kb32 > wave ? (kb32 - wave + NWV - 1) / NWV : 0;
+
+  floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < nsteps; s0 += U) {
+    u32x4 av[U], wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int st = s0 + u < nsteps ? s0 + u : 0;
+      const int kb = wave + NWV * st;
+      av[u] = *reinterpret_cast<const u32x4*>(a_src + (int64_t)kb * 32);
+      wv[u] = *reinterpret_cast<const u32x4*>(w_src + (int64_t)kb * 1024);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (s0 + u < nsteps) {
+        if constexpr (T == GemmType::kBF16)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[u]),
+                                                        __builtin_bit_cast(bf16x8, wv[u]), acc, 0,
+                                                        0, 0);
+        else
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8, av[u]),
+                                                       __builtin_bit_cast(halfx8, wv[u]), acc, 0,
+                                                       0, 0);
+      }
+    }
+  }
+
+  __shared__ floatx4 red[NWV - 1][64];
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int w = 0; w < NWV - 1; ++w) acc += red[w][lane];
+
+  // lane holds rows 4*fq + e of column n (N is a multiple of 32: every
+  // column exists)
+  const int n = tn * 16 + fr;
+  const GemmEpilogue& ep = g.ep;
+  const float bias_v = ep.bias ? ep.bias[n] : 0.0f;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = acc[e] + bias_v;
+    if (ep.round_lp) v[e] = round_lp_t<FMT>(v[e]);
+    if (ep.act == 1) v[e] = fmaxf(v[e], 0.0f);
+  }
+  if (ep.residual) {
+    float res[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 4 * fq + e;
+      res[e] = m < M ? ep.residual[(int64_t)m * ep.ldr + n] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += res[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = 4 * fq + e;
+    if (m >= M) continue;
+    if (ep.out) ep.out[(int64_t)m * ep.ldo + n] = v[e];
+    if (ep.out_lp) ep.out_lp[(int64_t)m * ep.ldl + n] = f32_to_lp_bits_t<FMT>(v[e]);
+  }
+}
+
 // lgkmcnt(0) tying every register of r (in groups of 8 or 4) to the wait.
 template <int N>
 __device__ __forceinline__ void ds_wait_all(u32x4 (&r)[N]) {
@@ -1031,6 +1129,17 @@ int gemm_wp(const GemmArgs& g, const GemmWorkspace& ws, hipStream_t stream, int 
   const int fmt = g.type == GemmType::kF16 ? kLpF16 : kLpBF16;
   HK_REQUIRE(!(g.ep.round_lp || g.ep.out_lp) || g.ep.lp_fmt == fmt,
              "gemm: the packed kernel rounds to its operand format");
+  if (g.M <= kSkinnyRows) {
+    const int tiles_n = g.N / 16;
+    if (g.type == GemmType::kF16)
+      hipLaunchKernelGGL((gemm_skinny_wp_kernel<GemmType::kF16>), dim3((unsigned)tiles_n),
+                         dim3(64 * kSkinnyWaves), 0, stream, g, tiles_n);
+    else
+      hipLaunchKernelGGL((gemm_skinny_wp_kernel<GemmType::kBF16>), dim3((unsigned)tiles_n),
+                         dim3(64 * kSkinnyWaves), 0, stream, g, tiles_n);
+    HK_LAUNCH_CHECK();
+    return HK_OK;
+  }
   // Tile: the largest of 64x128, 64x64, 32x64, 32x32 (rows x columns) that
   // still gives at least min_tiles work-groups without splitting K; failing
   // that the smallest, with K split to fill the device. Measured on the

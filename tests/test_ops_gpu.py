@@ -275,13 +275,15 @@ def test_cast_linear_matches_castlinear(dev, dtype, M, N, K):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,N,K", [(256, 8192, 2048), (256, 4096, 2048), (256, 2048, 2048),
                                    (179, 8448, 2048), (77, 2048, 4096), (37, 2048, 4096),
-                                   (5, 8448, 2048), (1, 64, 64), (100, 320, 640), (300, 1024, 192)])
+                                   (5, 8448, 2048), (1, 64, 64), (100, 320, 640), (300, 1024, 192),
+                                   (16, 2048, 4096), (12, 320, 640), (17, 2048, 2048)])
 def test_cast_linear_packed_matches_castlinear(dev, dtype, M, N, K):
     """The engine's projection kernel (hk_cast_linear_packed, the weight
     rearranged by hk_pack_cast_weight) against CastLinear's expression at the
     bar of test_cast_linear_matches_castlinear. The shapes cover every tile
     of the kernel (64x128, 64x64, 32x64, 32x32; rows past M, split K when the
-    tiles cannot fill the device) and the tick's projections, under the tile
+    tiles cannot fill the device; at most 16 rows, the one-fragment form
+    that takes all of K per work-group) and the tick's projections, under the tile
     rule of a lone GEMM, of the engine's ticks (112 work-groups) and one no
     shape meets (always the smallest tile, K split); the packed result also
     equals the row-major kernel's within the same bound."""
