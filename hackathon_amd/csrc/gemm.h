@@ -10,8 +10,9 @@
 //        GemmArgs::split_wscale set, the same fp32 operands multiply on f16
 //        matrix cores as value plus remainder (v_mfma_f32_16x16x32_f16).
 // fp32 products of at most 16 rows (any batch description, every epilogue;
-// split_wscale is not used there: exact fp32) run on a kernel of their own
-// that streams W through registers without splitting K.
+// split_wscale is not used there: exact fp32), and packed 16-bit
+// projections of at most 16 rows, run on kernels of their own that stream W
+// through registers without splitting K.
 #pragma once
 
 #include "common.h"

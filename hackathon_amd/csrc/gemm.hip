@@ -1,11 +1,11 @@
-// Projection GEMM kernels (see gemm.h). Three kernels:
+// Projection GEMM kernels (see gemm.h). Four kernels:
 // - gemm_wp_kernel, for the engine's 16-bit CastLinear projections, whose
 //   weights are stored packed in MFMA fragment order (described at the
 //   kernel);
 // - gemm_kernel, below, for fp32 products (the fp32 mode's linears and the
 //   BlockLinear batches) and 16-bit weights in row-major layout;
-// - gemm_skinny_kernel, for fp32 products of at most 16 rows (described at
-//   the kernel).
+// - gemm_skinny_kernel and gemm_skinny_wp_kernel, for fp32 products and
+//   packed 16-bit projections of at most 16 rows (described at the kernels).
 //
 // gemm_kernel: 64x64 output tile per 256-thread work-group, 4 wave64s in a 2x2 layout,
 // each wave owning a 32x32 sub-tile = 2x2 MFMA 16x16 fragments. K advances in
