@@ -62,12 +62,19 @@ __device__ __forceinline__ float gelu_erf(float x) {
 }
 
 // Round-to-nearest-even fp32 -> bf16 bits (no NaN inputs on this path, but a
-// NaN stays a NaN: the quiet bit is forced). Written as selects, not early
-// returns, so a wave converts without branching.
+// NaN stays a NaN: the quiet bit is forced). The device converts with the
+// hardware instruction (v_cvt_pk_bf16_f32 on gfx950): the kernels' float mode
+// is round-to-nearest-even with subnormals kept, so it rounds every non-NaN
+// input as the integer form below, which the host uses. That form is written
+// as selects, not early returns.
 __host__ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   const uint32_t u = __builtin_bit_cast(uint32_t, f);
   const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
   return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : r);
+#endif
 }
 
 __host__ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
@@ -85,8 +92,14 @@ __host__ __device__ __forceinline__ float round_bf16(float f) {
 // the fp32 adder round |f| to a multiple of 2^-24; the low bits of the sum
 // are that multiple. Every case is computed and the result selected (no
 // branches): NaN -> quiet NaN, |f| >= 65520 (rounds past 65504) or infinity
-// -> infinity, |f| >= 2^-14 -> normal, else subnormal or zero.
+// -> infinity, |f| >= 2^-14 -> normal, else subnormal or zero. The device
+// uses the hardware conversion (v_cvt_f16_f32), which rounds every non-NaN
+// input the same way under the kernels' float mode (round-to-nearest-even,
+// fp16 subnormals kept).
 __host__ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+#else
   const uint32_t u = __builtin_bit_cast(uint32_t, f);
   const uint32_t sign = (u >> 16) & 0x8000u;
   const uint32_t a = u & 0x7fffffffu;
@@ -98,9 +111,14 @@ __host__ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   v = a >= 0x477ff000u ? 0x7c00u : v;
   v = a > 0x7f800000u ? 0x7e00u : v;
   return (uint16_t)(sign | v);
+#endif
 }
 
+// fp16 bits -> fp32 (exact: every fp16 value is an fp32 value).
 __host__ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return (float)__builtin_bit_cast(_Float16, h);
+#else
   const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
   const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
   // zero / subnormal: m * 2^-24, exact in fp32; infinity / NaN; normal
@@ -108,6 +126,7 @@ __host__ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   uint32_t v = e == 31u ? 0x7f800000u | (m << 13) : ((e + 112u) << 23) | (m << 13);
   v = e == 0u ? sub : v;
   return __builtin_bit_cast(float, sign | v);
+#endif
 }
 
 // The 16-bit compute formats of CastLinear (example_model.py:150-155).

@@ -1,7 +1,9 @@
-"""The library's fp32 -> 16-bit conversions (hk_to_lp_host; the kernels use
-the same routine) against torch's casts, which CastLinear applies to its
-weights, biases, inputs and outputs (example_model.py:82-95): round to
-nearest even, fp16 overflow to infinity, subnormals, signed zeros, NaN."""
+"""The library's fp32 -> 16-bit conversions against torch's casts, which
+CastLinear applies to its weights, biases, inputs and outputs
+(example_model.py:82-95): round to nearest even, fp16 overflow to infinity,
+subnormals, signed zeros, NaN. The host routine (hk_to_lp_host, the integer
+form) on the CPU; the kernels' hardware conversion on the GPU, through the
+projection GEMMs' rounding of their outputs."""
 
 import numpy as np
 import pytest
@@ -38,3 +40,46 @@ def test_to_lp_matches_torch_cast(fmt):
     # NaN stays NaN
     nan_in = torch.tensor([float("nan")])
     assert torch.isnan(weights.to_lp_bits(nan_in, fmt).view(FMT[fmt]).float()).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["bf16", "fp16"])
+def test_device_rounding_matches_torch_cast(dev, fmt):
+    """The GEMM epilogue's rounding to the format (fp32 -> 16-bit -> fp32 on
+    the device, the conversion every kernel uses for its 16-bit stores) bit
+    for bit against torch's cast, on every non-NaN value of _values(): with
+    x = 0 and W = 0 the output of CastLinear's GEMM is round(0 + bias), so
+    the fp32 bias carries the values in. Both entry points and both kernel
+    forms of the packed one (1 row: the one-fragment kernel; 32 rows: the
+    tiled kernel). The bias is b + 0.0 (-0.0 becomes +0.0). The row-major
+    kernel adds its (zero) residual after the rounding, so a negative value
+    that rounds to zero comes out +0.0 there: it is compared with zeros
+    unsigned, the packed kernel bit for bit."""
+    from hackathon_amd import _lib, kernels as hk
+
+    v = torch.from_numpy(_values())
+    v = v[~torch.isnan(v)]
+    n = v.numel() // 32 * 32
+    b = (v[:n] + 0.0).contiguous()
+    want = b.to(FMT[fmt]).to(torch.float32)
+    K = 64
+    wl = torch.zeros(n, K, dtype=FMT[fmt], device=dev)
+    packed = hk.pack_cast_weight(wl)
+    bd = b.to(dev)
+    lib = _lib.lib()
+    for M in (1, 32):
+        x = torch.zeros(M, K, dtype=FMT[fmt], device=dev)
+        for name, w in (("hk_cast_linear_packed", packed), ("hk_cast_linear", wl)):
+            out = torch.full((M, n), float("nan"), device=dev)
+            stream = _lib.current_stream(dev)
+            if name == "hk_cast_linear_packed":
+                st = lib.hk_cast_linear_packed(x.data_ptr(), w.data_ptr(), bd.data_ptr(), out.data_ptr(),
+                                               M, n, K, weights.LP_FORMATS[fmt], 0, None, 0, stream)
+            else:
+                st = lib.hk_cast_linear(x.data_ptr(), w.data_ptr(), bd.data_ptr(), out.data_ptr(),
+                                        M, n, K, weights.LP_FORMATS[fmt], None, 0, stream)
+            _lib.check(st, name)
+            got = out.cpu()
+            ref = want if name == "hk_cast_linear_packed" else want + 0.0
+            for r in range(M):
+                assert torch.equal(got[r].view(torch.int32), ref.view(torch.int32)), (name, M, r)
