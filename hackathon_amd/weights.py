@@ -47,8 +47,9 @@ def generate(cfg: ModelConfig, seed: int = 0) -> dict[str, torch.Tensor]:
 
 def to_lp_bits(x: torch.Tensor, fmt: str) -> torch.Tensor:
     """16-bit patterns (int16 tensor) of fp32 values in CastLinear format
-    `fmt` ("bf16" / "fp16"), by the library's conversion (hk_to_lp_host),
-    the one its kernels apply to weights, biases and activations."""
+    `fmt` ("bf16" / "fp16"), by the library's host conversion
+    (hk_to_lp_host), which rounds every non-NaN value as its kernels'
+    device conversion does for weights, biases and activations."""
     x = x.detach().to(torch.float32).contiguous().cpu()
     out = torch.empty(x.shape, dtype=torch.int16)
     _lib.check(_lib.lib().hk_to_lp_host(x.data_ptr(), out.data_ptr(), x.numel(), LP_FORMATS[fmt]),

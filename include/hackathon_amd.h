@@ -174,7 +174,8 @@ int hk_fill_uniform_host(float* dst, int64_t n, uint64_t key, float lo, float hi
  * 1 fp16), round to nearest even, fp16 overflowing to infinity: torch's
  * .to(torch.bfloat16) / .to(torch.float16), which CastLinear applies to its
  * weights, biases, inputs and outputs (example_model.py:82-95). The engine's
- * kernels use the same conversion. Host memory, no GPU. */
+ * kernels round the same way (the device's conversion instructions, every
+ * non-NaN input alike). Host memory, no GPU. */
 int hk_to_lp_host(const float* src, uint16_t* dst, int64_t n, int fmt);
 
 /* ---------------------------------------------------------------------------
