@@ -82,8 +82,11 @@ def _feature_rows(requests, width: int) -> np.ndarray:
     ext = vals.extend
     try:
         for q in requests:
-            ext(q.features)
-        if len(vals) == len(requests) * width:
+            f = q.features
+            if len(f) != width:
+                break
+            ext(f)
+        else:
             return np.frombuffer(array.array("f", vals), dtype=np.float32).reshape(len(requests), width)
     except TypeError:
         pass

@@ -138,5 +138,8 @@ def test_feature_rows_matches_numpy():
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     with pytest.raises(ValueError):
         _feature_rows([PendingRequest(0, "S", [1.0, 2.0]), PendingRequest(1, "S", [1.0])], 2)
+    # ragged rows whose lengths add up to the full count are still ragged
+    with pytest.raises(ValueError):
+        _feature_rows([PendingRequest(0, "S", [1.0, 2.0, 3.0]), PendingRequest(1, "S", [1.0])], 2)
     with pytest.raises(ValueError):
         _feature_rows([PendingRequest(0, "S", ["a", "b"])], 2)
