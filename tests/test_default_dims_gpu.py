@@ -361,7 +361,7 @@ def test_c4_bf16_1000_ticks_sampled_symbols(dev, params):
     pd = {k: v.to(dev) for k, v in params.items()}
     p32, _ = reference_rounds(om.Params(pd), cfg, histories, device=dev)
     torch.cuda.empty_cache()
-    plp, _ = reference_rounds(om.Params(pd, lp=lp), cfg, histories, device=dev)
+    plp, _ = reference_rounds(om.Params(pd, lp="bf16"), cfg, histories, device=dev)
     del pd
     torch.cuda.empty_cache()
     cat = lambda v: np.concatenate([np.asarray(a) for a in v])
